@@ -1,0 +1,191 @@
+"""Benchmark of the MI355X Gated DeltaNet operators (one JSON line on stdout).
+
+Headline workload (BASELINE.json configs[1] at its quoted point): one decode
+step at B=64 -- state [64, 8, 128, 128] f32 read and written once.  A "step"
+is one call of the decode DPS entry point.  Inputs are synthetic (numpy
+default_rng, the configs[1] recipe) and resident in HBM before timing starts.
+The state pairs rotate over 8 distinct (state, new_state) buffers (512 MiB,
+twice the 256 MB Infinity Cache) so no step reads a state that is still cached.
+
+Reported beside it: decode kernel time and achieved HBM bandwidth (the
+roofline of the dominant kernel, from HIP events around each launch on the
+launch stream), the prefill at 1x8192 (ms and tokens/s), and the CPU baseline
+(the reference's loop nest restated in numpy, oracle/gdn_oracle.py:decode_loop,
+single thread, on a bounded sample).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep]
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "gated-delta-network_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "decode µs/step + HBM GB/s at B=64; prefill tokens/s + ms at 1×8192"
+HBM_PEAK_GBPS = 8000.0
+# Published B200 decode latency at B=64 (reference README.md:49): 0.023 ms/step.
+B200_DECODE_MS_B64 = 0.023
+ROTATE = 8
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _dev_inputs(inp, dev):
+    import numpy as np
+    import torch
+    d = {}
+    for name in ("q", "k", "v", "a", "b"):
+        d[name] = torch.from_numpy(np.ascontiguousarray(inp[name])).to(dev).to(torch.bfloat16)
+    for name in ("A_log", "dt_bias"):
+        d[name] = torch.from_numpy(inp[name]).to(dev)
+    d["state"] = None if inp["state"] is None else torch.from_numpy(inp["state"]).to(dev)
+    return d
+
+
+def bench_decode(B, steps, warmup, dev, variant=-1):
+    """Returns (ms per step over `steps` back-to-back calls, mean kernel ms)."""
+    import torch
+    from gdn_amd import decode
+    from oracle import gdn_oracle as O  # input recipe only
+
+    inp = O.make_decode_inputs(B, seed=1)
+    d = _dev_inputs(inp, dev)
+    states = [d["state"].clone() for _ in range(ROTATE)]
+    new_states = [torch.empty_like(d["state"]) for _ in range(ROTATE)]
+    out = torch.empty((B, 1, 8, 128), dtype=torch.bfloat16, device=dev)
+    args = (d["q"], d["k"], d["v"])
+    tail = (d["A_log"], d["a"], d["dt_bias"], d["b"], inp["scale"], out)
+
+    def step(i):
+        decode.kernel(*args, states[i % ROTATE], *tail, new_states[i % ROTATE], variant=variant)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    # Pass 1: wall time of back-to-back steps.
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        step(i)
+    t1.record()
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / steps
+    # Pass 2: each launch bracketed by events on its stream (kernel duration).
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for i in range(steps):
+        evs[i][0].record()
+        step(i)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    durs = sorted(a.elapsed_time(b) for a, b in evs)
+    ms_kernel = sum(durs) / len(durs)
+    return ms_step, ms_kernel, durs[len(durs) // 2]
+
+
+def cpu_baseline_decode(B, seconds):
+    """The reference's decode loop nest restated in numpy (oracle decode_loop),
+    one thread, repeated until `seconds` of CPU time have passed."""
+    from threadpoolctl import threadpool_limits
+    from oracle import gdn_oracle as O
+
+    inp = O.make_decode_inputs(B, seed=1)
+    reps = 0
+    with threadpool_limits(limits=1):
+        t = time.perf_counter()
+        while True:
+            O.decode_loop(**inp)
+            reps += 1
+            el = time.perf_counter() - t
+            if el >= seconds:
+                break
+    return el / reps, reps
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--variant", type=int, default=-1, help="decode tiling (-1 = built-in)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="also time every decode batch size of configs[1] and every tiling")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the operators "
+              "are per-GPU shards with no cross-GPU exchange; see DESIGN.md for how they "
+              "would shard).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from oracle import gdn_oracle as O
+
+    dev = torch.device("cuda", 0)
+    log(f"device: {torch.cuda.get_device_name(dev)}")
+    B = args.batch
+
+    if args.sweep:
+        for b in (1, 2, 4, 8, 16, 32, 48, 64):
+            for var in [-1] + list(range(10)) + [16 + i for i in range(10)]:
+                ms, mk, med = bench_decode(b, args.steps, args.warmup, dev, var)
+                gbs = O.decode_bytes(b) / (mk * 1e-3) / 1e9
+                log(f"sweep decode B={b:3d} variant={var:3d}: {ms * 1e3:8.2f} us/step, "
+                    f"kernel {mk * 1e3:8.2f} us (median {med * 1e3:8.2f}), {gbs:8.1f} GB/s")
+
+    ms_step, ms_kernel, ms_kernel_med = bench_decode(B, args.steps, args.warmup, dev,
+                                                    args.variant)
+    nbytes = O.decode_bytes(B)
+    gbs_step = nbytes / (ms_step * 1e-3) / 1e9
+    gbs_kernel = nbytes / (ms_kernel * 1e-3) / 1e9
+    log(f"decode B={B}: {ms_step * 1e3:.2f} us/step, kernel {ms_kernel * 1e3:.2f} us "
+        f"({gbs_kernel:.1f} GB/s, {gbs_kernel / HBM_PEAK_GBPS:.1%} of peak)")
+
+    cpu_s, reps = cpu_baseline_decode(B, args.cpu_seconds)
+    cpu_gbs = nbytes / cpu_s / 1e9
+    log(f"cpu baseline decode B={B}: {cpu_s * 1e3:.1f} ms/step over {reps} steps")
+
+    b200_gbs = O.decode_bytes(64) / (B200_DECODE_MS_B64 * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(gbs_step, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(gbs_step / b200_gbs, 4) if B == 64 else None,
+        "dtype": "f32",
+        "data": "synthetic: numpy default_rng(seed=1), configs[1] recipe; 8 rotating state buffers",
+        "config": {"workload": f"decode step, B={B} (configs[1]), k-last f32 state",
+                   "batch": B, "heads_qk": 4, "heads_v": 8, "head_dim": 128},
+        "decode_us_per_step": round(ms_step * 1e3, 3),
+        "decode_kernel_us": round(ms_kernel * 1e3, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs_kernel, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbs_kernel / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "kernel": "gdn::decode_kernel",
+                     "bytes_per_launch": nbytes},
+        "cpu_baseline": {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+                         "sample": f"{reps} decode steps at B={B} "
+                                   f"({cpu_s * 1e3:.1f} ms/step), oracle decode_loop, 1 thread"},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,244 @@
+// Gated DeltaNet decode (T = 1): one fused, HBM-bound pass over the state.
+//
+// Semantics: reference/gdn_decode_ref.py:12-83.  Per (batch row n, v-head h):
+//   decay = exp(-exp(A_log[h]) * softplus(a + dt_bias[h])),  beta = sigmoid(b)
+//   for every V-row r of the k-last state S[n,h] ([V=128, K=128] f32):
+//     pred  = decay * <S[r,:], k>          v_new = beta * (v[r] - pred)
+//     S'[r] = decay * S[r,:] + v_new * k   o[r]  = scale * <S'[r,:], q>
+// where q, k are q/k head h/2 (GVA without copies).  <S'[r], q> is evaluated
+// as decay*<S[r],q> + v_new*<k,q>, so both row reductions run together.
+//
+// Work mapping (gfx950, wave64): a row of 128 floats is held by one aligned
+// group of 16 lanes, 8 floats per lane as two 16-byte loads at columns 4c and
+// 64+4c (c = lane % 16), so each wave-wide load instruction reads 4 x 256
+// contiguous bytes.  The row sums use 4 DPP adds inside the 16-lane group.  A
+// workgroup of WAVES waves covers 4*WAVES rows per pass and PASSES passes;
+// every pass's loads are issued before any arithmetic, so one workgroup keeps
+// 4*WAVES*PASSES*512 bytes of state in flight.  Each lane needs only its 8
+// columns of q and k, loaded once.
+#include "gdn_device.h"
+#include "gdn_host.h"
+
+namespace gdn {
+
+template <int WAVES, int PASSES, bool HAS_STATE, bool NONTEMPORAL>
+__global__ __launch_bounds__(64 * WAVES) void decode_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
+    const uint16_t *__restrict__ v, const float *state, const float *__restrict__ A_log,
+    const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
+    const uint16_t *__restrict__ b, float scale, uint16_t *__restrict__ out, float *new_state) {
+  constexpr int kRowsPerPass = 4 * WAVES;
+  constexpr int kRows = kRowsPerPass * PASSES;
+  constexpr int kTiles = kDV / kRows;
+  static_assert(kDV % kRows == 0, "row tile must divide 128");
+
+  const int tile = blockIdx.x % kTiles;
+  const int nh = blockIdx.x / kTiles;  // n * 8 + h
+  const int h = nh % kHV;
+  const int n = nh / kHV;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane & 15;
+  const int row0 = tile * kRows + wave * 4 + (lane >> 4);
+
+  // Gating (reference/gdn_decode_ref.py:42-44), in every lane: a few
+  // transcendental ops, cheaper than a broadcast.
+  const float decay =
+      expf(gdn_log_decay(A_log[h], bf16_to_f32(a[nh]), dt_bias[h]));
+  const float beta = sigmoidf_(bf16_to_f32(b[nh]));
+
+  // This lane's 8 columns of q and k (q/k head h/2).
+  const int qk_off = (n * kHQK + h / 2) * kDK;
+  const u16x4 qa = *reinterpret_cast<const u16x4 *>(q + qk_off + 4 * c);
+  const u16x4 qb = *reinterpret_cast<const u16x4 *>(q + qk_off + 64 + 4 * c);
+  const u16x4 ka = *reinterpret_cast<const u16x4 *>(k + qk_off + 4 * c);
+  const u16x4 kb = *reinterpret_cast<const u16x4 *>(k + qk_off + 64 + 4 * c);
+  float qf[8], kf[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    qf[i] = bf16_to_f32(qa[i]);
+    qf[4 + i] = bf16_to_f32(qb[i]);
+    kf[i] = bf16_to_f32(ka[i]);
+    kf[4 + i] = bf16_to_f32(kb[i]);
+  }
+
+  // Issue every load of this workgroup's rows first.
+  f32x4 s[PASSES][2];
+  float vr[PASSES];
+  const size_t head_base = static_cast<size_t>(nh) * kDV * kDK;
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int row = row0 + p * kRowsPerPass;
+    const size_t base = head_base + static_cast<size_t>(row) * kDK;
+    if constexpr (HAS_STATE) {
+      const f32x4 *src0 = reinterpret_cast<const f32x4 *>(state + base + 4 * c);
+      const f32x4 *src1 = reinterpret_cast<const f32x4 *>(state + base + 64 + 4 * c);
+      if constexpr (NONTEMPORAL) {
+        s[p][0] = __builtin_nontemporal_load(src0);
+        s[p][1] = __builtin_nontemporal_load(src1);
+      } else {
+        s[p][0] = *src0;
+        s[p][1] = *src1;
+      }
+    } else {
+      s[p][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      s[p][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    vr[p] = bf16_to_f32(v[nh * kDV + row]);
+  }
+
+  float kq = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) kq = fmaf(kf[i], qf[i], kq);
+  kq = row16_sum(kq);
+
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int row = row0 + p * kRowsPerPass;
+    float sv[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sv[i] = s[p][0][i];
+      sv[4 + i] = s[p][1][i];
+    }
+    float sk = 0.f, sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      sk = fmaf(sv[i], kf[i], sk);
+      sq = fmaf(sv[i], qf[i], sq);
+    }
+    sk = row16_sum(sk);
+    sq = row16_sum(sq);
+    const float v_new = beta * (vr[p] - decay * sk);
+    const float o = scale * fmaf(decay, sq, v_new * kq);
+    f32x4 n0, n1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      n0[i] = fmaf(decay, sv[i], v_new * kf[i]);
+      n1[i] = fmaf(decay, sv[4 + i], v_new * kf[4 + i]);
+    }
+    const size_t base = head_base + static_cast<size_t>(row) * kDK;
+    f32x4 *dst0 = reinterpret_cast<f32x4 *>(new_state + base + 4 * c);
+    f32x4 *dst1 = reinterpret_cast<f32x4 *>(new_state + base + 64 + 4 * c);
+    if constexpr (NONTEMPORAL) {
+      __builtin_nontemporal_store(n0, dst0);
+      __builtin_nontemporal_store(n1, dst1);
+    } else {
+      *dst0 = n0;
+      *dst1 = n1;
+    }
+    if (c == 0) out[nh * kDV + row] = f32_to_bf16(o);
+  }
+}
+
+namespace {
+
+typedef void (*decode_fn)(const uint16_t *, const uint16_t *, const uint16_t *, const float *,
+                          const float *, const uint16_t *, const float *, const uint16_t *,
+                          float, uint16_t *, float *);
+
+struct DecodeVariant {
+  int waves, passes;
+  decode_fn with_state[2];  // [nontemporal]
+  decode_fn no_state[2];
+};
+
+#define GDN_DECODE_VARIANT(W, P)                                                     \
+  {                                                                                  \
+    W, P, {decode_kernel<W, P, true, false>, decode_kernel<W, P, true, true>}, {     \
+      decode_kernel<W, P, false, false>, decode_kernel<W, P, false, true>            \
+    }                                                                                \
+  }
+
+// Tilings: rows per workgroup = 4 * waves * passes.
+const DecodeVariant kVariants[] = {
+    GDN_DECODE_VARIANT(4, 8),  // 0: 128 rows, 256 threads
+    GDN_DECODE_VARIANT(4, 4),  // 1:  64 rows, 256 threads
+    GDN_DECODE_VARIANT(4, 2),  // 2:  32 rows, 256 threads
+    GDN_DECODE_VARIANT(4, 1),  // 3:  16 rows, 256 threads
+    GDN_DECODE_VARIANT(2, 4),  // 4:  32 rows, 128 threads
+    GDN_DECODE_VARIANT(1, 8),  // 5:  32 rows,  64 threads
+    GDN_DECODE_VARIANT(1, 4),  // 6:  16 rows,  64 threads
+    GDN_DECODE_VARIANT(1, 2),  // 7:   8 rows,  64 threads
+    GDN_DECODE_VARIANT(2, 8),  // 8:  64 rows, 128 threads
+    GDN_DECODE_VARIANT(1, 16), // 9:  64 rows,  64 threads
+};
+constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
+constexpr int kNontemporalFlag = 16;
+
+// Built-in tiling per batch size (measured on MI355X; see the decode sweep).
+int default_variant(int batch) {
+  if (batch <= 4) return 7;
+  if (batch <= 16) return 6;
+  return 2;
+}
+
+}  // namespace
+
+static int decode_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                         const float *state, const float *A_log, const gdn_bf16 *a,
+                         const float *dt_bias, const gdn_bf16 *b, float scale, gdn_bf16 *output,
+                         float *new_state, int batch, void *stream, int variant) {
+  clear_error();
+  if (batch < 0) return fail(GDN_ERR_INVALID, "gdn_decode_fwd: batch=%d < 0", batch);
+  if (!q || !k || !v || !A_log || !a || !dt_bias || !b || !output || !new_state)
+    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: null pointer argument");
+  if (!(scale > 0.0f) || scale == __builtin_inff())
+    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: scale must be finite and > 0");
+  if (!aligned(new_state, 16) || (state && !aligned(state, 16)))
+    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: state/new_state must be 16-byte aligned");
+  if (!aligned(q, 8) || !aligned(k, 8))
+    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: q/k must be 8-byte aligned");
+  if (batch == 0) return GDN_OK;
+  const size_t nb = static_cast<size_t>(batch);
+  const size_t state_bytes = nb * kHV * kDV * kDK * sizeof(float);
+  const size_t out_bytes = nb * kHV * kDV * sizeof(uint16_t);
+  // new_state may be exactly state (in-place); no other overlap is allowed.
+  if (state != new_state && overlaps(state, state_bytes, new_state, state_bytes))
+    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: new_state partially overlaps state");
+  const void *ins[] = {q, k, v, a, b, A_log, dt_bias, state};
+  const size_t in_bytes[] = {nb * kHQK * kDK * 2, nb * kHQK * kDK * 2, nb * kHV * kDV * 2,
+                             nb * kHV * 2,        nb * kHV * 2,        kHV * 4,
+                             kHV * 4,             state ? state_bytes : 0};
+  for (int i = 0; i < 8; ++i) {
+    if (overlaps(output, out_bytes, ins[i], in_bytes[i]))
+      return fail(GDN_ERR_INVALID, "gdn_decode_fwd: output overlaps an input");
+    if (i < 7 && overlaps(new_state, state_bytes, ins[i], in_bytes[i]))
+      return fail(GDN_ERR_INVALID, "gdn_decode_fwd: new_state overlaps an input");
+  }
+  if (overlaps(output, out_bytes, new_state, state_bytes))
+    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: output overlaps new_state");
+
+  if (variant < 0) variant = default_variant(batch);
+  const int nt = (variant & kNontemporalFlag) ? 1 : 0;
+  const int vi = variant & (kNontemporalFlag - 1);
+  if (vi >= kNumVariants) return fail(GDN_ERR_INVALID, "gdn_decode_fwd: unknown variant %d", variant);
+  const DecodeVariant &cfg = kVariants[vi];
+  const int rows = 4 * cfg.waves * cfg.passes;
+  const long long blocks = static_cast<long long>(batch) * kHV * (kDV / rows);
+  if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_decode_fwd: batch too large");
+  decode_fn fn = state ? cfg.with_state[nt] : cfg.no_state[nt];
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(64 * cfg.waves), 0,
+                     static_cast<hipStream_t>(stream), q, k, v, state, A_log, a, dt_bias, b,
+                     scale, output, new_state);
+  return check_launch("gdn_decode_fwd");
+}
+
+}  // namespace gdn
+
+extern "C" int gdn_decode_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                              const float *state, const float *A_log, const gdn_bf16 *a,
+                              const float *dt_bias, const gdn_bf16 *b, float scale,
+                              gdn_bf16 *output, float *new_state, int batch, void *stream) {
+  return gdn::decode_launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
+                            stream, -1);
+}
+
+extern "C" int gdn_decode_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                                      const float *state, const float *A_log, const gdn_bf16 *a,
+                                      const float *dt_bias, const gdn_bf16 *b, float scale,
+                                      gdn_bf16 *output, float *new_state, int batch, void *stream,
+                                      int variant) {
+  return gdn::decode_launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
+                            stream, variant);
+}

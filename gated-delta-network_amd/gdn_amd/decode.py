@@ -1,0 +1,76 @@
+"""Decode entry point: the reference's destination-passing ``kernel(...)``.
+
+Same name, argument order and meaning as
+solutions/gdn_decode_qk4_v8_d128_k_last/solution/triton/kernel.py:85 and
+solution/cuda/binding.py:195, with the semantics of
+reference/gdn_decode_ref.py:12-83 (state may be None; scale None/0.0 means
+1/sqrt(128)).  The work is one launch of the HIP kernel behind
+``gdn_decode_fwd`` (include/gdn_amd.h) on torch's current stream.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._common import DK, DV, H_QK, HV, check_output, check_tensor, dense, resolve_scale, stream_of
+
+
+def _validate(q, k, v, state, A_log, a, dt_bias, b, output, new_state):
+    if not isinstance(q, torch.Tensor) or q.dim() != 4:
+        raise ValueError("q must be a [B, 1, 4, 128] tensor")
+    B = q.shape[0]
+    dev = q.device
+    if dev.type != "cuda":
+        raise ValueError(f"q is on {dev}; the HIP kernels need device tensors")
+    bf, f32 = torch.bfloat16, torch.float32
+    check_tensor("q", q, (B, 1, H_QK, DK), bf, dev)
+    check_tensor("k", k, (B, 1, H_QK, DK), bf, dev)
+    check_tensor("v", v, (B, 1, HV, DV), bf, dev)
+    if state is not None:
+        check_tensor("state", state, (B, HV, DV, DK), f32, dev)
+    check_tensor("A_log", A_log, (HV,), f32, dev)
+    check_tensor("a", a, (B, 1, HV), bf, dev)
+    check_tensor("dt_bias", dt_bias, (HV,), f32, dev)
+    check_tensor("b", b, (B, 1, HV), bf, dev)
+    check_tensor("output", output, (B, 1, HV, DV), bf, dev)
+    check_tensor("new_state", new_state, (B, HV, DV, DK), f32, dev)
+    check_output("output", output)
+    check_output("new_state", new_state)
+    return B, dev
+
+
+def kernel(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, *, variant=-1):
+    """One GDN decode step (T=1), written into ``output`` and ``new_state``.
+
+    q, k [B,1,4,128] bf16; v [B,1,8,128] bf16; state [B,8,128,128] f32 k-last
+    or None; A_log, dt_bias [8] f32; a, b [B,1,8] bf16; scale float, 0-d
+    tensor or None; output [B,1,8,128] bf16; new_state [B,8,128,128] f32.
+    ``new_state`` may be ``state`` itself (in-place update).  ``variant``
+    picks a tiling (gdn_decode_fwd_variant); the default is the built-in one.
+    """
+    lib = _lib.load()
+    B, dev = _validate(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
+    scale = resolve_scale(scale)
+    if state is not None and state.data_ptr() != new_state.data_ptr():
+        state = dense(state)
+    q, k, v, a, b, A_log, dt_bias = (dense(t) for t in (q, k, v, a, b, A_log, dt_bias))
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            None if state is None else state.data_ptr(), A_log.data_ptr(), a.data_ptr(),
+            dt_bias.data_ptr(), b.data_ptr(), scale, output.data_ptr(), new_state.data_ptr(),
+            B, stream_of(dev))
+    if variant == -1:
+        rc = lib.gdn_decode_fwd(*args)
+    else:
+        rc = lib.gdn_decode_fwd_variant(*args, int(variant))
+    _lib.check(rc, "gdn_decode_fwd")
+
+
+def run(q, k, v, state, A_log, a, dt_bias, b, scale):
+    """Non-DPS form with the reference's return convention
+    (reference/gdn_decode_ref.py:12, returns (output, new_state))."""
+    B = q.shape[0]
+    output = torch.empty((B, 1, HV, DV), dtype=torch.bfloat16, device=q.device)
+    new_state = torch.empty((B, HV, DV, DK), dtype=torch.float32, device=q.device)
+    kernel(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state)
+    return output, new_state

@@ -1,0 +1,111 @@
+"""Prefill entry point: the reference's destination-passing ``kernel(...)``.
+
+Same name, argument order and meaning as
+solutions/gdn_prefill_qk4_v8_d128_k_last/solution/triton/fla_kernels.py:1049,
+with the semantics of reference/gdn_prefill_ref.py:12-91 (state may be None;
+scale None/0.0 means 1/sqrt(128); a zero-length sequence yields a zero
+state).  The work is the HIP pipeline behind ``gdn_prefill_fwd``
+(include/gdn_amd.h) on torch's current stream.  cu_seqlens is never copied to
+the host: the chunk table is built on the device, and the workspace is sized
+from (T, N) alone.
+
+Workspace: device memory from torch's caching allocator, kept per (device,
+stream) and grown on demand, replacing the reference's module-level buffer
+cache (fla_kernels.py:950-957), which was keyed by name only.
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+from ._common import DK, DV, H_QK, HV, check_output, check_tensor, dense, resolve_scale, stream_of
+
+_ws_lock = threading.Lock()
+_workspaces: dict = {}
+
+
+def workspace_bytes(total_tokens: int, num_seqs: int) -> int:
+    return int(_lib.load().gdn_prefill_workspace_bytes(int(total_tokens), int(num_seqs)))
+
+
+def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """A byte buffer of at least nbytes, reused by later calls on the same
+    stream (work on one stream is ordered, so reuse needs no sync)."""
+    key = (dev.index, stream)
+    with _ws_lock:
+        buf = _workspaces.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+            _workspaces[key] = buf
+        return buf
+
+
+def _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state):
+    if not isinstance(q, torch.Tensor) or q.dim() != 3:
+        raise ValueError("q must be a [T, 4, 128] tensor")
+    T = q.shape[0]
+    dev = q.device
+    if dev.type != "cuda":
+        raise ValueError(f"q is on {dev}; the HIP kernels need device tensors")
+    if not isinstance(cu_seqlens, torch.Tensor) or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 1:
+        raise ValueError("cu_seqlens must be a 1-D tensor of N+1 offsets")
+    if cu_seqlens.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"cu_seqlens must be int32 or int64, got {cu_seqlens.dtype}")
+    if cu_seqlens.device != dev:
+        raise ValueError(f"cu_seqlens is on {cu_seqlens.device}, expected {dev}")
+    N = cu_seqlens.numel() - 1
+    bf, f32 = torch.bfloat16, torch.float32
+    check_tensor("q", q, (T, H_QK, DK), bf, dev)
+    check_tensor("k", k, (T, H_QK, DK), bf, dev)
+    check_tensor("v", v, (T, HV, DV), bf, dev)
+    if state is not None:
+        check_tensor("state", state, (N, HV, DV, DK), f32, dev)
+    check_tensor("A_log", A_log, (HV,), f32, dev)
+    check_tensor("a", a, (T, HV), bf, dev)
+    check_tensor("dt_bias", dt_bias, (HV,), f32, dev)
+    check_tensor("b", b, (T, HV), bf, dev)
+    check_tensor("output", output, (T, HV, DV), bf, dev)
+    check_tensor("new_state", new_state, (N, HV, DV, DK), f32, dev)
+    check_output("output", output)
+    check_output("new_state", new_state)
+    return T, N, dev
+
+
+def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state):
+    """Chunked GDN prefill over a packed batch, written into ``output`` and
+    ``new_state``.
+
+    q, k [T,4,128] bf16; v [T,8,128] bf16; state [N,8,128,128] f32 k-last or
+    None; A_log, dt_bias [8] f32; a, b [T,8] bf16; cu_seqlens [N+1] int32/int64
+    on the device (0 = cu[0] <= ... <= cu[N] = T); scale float, 0-d tensor or
+    None; output [T,8,128] bf16; new_state [N,8,128,128] f32 (may be state).
+    """
+    lib = _lib.load()
+    T, N, dev = _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state)
+    scale = resolve_scale(scale)
+    if state is not None and state.data_ptr() != new_state.data_ptr():
+        state = dense(state)
+    q, k, v, a, b, A_log, dt_bias, cu_seqlens = (
+        dense(t) for t in (q, k, v, a, b, A_log, dt_bias, cu_seqlens))
+    stream = stream_of(dev)
+    nbytes = int(lib.gdn_prefill_workspace_bytes(T, N))
+    ws = _workspace(dev, stream, nbytes)
+    rc = lib.gdn_prefill_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), None if state is None else state.data_ptr(),
+        A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr(), cu_seqlens.data_ptr(),
+        1 if cu_seqlens.dtype == torch.int64 else 0, N, T, scale, output.data_ptr(),
+        new_state.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    _lib.check(rc, "gdn_prefill_fwd")
+
+
+def run(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale):
+    """Non-DPS form with the reference's return convention
+    (reference/gdn_prefill_ref.py:12, returns (output, new_state))."""
+    T, N = q.shape[0], cu_seqlens.numel() - 1
+    output = torch.empty((T, HV, DV), dtype=torch.bfloat16, device=q.device)
+    new_state = torch.empty((N, HV, DV, DK), dtype=torch.float32, device=q.device)
+    kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state)
+    return output, new_state

@@ -1,0 +1,120 @@
+/*
+ * gdn_amd.h -- C ABI of the MI355X (gfx950) Gated DeltaNet operators.
+ *
+ * Shapes are fixed by the operator definitions gdn_decode_qk4_v8_d128_k_last
+ * and gdn_prefill_qk4_v8_d128_k_last: 4 q/k heads, 8 v-heads (head hv reads
+ * q/k head hv/2), head size 128, recurrent state in k-last layout
+ * [*, 8, 128 (V), 128 (K)] float32.  All tensors are dense, row-major and
+ * live in device memory of the current HIP device.  bf16 tensors are passed
+ * as their 16-bit patterns (gdn_bf16).  Nothing here allocates device memory
+ * or synchronises the host; every launch goes to the given HIP stream
+ * (NULL = the legacy default stream).
+ *
+ * Return value: GDN_OK (0) or a negative GDN_ERR_* code; gdn_last_error()
+ * then describes the failure (thread-local, valid until the next call from
+ * the same thread).
+ */
+#ifndef GDN_AMD_H
+#define GDN_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t gdn_bf16;
+
+#define GDN_OK 0
+#define GDN_ERR_INVALID (-1)   /* bad pointer, size, alignment or aliasing */
+#define GDN_ERR_LAUNCH (-2)    /* the HIP runtime refused a launch */
+#define GDN_ERR_WORKSPACE (-3) /* workspace missing or smaller than required */
+
+/* ABI version of this header; bumped on any signature change. */
+int gdn_abi_version(void);
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char *gdn_last_error(void);
+
+/*
+ * One decode step (T = 1) for a batch of B sequences.
+ *
+ * Replaces the launch behind the reference's decode entry point
+ * kernel(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state):
+ *   solutions/gdn_decode_qk4_v8_d128_k_last/solution/triton/kernel.py:85-113
+ *   and its CUDA twin gdn_decode_cuda(), solution/cuda/binding.py:127-168.
+ * Semantics: reference/gdn_decode_ref.py:12-83.
+ *
+ *   q, k      [B, 1, 4, 128] bf16      v         [B, 1, 8, 128] bf16
+ *   state     [B, 8, 128, 128] f32 or NULL (treated as zeros)
+ *   A_log     [8] f32                  a, b      [B, 1, 8] bf16
+ *   dt_bias   [8] f32                  scale     > 0, already resolved
+ *   output    [B, 1, 8, 128] bf16      new_state [B, 8, 128, 128] f32
+ *
+ * new_state may be the same buffer as state (in-place update); any other
+ * overlap between an output and an input is rejected.  state/new_state must
+ * be 16-byte aligned, q/k 8-byte aligned.
+ */
+int gdn_decode_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v, const float *state,
+                   const float *A_log, const gdn_bf16 *a, const float *dt_bias,
+                   const gdn_bf16 *b, float scale, gdn_bf16 *output, float *new_state,
+                   int batch, void *stream);
+
+/*
+ * gdn_decode_fwd with an explicit tiling, the counterpart of the block_v
+ * argument of the reference's gdn_decode_cuda (solutions/
+ * gdn_decode_qk4_v8_d128_k_last/solution/cuda/binding.py:127-131,206-211).
+ * variant = tiling index (0..9, rows per workgroup 128/64/32/16/32/32/16/8/64/64
+ * with 256/256/256/256/128/64/64/64/128/64 threads) + 16 for non-temporal state
+ * loads/stores; -1 = the built-in choice for the batch size (what
+ * gdn_decode_fwd uses).  Results are identical for every variant.
+ */
+int gdn_decode_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                           const float *state, const float *A_log, const gdn_bf16 *a,
+                           const float *dt_bias, const gdn_bf16 *b, float scale,
+                           gdn_bf16 *output, float *new_state, int batch, void *stream,
+                           int variant);
+
+/*
+ * Bytes of device workspace gdn_prefill_fwd needs for a packed batch of
+ * total_tokens tokens in num_seqs sequences.  The bound does not depend on the
+ * individual lengths (they stay on the device), so a caller can size it once.
+ * Replaces the module-level buffer cache of the reference prefill,
+ * solutions/gdn_prefill_qk4_v8_d128_k_last/solution/triton/fla_kernels.py:950-957.
+ */
+size_t gdn_prefill_workspace_bytes(int total_tokens, int num_seqs);
+
+/*
+ * Chunked prefill over a packed batch of variable-length sequences.
+ *
+ * Replaces the six launches behind the reference's prefill entry point
+ * kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+ * new_state): solutions/gdn_prefill_qk4_v8_d128_k_last/solution/triton/
+ * fla_kernels.py:975-1053.  Semantics: reference/gdn_prefill_ref.py:12-91.
+ *
+ *   q, k       [T, 4, 128] bf16         v          [T, 8, 128] bf16
+ *   state      [N, 8, 128, 128] f32 or NULL (treated as zeros)
+ *   A_log      [8] f32                  a, b       [T, 8] bf16
+ *   dt_bias    [8] f32                  cu_seqlens [N + 1] int32 or int64
+ *   scale      > 0, already resolved    output     [T, 8, 128] bf16
+ *   new_state  [N, 8, 128, 128] f32     workspace  >= gdn_prefill_workspace_bytes(T, N)
+ *
+ * cu_seqlens stays on the device and is never read by the host: it must start
+ * at 0, be non-decreasing and end at T (a violating batch leaves the outputs
+ * unspecified but never accesses memory out of bounds).  A zero-length
+ * sequence gets an all-zero new_state, as the reference does.  new_state may
+ * alias state; output must not overlap any input.
+ */
+int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                    const float *state, const float *A_log, const gdn_bf16 *a,
+                    const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
+                    int cu_seqlens_is_int64, int num_seqs, int total_tokens, float scale,
+                    gdn_bf16 *output, float *new_state, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_AMD_H */

@@ -1,0 +1,87 @@
+"""The C-ABI library: it loads, exports every symbol include/gdn_amd.h
+declares, and rejects bad arguments before touching the GPU (no device
+needed; nothing here launches a kernel)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from gdn_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                      "include", "gdn_amd.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gdn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared_functions()
+    for want in ("gdn_decode_fwd", "gdn_prefill_fwd", "gdn_prefill_workspace_bytes",
+                 "gdn_last_error", "gdn_abi_version"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"{name} declared in gdn_amd.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes prototype"
+
+
+def test_abi_version_and_load():
+    lib = _lib.load()
+    assert lib.gdn_abi_version() == _lib.ABI_VERSION
+
+
+def _decode_args(**over):
+    args = dict(q=1 << 20, k=2 << 20, v=3 << 20, state=None, A_log=4 << 20, a=5 << 20,
+                dt_bias=6 << 20, b=7 << 20, scale=0.1, output=8 << 20, new_state=16 << 20,
+                batch=1, stream=None)
+    args.update(over)
+    return list(args.values())
+
+
+@pytest.mark.parametrize("over, needle", [
+    (dict(q=None), "null"),
+    (dict(output=None), "null"),
+    (dict(batch=-1), "batch"),
+    (dict(scale=0.0), "scale"),
+    (dict(scale=float("nan")), "scale"),
+    (dict(scale=float("inf")), "scale"),
+    (dict(new_state=(16 << 20) + 4), "aligned"),
+    (dict(q=(1 << 20) + 2), "aligned"),
+    (dict(output=(3 << 20) + 256), "overlap"),
+    (dict(state=(16 << 20) + 1024), "overlap"),
+])
+def test_decode_rejects_bad_arguments(over, needle):
+    lib = _lib.load()
+    rc = lib.gdn_decode_fwd(*_decode_args(**over))
+    assert rc == _lib.GDN_ERR_INVALID
+    assert needle in _lib.last_error()
+
+
+def test_decode_zero_batch_is_a_no_op():
+    lib = _lib.load()
+    assert lib.gdn_decode_fwd(*_decode_args(batch=0)) == _lib.GDN_OK
+
+
+def test_decode_unknown_variant():
+    lib = _lib.load()
+    rc = lib.gdn_decode_fwd_variant(*_decode_args(), 15)
+    assert rc == _lib.GDN_ERR_INVALID and "variant" in _lib.last_error()
+
+
+def test_check_maps_status_to_exceptions():
+    _lib.check(_lib.GDN_OK, "x")
+    with pytest.raises(ValueError):
+        _lib.check(_lib.GDN_ERR_INVALID, "x")
+    with pytest.raises(_lib.GdnWorkspaceError):
+        _lib.check(_lib.GDN_ERR_WORKSPACE, "x")
+    with pytest.raises(_lib.GdnError):
+        _lib.check(_lib.GDN_ERR_LAUNCH, "x")

@@ -1,0 +1,224 @@
+"""Decode parity on the GPU: the HIP kernel (through the C ABI, via the DPS
+entry point) against the CPU oracle on the same seeded inputs.
+
+Tolerance (stated once in conftest.py): bf16 output atol = rtol = 1e-2; f32
+state atol = 1e-3 * max|state_ref|.  Decode is f32 end to end, so its state
+is also held to a tighter 1e-5 * max|state_ref| regression bound.
+"""
+
+import importlib.util
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import PKG, assert_output_close, assert_state_close
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SOLUTION = os.path.join(PKG, "solutions", "gdn_decode_qk4_v8_d128_k_last", "solution", "hip",
+                        "kernel.py")
+
+
+def _entry():
+    spec = importlib.util.spec_from_file_location("gdn_decode_solution", SOLUTION)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.kernel
+
+
+kernel = _entry()
+
+
+def to_dev(inp, dev):
+    bf = torch.bfloat16
+    out = {}
+    for name in ("q", "k", "v", "a", "b"):
+        out[name] = torch.from_numpy(np.ascontiguousarray(inp[name])).to(dev).to(bf)
+    for name in ("A_log", "dt_bias"):
+        out[name] = torch.from_numpy(inp[name]).to(dev)
+    out["state"] = None if inp["state"] is None else torch.from_numpy(inp["state"]).to(dev)
+    out["scale"] = inp["scale"]
+    return out
+
+
+def run_gpu(d, B, dev, variant=-1, in_place=False):
+    output = torch.empty((B, 1, 8, 128), dtype=torch.bfloat16, device=dev)
+    if in_place:
+        new_state = d["state"]
+    else:
+        new_state = torch.empty((B, 8, 128, 128), dtype=torch.float32, device=dev)
+    kernel(d["q"], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"], d["b"],
+           d["scale"], output, new_state, variant=variant)
+    torch.cuda.synchronize()
+    return output.float().cpu().numpy(), new_state.cpu().numpy()
+
+
+def check(o, s, o_ref, s_ref):
+    assert_output_close(o, o_ref)
+    assert_state_close(s, s_ref)
+    assert_state_close(s, s_ref, rel_atol=1e-5, what="state (f32 regression bound)")
+
+
+@pytest.mark.parametrize("B", [1, 2, 4, 8, 16, 32, 48, 64])
+def test_decode_parity_batch_sweep(cuda_device, B):
+    print(f"decode parity B={B} seed=1", flush=True)
+    inp = O.make_decode_inputs(B, seed=1)
+    o_ref, s_ref = O.decode(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), B, cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+def test_decode_config0_single(cuda_device):
+    inp = O.make_decode_inputs(1, seed=0)
+    o_ref, s_ref = O.decode_loop(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), 1, cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+def test_decode_large_batch(cuda_device):
+    B = 512  # the reference's largest test batch (tests/test_decode.py:171)
+    inp = O.make_decode_inputs(B, seed=7)
+    o_ref, s_ref = O.decode(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), B, cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+@pytest.mark.parametrize("variant", list(range(10)) + [16 + i for i in range(10)])
+def test_decode_every_tiling_is_identical(cuda_device, variant):
+    B = 6
+    inp = O.make_decode_inputs(B, seed=8)
+    d = to_dev(inp, cuda_device)
+    o0, s0 = run_gpu(d, B, cuda_device)
+    o, s = run_gpu(d, B, cuda_device, variant=variant)
+    assert np.array_equal(o, o0) and np.array_equal(s, s0)
+    o_ref, s_ref = O.decode(**inp)
+    check(o, s, o_ref, s_ref)
+
+
+def test_decode_state_none_is_zero_state(cuda_device):
+    B = 3
+    inp = O.make_decode_inputs(B, seed=9, with_state=False)
+    d = to_dev(inp, cuda_device)
+    o, s = run_gpu(d, B, cuda_device)
+    o_ref, s_ref = O.decode(**inp)
+    check(o, s, o_ref, s_ref)
+    d["state"] = torch.zeros((B, 8, 128, 128), dtype=torch.float32, device=cuda_device)
+    o2, s2 = run_gpu(d, B, cuda_device)
+    assert np.array_equal(o, o2) and np.array_equal(s, s2)
+
+
+def test_decode_in_place_update(cuda_device):
+    B = 5
+    inp = O.make_decode_inputs(B, seed=10)
+    d = to_dev(inp, cuda_device)
+    o1, s1 = run_gpu(d, B, cuda_device)
+    o2, s2 = run_gpu(d, B, cuda_device, in_place=True)
+    assert np.array_equal(o1, o2) and np.array_equal(s1, s2)
+    assert np.array_equal(d["state"].cpu().numpy(), s1)
+
+
+def test_decode_scale_forms(cuda_device):
+    B = 2
+    inp = O.make_decode_inputs(B, seed=11)
+    d = to_dev(inp, cuda_device)
+    o_default, _ = run_gpu(dict(d, scale=None), B, cuda_device)
+    o_zero, _ = run_gpu(dict(d, scale=0.0), B, cuda_device)
+    o_explicit, _ = run_gpu(dict(d, scale=1 / math.sqrt(128)), B, cuda_device)
+    o_tensor, _ = run_gpu(dict(d, scale=torch.tensor(1 / math.sqrt(128))), B, cuda_device)
+    assert np.array_equal(o_default, o_zero)
+    assert np.array_equal(o_default, o_explicit)
+    assert np.array_equal(o_default, o_tensor)
+    o_ref, _ = O.decode(**dict(inp, scale=2.0))
+    o2, _ = run_gpu(dict(d, scale=2.0), B, cuda_device)
+    assert_output_close(o2, o_ref)
+
+
+def test_decode_reference_test_distribution(cuda_device):
+    # The reference's own test recipe (tests/test_decode.py:82-96): q, k, v ~
+    # 0.1 N(0,1) (not normalised), state 0.01 N(0,1), A_log, dt_bias, a ~ 0.1
+    # N(0,1), b ~ N(0,1), scale 1.0.
+    rng = np.random.default_rng(42)
+    B = 16
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    inp = dict(q=O.bf16_round(0.1 * f(B, 1, 4, 128)), k=O.bf16_round(0.1 * f(B, 1, 4, 128)),
+               v=O.bf16_round(0.1 * f(B, 1, 8, 128)), state=0.01 * f(B, 8, 128, 128),
+               A_log=0.1 * f(8), a=O.bf16_round(0.1 * f(B, 1, 8)), dt_bias=0.1 * f(8),
+               b=O.bf16_round(f(B, 1, 8)), scale=1.0)
+    o_ref, s_ref = O.decode(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), B, cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+def test_decode_extreme_gates(cuda_device):
+    # softplus threshold (x > 20), beta saturating at 0 and 1, decay ~ 0 and 1
+    B = 4
+    inp = O.make_decode_inputs(B, seed=12)
+    inp["a"][:, 0, :] = O.bf16_round(np.array([30.0, -30.0, 20.0, 0.0, 19.5, -5.0, 5.0, 1.0],
+                                              np.float32))
+    inp["b"][:, 0, :] = O.bf16_round(np.array([-40.0, 40.0, 0.0, 8.0, -8.0, 1.0, -1.0, 0.0],
+                                              np.float32))
+    inp["A_log"][:] = np.array([-10.0, 2.7, 0.0, -20.0, 1.0, 0.5, 0.1, 2.0], np.float32)
+    o_ref, s_ref = O.decode(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), B, cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+def test_decode_strided_inputs(cuda_device):
+    B = 3
+    inp = O.make_decode_inputs(B, seed=13)
+    d = to_dev(inp, cuda_device)
+    big = torch.zeros((B, 1, 8, 128), dtype=torch.bfloat16, device=cuda_device)
+    big[:, :, ::2] = d["q"]
+    d2 = dict(d, q=big[:, :, ::2])
+    assert not d2["q"].is_contiguous()
+    o1, s1 = run_gpu(d, B, cuda_device)
+    o2, s2 = run_gpu(d2, B, cuda_device)
+    assert np.array_equal(o1, o2) and np.array_equal(s1, s2)
+
+
+def test_decode_rejects_bad_outputs(cuda_device):
+    B = 2
+    d = to_dev(O.make_decode_inputs(B, seed=14), cuda_device)
+    out = torch.empty((B, 1, 8, 128), dtype=torch.bfloat16, device=cuda_device)
+    ns = torch.empty((B, 8, 128, 256), dtype=torch.float32, device=cuda_device)[..., ::2]
+    with pytest.raises(ValueError, match="contiguous"):
+        kernel(d["q"], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"], d["b"],
+               d["scale"], out, ns)
+    with pytest.raises(ValueError, match="dtype|float32"):
+        kernel(d["q"], d["k"], d["v"], d["state"].double(), d["A_log"], d["a"], d["dt_bias"],
+               d["b"], d["scale"], out, ns.contiguous())
+
+
+def test_decode_chained_steps_match_prefill_oracle(cuda_device):
+    # 24 decode steps carrying the state == the sequential prefill oracle.
+    L = 24
+    p = O.make_prefill_inputs([L], seed=15)
+    o_ref, s_ref = O.prefill_seq(**p)
+    dev = cuda_device
+    state = torch.from_numpy(p["state"]).to(dev)
+    outs = []
+    for t in range(L):
+        step = dict(q=p["q"][t][None, None], k=p["k"][t][None, None], v=p["v"][t][None, None],
+                    a=p["a"][t][None, None], b=p["b"][t][None, None], A_log=p["A_log"],
+                    dt_bias=p["dt_bias"], state=None, scale=p["scale"])
+        d = to_dev(step, dev)
+        out = torch.empty((1, 1, 8, 128), dtype=torch.bfloat16, device=dev)
+        kernel(d["q"], d["k"], d["v"], state, d["A_log"], d["a"], d["dt_bias"], d["b"],
+               d["scale"], out, state)
+        outs.append(out)
+    torch.cuda.synchronize()
+    o = torch.cat(outs).float().cpu().numpy()[:, 0]
+    assert_output_close(o, o_ref)
+    assert_state_close(state.cpu().numpy(), s_ref)
+
+
+def test_decode_deterministic(cuda_device):
+    B = 8
+    d = to_dev(O.make_decode_inputs(B, seed=16), cuda_device)
+    runs = [run_gpu(d, B, cuda_device) for _ in range(3)]
+    for o, s in runs[1:]:
+        assert np.array_equal(o, runs[0][0]) and np.array_equal(s, runs[0][1])
