@@ -52,5 +52,26 @@ def check_output(name: str, t: torch.Tensor) -> None:
         raise ValueError(f"{name} must be contiguous: it is written in place")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> int:
+    """Handle of torch's current stream on `device` (a hipStream_t on ROCm)."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else 0)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def fast_ok(tensors, dtypes, shapes) -> bool:
+    """Cheap all-in-one check run before the detailed, message-producing one:
+    every tensor on one CUDA device, with the given dtype and shape, and
+    dense.  False means "run the detailed validation"."""
+    Tensor = torch.Tensor
+    dev = tensors[0].get_device() if isinstance(tensors[0], Tensor) else -1
+    if dev < 0:
+        return False
+    for t, dt, sh in zip(tensors, dtypes, shapes):
+        if (not isinstance(t, Tensor) or t.dtype is not dt or t.shape != sh
+                or t.get_device() != dev or not t.is_contiguous()):
+            return False
+    return True

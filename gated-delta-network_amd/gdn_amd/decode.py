@@ -13,7 +13,12 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from ._common import DK, DV, H_QK, HV, check_output, check_tensor, dense, resolve_scale, stream_of
+from ._common import (DK, DV, H_QK, HV, check_output, check_tensor, dense, fast_ok,
+                      resolve_scale, stream_of)
+
+_BF = torch.bfloat16
+_F32 = torch.float32
+_DTYPES = (_BF, _BF, _BF, _F32, _BF, _F32, _BF, _BF, _F32)
 
 
 def _validate(q, k, v, state, A_log, a, dt_bias, b, output, new_state):
@@ -50,11 +55,19 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, *, va
     picks a tiling (gdn_decode_fwd_variant); the default is the built-in one.
     """
     lib = _lib.load()
-    B, dev = _validate(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
+    B = q.shape[0] if isinstance(q, torch.Tensor) and q.dim() == 4 else -1
+    ts = (q, k, v, A_log, a, dt_bias, b, output, new_state)
+    shapes = ((B, 1, H_QK, DK), (B, 1, H_QK, DK), (B, 1, HV, DV), (HV,), (B, 1, HV), (HV,),
+              (B, 1, HV), (B, 1, HV, DV), (B, HV, DV, DK))
+    if B < 0 or not (fast_ok(ts, _DTYPES, shapes) and
+                     (state is None or fast_ok((q, state), (_BF, _F32),
+                                               (shapes[0], shapes[-1])))):
+        _validate(q, k, v, state, A_log, a, dt_bias, b, output, new_state)
+        if state is not None and state.data_ptr() != new_state.data_ptr():
+            state = dense(state)
+        q, k, v, a, b, A_log, dt_bias = (dense(t) for t in (q, k, v, a, b, A_log, dt_bias))
+    dev = q.device
     scale = resolve_scale(scale)
-    if state is not None and state.data_ptr() != new_state.data_ptr():
-        state = dense(state)
-    q, k, v, a, b, A_log, dt_bias = (dense(t) for t in (q, k, v, a, b, A_log, dt_bias))
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(),
             None if state is None else state.data_ptr(), A_log.data_ptr(), a.data_ptr(),
             dt_bias.data_ptr(), b.data_ptr(), scale, output.data_ptr(), new_state.data_ptr(),
