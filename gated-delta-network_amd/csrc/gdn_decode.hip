@@ -166,11 +166,15 @@ const DecodeVariant kVariants[] = {
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 constexpr int kNontemporalFlag = 16;
 
-// Built-in tiling per batch size (measured on MI355X; see the decode sweep).
+// Built-in tiling per batch size, from the MI355X sweep of every tiling at
+// B = 1..64 (HIP-graph replay timing): small batches want many small
+// workgroups, large ones one wave streaming 64 rows (32 KiB in flight per
+// wave); non-temporal state accesses win at every size.
 int default_variant(int batch) {
-  if (batch <= 4) return 7;
-  if (batch <= 16) return 6;
-  return 2;
+  if (batch <= 4) return 3 + kNontemporalFlag;   // 16 rows, 256 threads
+  if (batch <= 8) return 2 + kNontemporalFlag;   // 32 rows, 256 threads
+  if (batch <= 32) return 5 + kNontemporalFlag;  // 32 rows,  64 threads
+  return 9 + kNontemporalFlag;                   // 64 rows,  64 threads
 }
 
 }  // namespace

@@ -60,3 +60,61 @@ __device__ __forceinline__ float gdn_log_decay(float A_log, float a, float dt_bi
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 }  // namespace gdn
+
+namespace gdn {
+
+// ---------------------------------------------------------------------------
+// MFMA (gfx950 v_mfma_f32_16x16x32_bf16) and the fragment conventions used by
+// every prefill kernel.  For one 16x16 output tile D = A (16x32) * B (32x16):
+//   A operand: lane l holds A[l & 15][8*(l >> 4) + e], e = 0..7 (8 bf16)
+//   B operand: lane l holds B[8*(l >> 4) + e][l & 15]
+//   D (4 f32): lane l holds D[4*(l >> 4) + r][l & 15], r = 0..3
+// Only the pairing of A's and B's k-index matters for the sum, and both use
+// the same (l >> 4, e) -> k map, so a fragment is always "8 consecutive k of
+// one row of A" or "8 consecutive k of one column of B".
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma_bf16(const u32x4 a, const u32x4 b, const f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Splits 8 floats into bf16 hi and lo parts with x = hi + lo + O(2^-17 |x|):
+// hi keeps the top 16 bits (exact remainder x - hi), lo is the remainder
+// rounded to nearest even.  Element e goes to bits [16e, 16e+16).
+__device__ __forceinline__ void split8(const float *x, u32x4 &hi, u32x4 &lo) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t u0 = __float_as_uint(x[2 * i]) & 0xffff0000u;
+    const uint32_t u1 = __float_as_uint(x[2 * i + 1]) & 0xffff0000u;
+    const float r0 = x[2 * i] - __uint_as_float(u0);
+    const float r1 = x[2 * i + 1] - __uint_as_float(u1);
+    hi[i] = (u0 >> 16) | u1;
+    lo[i] = static_cast<uint32_t>(f32_to_bf16(r0)) |
+            (static_cast<uint32_t>(f32_to_bf16(r1)) << 16);
+  }
+}
+
+// Rounds 8 floats to bf16 (nearest even) and packs them.
+__device__ __forceinline__ u32x4 pack8(const float *x) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r[i] = static_cast<uint32_t>(f32_to_bf16(x[2 * i])) |
+           (static_cast<uint32_t>(f32_to_bf16(x[2 * i + 1])) << 16);
+  return r;
+}
+
+// Unpacks 8 bf16 (as produced by pack8 / loaded from memory) to floats.
+__device__ __forceinline__ void unpack8(const u32x4 p, float *x) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __uint_as_float(p[i] << 16);
+    x[2 * i + 1] = __uint_as_float(p[i] & 0xffff0000u);
+  }
+}
+
+}  // namespace gdn

@@ -1,16 +1,749 @@
-// Gated DeltaNet chunked prefill: C-ABI entry points (kernels to follow).
+// Gated DeltaNet chunked prefill over a packed batch of variable-length
+// sequences (chunk = 64 tokens, WY representation), gfx950.
+//
+// Semantics: reference/gdn_prefill_ref.py:12-91.  Per sequence, v-head h and
+// chunk of C <= 64 tokens (g_i = -exp(A_log) softplus(a_i + dt_bias) is the
+// log decay, G = chunk-local inclusive cumsum of g, beta_i = sigmoid(b_i),
+// S = the [K=128, V=128] state at the chunk start):
+//   A_ij  = beta_i exp(G_i - G_j) <k_i, k_j>  for i > j, else 0
+//   T     = (I + A)^-1                       (unit lower triangular)
+//   u     = T (beta * V),   w = T (beta exp(G) * K)
+//   v_new = u - w S
+//   o_i   = scale (exp(G_i) q_i S + sum_{j<=i} exp(G_i - G_j) <q_i, k_j> v_new_j)
+//   S    <- exp(G_last) S + K^T (exp(G_last - G) * v_new)
+// the same chunked algebra as the reference's inlined FLA pipeline
+// (solutions/gdn_prefill_qk4_v8_d128_k_last/solution/triton/fla_kernels.py:
+// 858-905, 197-314, 334-383, 411-671, 714-796), re-planned for CDNA4:
+//
+//   1. index  : one workgroup turns cu_seqlens (on the device, never copied
+//               to the host) into the chunk table and per-sequence chunk
+//               offsets.  A zero-length sequence gets no chunk (the
+//               reference's seq-id rule, fla_kernels.py:63, would misnumber
+//               every later sequence).
+//   2. intra  : per (chunk, v-head): gating, cumsum, K K^T on MFMA, the
+//               64x64 triangular inverse in LDS (four 16x16 diagonal blocks
+//               by forward substitution, then the off-diagonal blocks by
+//               distance), u and w on MFMA.  No GVA copies: v-head h reads
+//               q/k head h/2 directly.
+//   3. state  : per (sequence, v-head, 16- or 32-column V block): the serial
+//               recurrence over chunks with the f32 state in MFMA
+//               accumulators; stores the chunk-start state and v_new.
+//   4. output : per (chunk, v-head): o from Q S, the masked Q K^T and v_new.
+//
+// Precision.  The state recurrence must hold 1e-3 of max|S| after 128-512
+// chunks.  Rounding any operand of w S or K^T v_new (or u, w themselves) to
+// one bf16 leaves ~2-4e-3 of max|S|, so those products use split bf16: an f32
+// operand x is carried as hi + lo (both bf16, x = hi + lo to ~2^-17) and a
+// product of two such operands as hi*hi + hi*lo + lo*hi (three MFMAs), or two
+// when the other operand is exact in bf16 (K).  u, w, T and the state stay
+// f32.  The output path (Q S, Q K^T, P v_new) uses single bf16 operands: its
+// error stays ~2^-9 relative, far inside the bf16 output tolerance.
 #include "gdn_device.h"
 #include "gdn_host.h"
 
-extern "C" size_t gdn_prefill_workspace_bytes(int total_tokens, int num_seqs) {
-  (void)total_tokens;
-  (void)num_seqs;
-  return 0;
+namespace gdn {
+
+// LDS row strides (elements), padded by 16 bytes against bank conflicts.
+constexpr int kStrideK = 136;  // bf16 [64][128] tiles
+constexpr int kStrideT = 72;   // bf16 [*][64]   tiles
+constexpr int kStrideA = 65;   // f32  [64][64]  tile
+
+// Workspace layout; every region starts on a 256-byte boundary.
+struct PrefillLayout {
+  int nt_max;  // upper bound on the chunk count from (T, N) alone
+  size_t chunks, offsets, G, beta, w_hi, w_lo, u, kt, ht, vnt, total;
+};
+
+static long long max_chunks(long long T, long long N) {
+  if (T <= 0 || N <= 0) return 0;
+  const long long bound = (T + N * (kChunk - 1)) / kChunk;
+  return bound < T ? bound : T;
 }
 
-extern "C" int gdn_prefill_fwd(const gdn_bf16 *, const gdn_bf16 *, const gdn_bf16 *, const float *,
-                               const float *, const gdn_bf16 *, const float *, const gdn_bf16 *,
-                               const void *, int, int, int, float, gdn_bf16 *, float *, void *,
-                               size_t, void *) {
-  return gdn::fail(GDN_ERR_LAUNCH, "gdn_prefill_fwd: not available in this build");
+static PrefillLayout prefill_layout(int T, int N) {
+  PrefillLayout L{};
+  const long long nt = max_chunks(T, N);
+  L.nt_max = static_cast<int>(nt);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off = (off + bytes + 255) & ~static_cast<size_t>(255);
+    return o;
+  };
+  const size_t n = static_cast<size_t>(nt);
+  L.chunks = take(n * sizeof(int4));
+  L.offsets = take((static_cast<size_t>(N) + 1) * sizeof(int));
+  L.G = take(n * kHV * kChunk * 4);
+  L.beta = take(n * kHV * kChunk * 4);
+  L.w_hi = take(n * kHV * kChunk * kDK * 2);
+  L.w_lo = take(n * kHV * kChunk * kDK * 2);
+  L.u = take(n * kHV * kChunk * kDV * 4);
+  L.kt = take(n * kHQK * kDK * kChunk * 2);
+  L.ht = take(n * kHV * kDV * kDK * 2);
+  L.vnt = take(n * kHV * kDV * kChunk * 2);
+  L.total = off;
+  return L;
+}
+
+__device__ __forceinline__ int load_cu(const void *cu, int is64, int i, int T) {
+  long long x = is64 ? static_cast<const long long *>(cu)[i] : static_cast<const int *>(cu)[i];
+  x = x < 0 ? 0 : x;
+  return static_cast<int>(x > T ? T : x);
+}
+
+// ---------------------------------------------------------------------------
+// 1. chunk table: chunks[c] = {sequence, first token, tokens (1..64), chunk
+// number within the sequence} for c < NT, {-1, 0, 0, 0} up to nt_max;
+// offsets[s] = first chunk of sequence s, offsets[N] = NT.  Token bounds are
+// clamped to [0, T] and the chunk count to nt_max, so a malformed cu_seqlens
+// cannot send any later kernel out of bounds.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int cu64, int N, int T,
+                                                              int nt_max, int4 *chunks,
+                                                              int *offsets) {
+  __shared__ int s_incl[1024];
+  const int tid = threadIdx.x;
+  long long carry = 0;
+  for (int base = 0; base < N; base += 1024) {
+    const int s = base + tid;
+    int n = 0;
+    if (s < N) {
+      const int bos = load_cu(cu, cu64, s, T);
+      int eos = load_cu(cu, cu64, s + 1, T);
+      eos = eos < bos ? bos : eos;
+      n = (eos - bos + kChunk - 1) / kChunk;
+    }
+    s_incl[tid] = n;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int y = tid >= off ? s_incl[tid - off] : 0;
+      __syncthreads();
+      s_incl[tid] += y;
+      __syncthreads();
+    }
+    const int tile_total = s_incl[1023];
+    if (s < N) {
+      const long long first = carry + s_incl[tid] - n;
+      offsets[s] = static_cast<int>(first < nt_max ? first : nt_max);
+    }
+    const int count = N - base < 1024 ? N - base : 1024;
+    const long long end = carry + tile_total < nt_max ? carry + tile_total : nt_max;
+    for (long long c = carry + tid; c < end; c += 1024) {
+      const int r = static_cast<int>(c - carry);
+      int lo = 0, hi = count - 1;  // first idx with s_incl[idx] > r
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (s_incl[mid] > r) hi = mid; else lo = mid + 1;
+      }
+      const int excl = lo == 0 ? 0 : s_incl[lo - 1];
+      const int sq = base + lo, local = r - excl;
+      const int bos = load_cu(cu, cu64, sq, T);
+      int eos = load_cu(cu, cu64, sq + 1, T);
+      eos = eos < bos ? bos : eos;
+      const int start = bos + local * kChunk;
+      const int len = eos - start < kChunk ? eos - start : kChunk;
+      chunks[c] = make_int4(sq, start, len, local);
+    }
+    carry += tile_total;
+    __syncthreads();
+  }
+  const int nt = static_cast<int>(carry < nt_max ? carry : nt_max);
+  if (tid == 0) offsets[N] = nt;
+  for (int c = nt + tid; c < nt_max; c += 1024) chunks[c] = make_int4(-1, 0, 0, 0);
+}
+
+// Index of an off-diagonal 16x16 block (p > q) of T in the sTo scratch.
+__device__ __forceinline__ int offdiag_slot(int p, int q) {
+  const int d = p - q;
+  return d == 1 ? q : (d == 2 ? 3 + q : 5);
+}
+
+// ---------------------------------------------------------------------------
+// 2. intra-chunk: per (chunk c = blockIdx.x, v-head h = blockIdx.y).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prefill_intra_kernel(
+    const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+    const float *__restrict__ A_log, const uint16_t *__restrict__ a,
+    const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
+    const int4 *__restrict__ chunks, float *__restrict__ ws_G, float *__restrict__ ws_beta,
+    uint16_t *__restrict__ ws_whi, uint16_t *__restrict__ ws_wlo, float *__restrict__ ws_u,
+    uint16_t *__restrict__ ws_kt) {
+  const int c = blockIdx.x, h = blockIdx.y;
+  const int4 ch = chunks[c];
+  if (ch.x < 0) return;
+  const int start = ch.y, len = ch.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, kg = (lane >> 4) * 8;
+  const int hq = h >> 1;
+
+  __shared__ __align__(16) uint16_t sK[kChunk * kStrideK];
+  __shared__ __align__(16) uint16_t sKt[kDK * kStrideT];
+  __shared__ __align__(16) uint16_t sVt[kDV * kStrideT];
+  __shared__ __align__(16) float sA[kChunk * kStrideA];
+  __shared__ float sTo[6][16 * 17];
+  __shared__ float sM[4][16 * 17];
+  __shared__ float sG[kChunk], sBeta[kChunk], sBG[kChunk];
+
+  // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding tokens
+  // get g = 0 and beta = 0, so G stays at G_last past the end of the chunk.
+  if (wave == 0) {
+    float g = 0.f, be = 0.f;
+    if (lane < len) {
+      const size_t t = static_cast<size_t>(start) + lane;
+      g = gdn_log_decay(A_log[h], bf16_to_f32(a[t * kHV + h]), dt_bias[h]);
+      be = sigmoidf_(bf16_to_f32(b[t * kHV + h]));
+    }
+    float G = g;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(G, off);
+      if (lane >= off) G += y;
+    }
+    sG[lane] = G;
+    sBeta[lane] = be;
+    sBG[lane] = be * expf(G);
+    const size_t gi = (static_cast<size_t>(c) * kHV + h) * kChunk + lane;
+    ws_G[gi] = G;
+    ws_beta[gi] = be;
+  }
+
+  // K (q/k head h/2) and V (head h) rows into LDS, zero past the chunk end;
+  // K row-major (for K K^T) and transposed (for w), V transposed (for u).
+  for (int idx = tid; idx < kChunk * 16; idx += 256) {
+    const int row = idx >> 4, c8 = (idx & 15) * 8;
+    u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
+    if (row < len) {
+      const size_t t = static_cast<size_t>(start) + row;
+      kv = *reinterpret_cast<const u32x4 *>(k + (t * kHQK + hq) * kDK + c8);
+      vv = *reinterpret_cast<const u32x4 *>(v + (t * kHV + h) * kDV + c8);
+    }
+    *reinterpret_cast<u32x4 *>(&sK[row * kStrideK + c8]) = kv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sKt[(c8 + e) * kStrideT + row] = static_cast<uint16_t>(kv[e >> 1] >> (16 * (e & 1)));
+      sVt[(c8 + e) * kStrideT + row] = static_cast<uint16_t>(vv[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+  __syncthreads();
+
+  // K^T of this chunk for the state kernel, once per q/k head.
+  if ((h & 1) == 0) {
+    uint16_t *dst = ws_kt + (static_cast<size_t>(c) * kHQK + hq) * kDK * kChunk;
+    for (int idx = tid; idx < kDK * 8; idx += 256) {
+      const int key = idx >> 3, t8 = (idx & 7) * 8;
+      *reinterpret_cast<u32x4 *>(dst + key * kChunk + t8) =
+          *reinterpret_cast<const u32x4 *>(&sKt[key * kStrideT + t8]);
+    }
+  }
+
+  // A = strictly-lower(beta_i exp(G_i - G_j) K K^T); wave w owns rows 16w..16w+15.
+  {
+    const int mb = wave;
+    for (int nb = 0; nb <= mb; ++nb) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const u32x4 af = *reinterpret_cast<const u32x4 *>(&sK[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
+        const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[(16 * nb + r16) * kStrideK + 32 * kk + kg]);
+        acc = mfma_bf16(af, bf, acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * mb + 4 * (lane >> 4) + r, j = 16 * nb + r16;
+        const float val = (i > j && i < len) ? sBeta[i] * expf(sG[i] - sG[j]) * acc[r] : 0.f;
+        sA[i * kStrideA + j] = val;
+      }
+    }
+  }
+  __syncthreads();
+
+  // T = (I + A)^-1.  Diagonal 16x16 blocks: wave w, lane j < 16 solves column j
+  // of block w by forward substitution and overwrites A's diagonal block.
+  if (lane < 16) {
+    const int base = 16 * wave;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float sacc = (i == lane) ? 1.f : 0.f;
+#pragma unroll
+      for (int m = 0; m < i; ++m) sacc -= sA[(base + i) * kStrideA + base + m] * x[m];
+      x[i] = sacc;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sA[(base + i) * kStrideA + base + lane] = x[i];
+  }
+  __syncthreads();
+
+  // Off-diagonal blocks, nearest the diagonal first:
+  //   T_pq = -T_pp * sum_{r=q}^{p-1} A_pr T_rq      (p > q)
+  // wave w handles block (p, q) = (w + d, w) of distance d; lane -> column
+  // j = lane & 15 and rows 4*(lane >> 4) + 0..3.
+  for (int d = 1; d <= 3; ++d) {
+    if (wave < 4 - d) {
+      const int p = wave + d, q = wave;
+      const int j = lane & 15, i0 = 4 * (lane >> 4);
+      float m4[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int r = q; r < p; ++r) {
+        // T_rq: diagonal block (r == q) lives in sA, the others in sTo.
+        const float *trq = (r == q) ? &sA[(16 * r) * kStrideA + 16 * q] : &sTo[offdiag_slot(r, q)][0];
+        const int trq_stride = (r == q) ? kStrideA : 17;
+#pragma unroll
+        for (int mm = 0; mm < 16; ++mm) {
+          const float t = trq[mm * trq_stride + j];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) m4[e] += sA[(16 * p + i0 + e) * kStrideA + 16 * r + mm] * t;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sM[wave][(i0 + e) * 17 + j] = m4[e];
+      __builtin_amdgcn_wave_barrier();
+      float t4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mm = 0; mm < 16; ++mm) {
+        const float mv = sM[wave][mm * 17 + j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t4[e] -= sA[(16 * p + i0 + e) * kStrideA + 16 * p + mm] * mv;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sTo[offdiag_slot(p, q)][(i0 + e) * 17 + j] = t4[e];
+    }
+    __syncthreads();
+  }
+
+  // Assemble the full T in sA: off-diagonal blocks from sTo, zeros above.
+  for (int idx = tid; idx < kChunk * kChunk; idx += 256) {
+    const int i = idx >> 6, j = idx & 63, p = i >> 4, q = j >> 4;
+    if (q > p) sA[i * kStrideA + j] = 0.f;
+    else if (q < p) sA[i * kStrideA + j] = sTo[offdiag_slot(p, q)][(i & 15) * 17 + (j & 15)];
+  }
+  __syncthreads();
+
+  // u = T (beta * V), w = T (beta exp(G) * K), split-bf16 products (3 MFMAs
+  // each); wave w owns rows 16w..16w+15 and all 128 columns.
+  {
+    const int mb = wave;
+    u32x4 th[2], tl[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = sA[(16 * mb + r16) * kStrideA + 32 * kk + kg + e];
+      split8(x, th[kk], tl[kk]);
+    }
+    const size_t row_base = (static_cast<size_t>(c) * kHV + h) * kChunk;
+    for (int nb = 0; nb < 8; ++nb) {
+      f32x4 au = {0.f, 0.f, 0.f, 0.f}, aw = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int j0 = 32 * kk + kg;
+        float fv[8], fk[8];
+        unpack8(*reinterpret_cast<const u32x4 *>(&sVt[(16 * nb + r16) * kStrideT + j0]), fv);
+        unpack8(*reinterpret_cast<const u32x4 *>(&sKt[(16 * nb + r16) * kStrideT + j0]), fk);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          fv[e] *= sBeta[j0 + e];
+          fk[e] *= sBG[j0 + e];
+        }
+        u32x4 vh, vl, kh, kl;
+        split8(fv, vh, vl);
+        split8(fk, kh, kl);
+        au = mfma_bf16(th[kk], vh, au);
+        au = mfma_bf16(th[kk], vl, au);
+        au = mfma_bf16(tl[kk], vh, au);
+        aw = mfma_bf16(th[kk], kh, aw);
+        aw = mfma_bf16(th[kk], kl, aw);
+        aw = mfma_bf16(tl[kk], kh, aw);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * mb + 4 * (lane >> 4) + r, n = 16 * nb + r16;
+        const size_t o = (row_base + i) * kDV + n;
+        ws_u[o] = au[r];
+        const uint32_t hb = __float_as_uint(aw[r]) & 0xffff0000u;
+        ws_whi[o] = static_cast<uint16_t>(hb >> 16);
+        ws_wlo[o] = f32_to_bf16(aw[r] - __uint_as_float(hb));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. state recurrence: per (sequence s, v-head h, V block of BV columns).
+// blockIdx.x = h + 8 * (vb + NVB * s): every workgroup of one head lands on
+// the same XCD (workgroups are dealt round-robin over the 8 XCDs), so the
+// per-head w and K^T stream through one L2.
+// State tile S[:, v0:v0+BV] ([K=128] x [BV], f32) lives in MFMA accumulators:
+// wave w owns K-rows 32w..32w+31 (two 16-row tiles) for all BV/16 column tiles.
+// ---------------------------------------------------------------------------
+template <int BV>
+__global__ __launch_bounds__(256) void prefill_state_kernel(
+    const float *state, float *new_state, const int *__restrict__ offsets,
+    const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_whi,
+    const uint16_t *__restrict__ ws_wlo, const float *__restrict__ ws_u,
+    const uint16_t *__restrict__ ws_kt, uint16_t *__restrict__ ws_ht,
+    uint16_t *__restrict__ ws_vnt) {
+  constexpr int NVB = kDV / BV;
+  constexpr int NTT = BV / 16;
+  const int h = blockIdx.x % kHV;
+  const int rest = blockIdx.x / kHV;
+  const int vb = rest % NVB, s = rest / NVB;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
+  const int v0 = vb * BV;
+
+  __shared__ __align__(16) uint16_t sSh[BV * kStrideK];
+  __shared__ __align__(16) uint16_t sSl[BV * kStrideK];
+  __shared__ __align__(16) uint16_t sVh[BV * kStrideT];
+  __shared__ __align__(16) uint16_t sVl[BV * kStrideT];
+  __shared__ float sG[kChunk];
+
+  const int c0 = offsets[s];
+  const int nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
+  const size_t sbase = (static_cast<size_t>(s) * kHV + h) * kDV * kDK;  // [V][K]
+
+  f32x4 S[2][NTT];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int nt = 0; nt < NTT; ++nt) {
+      const int kr = 16 * (2 * wave + mi) + q4, vc = v0 + 16 * nt + r16;
+      if (state != nullptr && nch > 0)
+        S[mi][nt] = *reinterpret_cast<const f32x4 *>(state + sbase + static_cast<size_t>(vc) * kDK + kr);
+      else
+        S[mi][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  for (int ci = 0; ci < nch; ++ci) {
+    const int c = c0 + ci;
+    const size_t ch_head = static_cast<size_t>(c) * kHV + h;
+    if (tid < kChunk) sG[tid] = ws_G[ch_head * kChunk + tid];
+
+    // (a) chunk-start state: split copy into LDS ([v][k]) for w S, and a bf16
+    //     copy ([v][k]) for the output kernel.
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int nt = 0; nt < NTT; ++nt) {
+        const int kr = 16 * (2 * wave + mi) + q4, vl = 16 * nt + r16;
+        u32x2 hi, lo, rn;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float x0 = S[mi][nt][2 * e], x1 = S[mi][nt][2 * e + 1];
+          const uint32_t u0 = __float_as_uint(x0) & 0xffff0000u;
+          const uint32_t u1 = __float_as_uint(x1) & 0xffff0000u;
+          hi[e] = (u0 >> 16) | u1;
+          lo[e] = static_cast<uint32_t>(f32_to_bf16(x0 - __uint_as_float(u0))) |
+                  (static_cast<uint32_t>(f32_to_bf16(x1 - __uint_as_float(u1))) << 16);
+          rn[e] = static_cast<uint32_t>(f32_to_bf16(x0)) |
+                  (static_cast<uint32_t>(f32_to_bf16(x1)) << 16);
+        }
+        *reinterpret_cast<u32x2 *>(&sSh[vl * kStrideK + kr]) = hi;
+        *reinterpret_cast<u32x2 *>(&sSl[vl * kStrideK + kr]) = lo;
+        *reinterpret_cast<u32x2 *>(ws_ht + (ch_head * kDV + v0 + vl) * kDK + kr) = rn;
+      }
+    __syncthreads();
+
+    // (b) v_new = u - w S for rows 16*wave..+15 (split bf16: 3 MFMAs per k-step).
+    f32x4 P[NTT];
+#pragma unroll
+    for (int nt = 0; nt < NTT; ++nt) P[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const size_t wrow = (ch_head * kChunk + 16 * wave + r16) * kDK;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 wh = *reinterpret_cast<const u32x4 *>(ws_whi + wrow + 32 * kk + kg);
+      const u32x4 wl = *reinterpret_cast<const u32x4 *>(ws_wlo + wrow + 32 * kk + kg);
+#pragma unroll
+      for (int nt = 0; nt < NTT; ++nt) {
+        const u32x4 sh = *reinterpret_cast<const u32x4 *>(&sSh[(16 * nt + r16) * kStrideK + 32 * kk + kg]);
+        const u32x4 sl = *reinterpret_cast<const u32x4 *>(&sSl[(16 * nt + r16) * kStrideK + 32 * kk + kg]);
+        P[nt] = mfma_bf16(wh, sh, P[nt]);
+        P[nt] = mfma_bf16(wh, sl, P[nt]);
+        P[nt] = mfma_bf16(wl, sh, P[nt]);
+      }
+    }
+
+    // (c) v_new -> workspace (bf16, [v][token]) for the output kernel, and
+    //     exp(G_last - G_i) v_new -> LDS (split, [v][token]) for K^T v.
+    const float G_last = sG[kChunk - 1];
+#pragma unroll
+    for (int nt = 0; nt < NTT; ++nt) {
+      const int vl = 16 * nt + r16;
+      float vn[4], vs[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * wave + q4 + r;
+        vn[r] = ws_u[(ch_head * kChunk + i) * kDV + v0 + vl] - P[nt][r];
+        vs[r] = expf(G_last - sG[i]) * vn[r];
+      }
+      u32x2 rn, hi, lo;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        rn[e] = static_cast<uint32_t>(f32_to_bf16(vn[2 * e])) |
+                (static_cast<uint32_t>(f32_to_bf16(vn[2 * e + 1])) << 16);
+        const uint32_t u0 = __float_as_uint(vs[2 * e]) & 0xffff0000u;
+        const uint32_t u1 = __float_as_uint(vs[2 * e + 1]) & 0xffff0000u;
+        hi[e] = (u0 >> 16) | u1;
+        lo[e] = static_cast<uint32_t>(f32_to_bf16(vs[2 * e] - __uint_as_float(u0))) |
+                (static_cast<uint32_t>(f32_to_bf16(vs[2 * e + 1] - __uint_as_float(u1))) << 16);
+      }
+      const int i0 = 16 * wave + q4;
+      *reinterpret_cast<u32x2 *>(ws_vnt + (ch_head * kDV + v0 + vl) * kChunk + i0) = rn;
+      *reinterpret_cast<u32x2 *>(&sVh[vl * kStrideT + i0]) = hi;
+      *reinterpret_cast<u32x2 *>(&sVl[vl * kStrideT + i0]) = lo;
+    }
+    __syncthreads();
+
+    // (d) S <- exp(G_last) S + K^T (exp(G_last - G) v_new); K is exact in bf16,
+    //     so two MFMAs (hi, lo) per k-step.
+    const float eg = expf(G_last);
+    const uint16_t *kt = ws_kt + (static_cast<size_t>(c) * kHQK + (h >> 1)) * kDK * kChunk;
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+      const int mt = 2 * wave + mi;
+#pragma unroll
+      for (int nt = 0; nt < NTT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[mi][nt][r] *= eg;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const u32x4 ka = *reinterpret_cast<const u32x4 *>(kt + (16 * mt + r16) * kChunk + 32 * kk + kg);
+#pragma unroll
+        for (int nt = 0; nt < NTT; ++nt) {
+          const u32x4 vh = *reinterpret_cast<const u32x4 *>(&sVh[(16 * nt + r16) * kStrideT + 32 * kk + kg]);
+          const u32x4 vl = *reinterpret_cast<const u32x4 *>(&sVl[(16 * nt + r16) * kStrideT + 32 * kk + kg]);
+          S[mi][nt] = mfma_bf16(ka, vh, S[mi][nt]);
+          S[mi][nt] = mfma_bf16(ka, vl, S[mi][nt]);
+        }
+      }
+    }
+  }
+
+  // Final state (zeros for a zero-length sequence, as the reference).
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int nt = 0; nt < NTT; ++nt) {
+      const int kr = 16 * (2 * wave + mi) + q4, vc = v0 + 16 * nt + r16;
+      *reinterpret_cast<f32x4 *>(new_state + sbase + static_cast<size_t>(vc) * kDK + kr) = S[mi][nt];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 4. chunk output: per (chunk c = blockIdx.x, v-head h = blockIdx.y).
+//   P  = mask_{j<=i} exp(G_i - G_j) Q K^T      (waves split the rows)
+//   O  = exp(G_i) Q S_c + P v_new              (waves split the columns)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prefill_output_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
+    const int4 *__restrict__ chunks, const float *__restrict__ ws_G,
+    const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
+    uint16_t *__restrict__ out) {
+  const int c = blockIdx.x, h = blockIdx.y;
+  const int4 ch = chunks[c];
+  if (ch.x < 0) return;
+  const int start = ch.y, len = ch.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
+  const int hq = h >> 1;
+  const size_t ch_head = static_cast<size_t>(c) * kHV + h;
+
+  __shared__ __align__(16) uint16_t sQ[kChunk * kStrideK];
+  __shared__ __align__(16) uint16_t sK[kChunk * kStrideK];
+  __shared__ __align__(16) uint16_t sP[kChunk * kStrideT];
+  __shared__ float sG[kChunk];
+
+  if (tid < kChunk) sG[tid] = ws_G[ch_head * kChunk + tid];
+  for (int idx = tid; idx < kChunk * 16; idx += 256) {
+    const int row = idx >> 4, c8 = (idx & 15) * 8;
+    u32x4 qv = {0u, 0u, 0u, 0u}, kv = {0u, 0u, 0u, 0u};
+    if (row < len) {
+      const size_t t = static_cast<size_t>(start) + row;
+      qv = *reinterpret_cast<const u32x4 *>(q + (t * kHQK + hq) * kDK + c8);
+      kv = *reinterpret_cast<const u32x4 *>(k + (t * kHQK + hq) * kDK + c8);
+    }
+    *reinterpret_cast<u32x4 *>(&sQ[row * kStrideK + c8]) = qv;
+    *reinterpret_cast<u32x4 *>(&sK[row * kStrideK + c8]) = kv;
+  }
+  __syncthreads();
+
+  {
+    const int mb = wave;
+    for (int nb = 0; nb < 4; ++nb) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (nb <= mb) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const u32x4 af = *reinterpret_cast<const u32x4 *>(&sQ[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
+          const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[(16 * nb + r16) * kStrideK + 32 * kk + kg]);
+          acc = mfma_bf16(af, bf, acc);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * mb + q4 + r, j = 16 * nb + r16;
+        const float p = (j <= i && i < len) ? expf(sG[i] - sG[j]) * acc[r] : 0.f;
+        sP[i * kStrideT + j] = f32_to_bf16(p);
+      }
+    }
+  }
+  __syncthreads();
+
+  f32x4 O[4][2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int n = 16 * (2 * wave + nt) + r16;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) O[mb][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 hb = *reinterpret_cast<const u32x4 *>(ws_ht + (ch_head * kDV + n) * kDK + 32 * kk + kg);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const u32x4 qa = *reinterpret_cast<const u32x4 *>(&sQ[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
+        O[mb][nt] = mfma_bf16(qa, hb, O[mb][nt]);
+      }
+    }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) O[mb][nt][r] *= expf(sG[16 * mb + q4 + r]);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const u32x4 vb = *reinterpret_cast<const u32x4 *>(ws_vnt + (ch_head * kDV + n) * kChunk + 32 * kk + kg);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const u32x4 pa = *reinterpret_cast<const u32x4 *>(&sP[(16 * mb + r16) * kStrideT + 32 * kk + kg]);
+        O[mb][nt] = mfma_bf16(pa, vb, O[mb][nt]);
+      }
+    }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * mb + q4 + r;
+        if (i < len)
+          out[((static_cast<size_t>(start) + i) * kHV + h) * kDV + n] = f32_to_bf16(scale * O[mb][nt][r]);
+      }
+  }
+}
+
+static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                          const float *state, const float *A_log, const gdn_bf16 *a,
+                          const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
+                          int cu64, int N, int T, float scale, gdn_bf16 *output, float *new_state,
+                          void *workspace, size_t ws_bytes, void *stream_ptr, int variant) {
+  clear_error();
+  if (N < 0 || T < 0) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: num_seqs=%d, total_tokens=%d", N, T);
+  if (!cu_seqlens) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: null cu_seqlens");
+  if (!A_log || !dt_bias) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: null pointer argument");
+  if (T > 0 && (!q || !k || !v || !a || !b || !output))
+    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: null pointer argument");
+  if (N > 0 && !new_state) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: null new_state");
+  if (!(scale > 0.0f) || scale == __builtin_inff())
+    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: scale must be finite and > 0");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16))
+    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: q/k/v must be 16-byte aligned");
+  if (!aligned(new_state, 16) || (state && !aligned(state, 16)))
+    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: state/new_state must be 16-byte aligned");
+  if (!aligned(cu_seqlens, cu64 ? 8 : 4))
+    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: cu_seqlens misaligned");
+  if (variant < -1 || variant > 1) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown variant %d", variant);
+  if (N == 0) return GDN_OK;
+
+  const PrefillLayout L = prefill_layout(T, N);
+  if (!workspace || ws_bytes < L.total)
+    return fail(GDN_ERR_WORKSPACE, "gdn_prefill_fwd: workspace of %zu bytes, %zu needed", ws_bytes, L.total);
+  if (!aligned(workspace, 256)) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: workspace must be 256-byte aligned");
+
+  const size_t nT = static_cast<size_t>(T), nN = static_cast<size_t>(N);
+  const size_t state_bytes = nN * kHV * kDV * kDK * 4;
+  const size_t out_bytes = nT * kHV * kDV * 2;
+  const void *ins[] = {q, k, v, a, b, A_log, dt_bias, cu_seqlens, state};
+  const size_t in_bytes[] = {nT * kHQK * kDK * 2, nT * kHQK * kDK * 2, nT * kHV * kDV * 2,
+                             nT * kHV * 2,        nT * kHV * 2,        kHV * 4,
+                             kHV * 4,             (nN + 1) * (cu64 ? 8 : 4),
+                             state ? state_bytes : 0};
+  for (int i = 0; i < 9; ++i) {
+    if (overlaps(output, out_bytes, ins[i], in_bytes[i]))
+      return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: output overlaps an input");
+    if (i < 8 && overlaps(new_state, state_bytes, ins[i], in_bytes[i]))
+      return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: new_state overlaps an input");
+    if (overlaps(workspace, L.total, ins[i], in_bytes[i]))
+      return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: workspace overlaps an input");
+  }
+  if (state != new_state && overlaps(state, state_bytes, new_state, state_bytes))
+    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: new_state partially overlaps state");
+  if (overlaps(output, out_bytes, new_state, state_bytes) ||
+      overlaps(workspace, L.total, output, out_bytes) ||
+      overlaps(workspace, L.total, new_state, state_bytes))
+    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: outputs/workspace overlap");
+
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  char *ws = static_cast<char *>(workspace);
+  int4 *chunks = reinterpret_cast<int4 *>(ws + L.chunks);
+  int *offsets = reinterpret_cast<int *>(ws + L.offsets);
+  float *wsG = reinterpret_cast<float *>(ws + L.G);
+  float *wsB = reinterpret_cast<float *>(ws + L.beta);
+  uint16_t *whi = reinterpret_cast<uint16_t *>(ws + L.w_hi);
+  uint16_t *wlo = reinterpret_cast<uint16_t *>(ws + L.w_lo);
+  float *wsu = reinterpret_cast<float *>(ws + L.u);
+  uint16_t *kt = reinterpret_cast<uint16_t *>(ws + L.kt);
+  uint16_t *ht = reinterpret_cast<uint16_t *>(ws + L.ht);
+  uint16_t *vnt = reinterpret_cast<uint16_t *>(ws + L.vnt);
+
+  hipLaunchKernelGGL(prefill_index_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, cu64, N, T,
+                     L.nt_max, chunks, offsets);
+  int rc = check_launch("gdn_prefill_fwd(index)");
+  if (rc) return rc;
+  if (L.nt_max > 0) {
+    hipLaunchKernelGGL(prefill_intra_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, k, v, A_log,
+                       a, dt_bias, b, chunks, wsG, wsB, whi, wlo, wsu, kt);
+    if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
+  }
+  const int bv = variant == 1 ? 32 : (variant == 0 ? 16 : (N * kHV * (kDV / 32) >= 512 ? 32 : 16));
+  const long long blocks = static_cast<long long>(N) * kHV * (kDV / bv);
+  if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
+  if (bv == 32)
+    hipLaunchKernelGGL(prefill_state_kernel<32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       stream, state, new_state, offsets, wsG, whi, wlo, wsu, kt, ht, vnt);
+  else
+    hipLaunchKernelGGL(prefill_state_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       stream, state, new_state, offsets, wsG, whi, wlo, wsu, kt, ht, vnt);
+  if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
+  if (L.nt_max > 0) {
+    hipLaunchKernelGGL(prefill_output_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, q, k, chunks,
+                       wsG, ht, vnt, scale, output);
+    if ((rc = check_launch("gdn_prefill_fwd(output)"))) return rc;
+  }
+  return GDN_OK;
+}
+
+}  // namespace gdn
+
+extern "C" size_t gdn_prefill_workspace_bytes(int total_tokens, int num_seqs) {
+  if (total_tokens < 0 || num_seqs < 0) return 0;
+  return gdn::prefill_layout(total_tokens, num_seqs).total;
+}
+
+extern "C" int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                               const float *state, const float *A_log, const gdn_bf16 *a,
+                               const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
+                               int cu_seqlens_is_int64, int num_seqs, int total_tokens, float scale,
+                               gdn_bf16 *output, float *new_state, void *workspace,
+                               size_t workspace_bytes, void *stream) {
+  return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
+                             num_seqs, total_tokens, scale, output, new_state, workspace,
+                             workspace_bytes, stream, -1);
+}
+
+extern "C" int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                                       const float *state, const float *A_log, const gdn_bf16 *a,
+                                       const float *dt_bias, const gdn_bf16 *b,
+                                       const void *cu_seqlens, int cu_seqlens_is_int64,
+                                       int num_seqs, int total_tokens, float scale,
+                                       gdn_bf16 *output, float *new_state, void *workspace,
+                                       size_t workspace_bytes, void *stream, int variant) {
+  return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
+                             num_seqs, total_tokens, scale, output, new_state, workspace,
+                             workspace_bytes, stream, variant);
 }

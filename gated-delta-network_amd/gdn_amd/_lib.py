@@ -34,6 +34,8 @@ SIGNATURES = {
     "gdn_prefill_workspace_bytes": (_SZ, [_I, _I]),
     "gdn_prefill_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P, _P,
                              _SZ, _P]),
+    "gdn_prefill_fwd_variant": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P,
+                                     _P, _SZ, _P, _I]),
 }
 
 

@@ -74,7 +74,8 @@ def _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_stat
     return T, N, dev
 
 
-def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state):
+def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state, *,
+           variant=-1):
     """Chunked GDN prefill over a packed batch, written into ``output`` and
     ``new_state``.
 
@@ -82,6 +83,8 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
     None; A_log, dt_bias [8] f32; a, b [T,8] bf16; cu_seqlens [N+1] int32/int64
     on the device (0 = cu[0] <= ... <= cu[N] = T); scale float, 0-d tensor or
     None; output [T,8,128] bf16; new_state [N,8,128,128] f32 (may be state).
+    ``variant`` picks the state-recurrence tiling (gdn_prefill_fwd_variant);
+    the default is the built-in one.
     """
     lib = _lib.load()
     T, N, dev = _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state)
@@ -93,11 +96,14 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
     stream = stream_of(dev)
     nbytes = int(lib.gdn_prefill_workspace_bytes(T, N))
     ws = _workspace(dev, stream, nbytes)
-    rc = lib.gdn_prefill_fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), None if state is None else state.data_ptr(),
-        A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr(), cu_seqlens.data_ptr(),
-        1 if cu_seqlens.dtype == torch.int64 else 0, N, T, scale, output.data_ptr(),
-        new_state.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), None if state is None else state.data_ptr(),
+            A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr(),
+            cu_seqlens.data_ptr(), 1 if cu_seqlens.dtype == torch.int64 else 0, N, T, scale,
+            output.data_ptr(), new_state.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    if variant == -1:
+        rc = lib.gdn_prefill_fwd(*args)
+    else:
+        rc = lib.gdn_prefill_fwd_variant(*args, int(variant))
     _lib.check(rc, "gdn_prefill_fwd")
 
 

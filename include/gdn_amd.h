@@ -113,6 +113,22 @@ int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                     gdn_bf16 *output, float *new_state, void *workspace,
                     size_t workspace_bytes, void *stream);
 
+/*
+ * gdn_prefill_fwd with an explicit tiling of the serial state recurrence:
+ * variant 0 = 16-column V blocks (8 workgroups per sequence and head),
+ * 1 = 32-column blocks (4 per sequence and head), -1 = the built-in choice
+ * (what gdn_prefill_fwd uses).  The counterpart of the reference's autotuned
+ * BV of chunk_gated_delta_rule_fwd_kernel_h (solutions/
+ * gdn_prefill_qk4_v8_d128_k_last/solution/triton/fla_kernels.py:407-426,
+ * 1028-1035).  Results agree to rounding for every variant.
+ */
+int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                            const float *state, const float *A_log, const gdn_bf16 *a,
+                            const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
+                            int cu_seqlens_is_int64, int num_seqs, int total_tokens, float scale,
+                            gdn_bf16 *output, float *new_state, void *workspace,
+                            size_t workspace_bytes, void *stream, int variant);
+
 #ifdef __cplusplus
 }
 #endif

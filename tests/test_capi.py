@@ -85,3 +85,46 @@ def test_check_maps_status_to_exceptions():
         _lib.check(_lib.GDN_ERR_WORKSPACE, "x")
     with pytest.raises(_lib.GdnError):
         _lib.check(_lib.GDN_ERR_LAUNCH, "x")
+
+
+def _prefill_args(**over):
+    args = dict(q=1 << 20, k=2 << 20, v=3 << 20, state=None, A_log=4 << 20, a=5 << 20,
+                dt_bias=6 << 20, b=7 << 20, cu=8 << 20, cu64=1, N=2, T=100, scale=0.1,
+                output=16 << 20, new_state=32 << 20, ws=64 << 20, ws_bytes=1 << 30, stream=None)
+    args.update(over)
+    return list(args.values())
+
+
+def test_prefill_workspace_bytes():
+    lib = _lib.load()
+    assert lib.gdn_prefill_workspace_bytes(0, 0) >= 0
+    assert lib.gdn_prefill_workspace_bytes(-1, 1) == 0
+    small = lib.gdn_prefill_workspace_bytes(64, 1)
+    big = lib.gdn_prefill_workspace_bytes(8192, 1)
+    assert 0 < small < big
+    # bounded by the chunk count alone: 1x8192 -> 128 chunks
+    assert big < 128 * 2 ** 20
+    assert lib.gdn_prefill_workspace_bytes(8192, 4) > big
+
+
+@pytest.mark.parametrize("over, needle, code", [
+    (dict(cu=None), "cu_seqlens", _lib.GDN_ERR_INVALID),
+    (dict(q=None), "null", _lib.GDN_ERR_INVALID),
+    (dict(N=-1), "num_seqs", _lib.GDN_ERR_INVALID),
+    (dict(scale=-1.0), "scale", _lib.GDN_ERR_INVALID),
+    (dict(q=(1 << 20) + 8), "aligned", _lib.GDN_ERR_INVALID),
+    (dict(ws_bytes=16), "workspace", _lib.GDN_ERR_WORKSPACE),
+    (dict(ws=None), "workspace", _lib.GDN_ERR_WORKSPACE),
+    (dict(output=(3 << 20) + 64), "overlap", _lib.GDN_ERR_INVALID),
+    (dict(ws=(1 << 20)), "overlap", _lib.GDN_ERR_INVALID),
+])
+def test_prefill_rejects_bad_arguments(over, needle, code):
+    lib = _lib.load()
+    rc = lib.gdn_prefill_fwd(*_prefill_args(**over))
+    assert rc == code
+    assert needle in _lib.last_error()
+
+
+def test_prefill_no_sequences_is_a_no_op():
+    lib = _lib.load()
+    assert lib.gdn_prefill_fwd(*_prefill_args(N=0, T=0)) == _lib.GDN_OK

@@ -1,0 +1,316 @@
+"""Prefill parity on the GPU: the HIP pipeline (through the C ABI, via the DPS
+entry point) against the CPU oracle on the same seeded inputs.
+
+Tolerance (stated once in conftest.py): bf16 output atol = rtol = 1e-2; f32
+final state atol = 1e-3 * max|state_ref|.  The oracle is the sequential
+recurrence (oracle/gdn_seq.c, pinned against the numpy restatement and the
+float64 chunked form in tests/test_oracle.py).  Stage checks compare the
+workspace intermediates with the float64 chunked oracle.
+"""
+
+import importlib.util
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import PKG, assert_output_close, assert_state_close
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SOLUTION = os.path.join(PKG, "solutions", "gdn_prefill_qk4_v8_d128_k_last", "solution", "hip",
+                        "kernel.py")
+
+
+def _entry():
+    spec = importlib.util.spec_from_file_location("gdn_prefill_solution", SOLUTION)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.kernel
+
+
+kernel = _entry()
+
+
+def to_dev(inp, dev, cu_dtype=torch.int64):
+    bf = torch.bfloat16
+    d = {n: torch.from_numpy(np.ascontiguousarray(inp[n])).to(dev).to(bf)
+         for n in ("q", "k", "v", "a", "b")}
+    for n in ("A_log", "dt_bias"):
+        d[n] = torch.from_numpy(inp[n]).to(dev)
+    d["state"] = None if inp["state"] is None else torch.from_numpy(inp["state"]).to(dev)
+    d["cu_seqlens"] = torch.from_numpy(inp["cu_seqlens"]).to(dev).to(cu_dtype)
+    d["scale"] = inp["scale"]
+    return d
+
+
+def run_gpu(d, dev, in_place=False, variant=None):
+    T = d["q"].shape[0]
+    N = d["cu_seqlens"].numel() - 1
+    out = torch.empty((T, 8, 128), dtype=torch.bfloat16, device=dev)
+    ns = d["state"] if in_place else torch.empty((N, 8, 128, 128), dtype=torch.float32, device=dev)
+    args = (d["q"], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"], d["b"],
+            d["cu_seqlens"], d["scale"], out, ns)
+    if variant is None:
+        kernel(*args)
+    else:
+        from gdn_amd import prefill
+        prefill.kernel(*args, variant=variant)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), ns.cpu().numpy()
+
+
+def check(o, s, o_ref, s_ref):
+    assert_output_close(o, o_ref)
+    assert_state_close(s, s_ref)
+
+
+# The reference's own prefill cases (tests/test_prefill.py:196-217) and the
+# configurations of its benchmark script (scripts/benchmark.py:131-142).
+REFERENCE_CASES = [
+    ([32], False), ([64], False), ([128], False), ([256], False), ([31], False), ([65], False),
+    ([127], False), ([64, 64], False), ([32, 96], False), ([64, 128], False),
+    ([64], True), ([128], True), ([64, 128], True),
+    ([512], True), ([1024], True), ([128, 128], True), ([256, 256], True),
+    ([32, 64, 128, 256], True),
+]
+
+
+@pytest.mark.parametrize("lens, with_state", REFERENCE_CASES)
+def test_prefill_reference_cases(cuda_device, lens, with_state):
+    print(f"prefill parity lens={lens} state={with_state}", flush=True)
+    inp = O.make_prefill_inputs(lens, seed=100 + len(lens), with_state=with_state)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+@pytest.mark.parametrize("lens", [[1], [2, 1, 3], [63], [0, 5, 0, 70], [0], [0, 0, 17],
+                                  [129, 0, 1, 64, 65]])
+def test_prefill_edge_lengths(cuda_device, lens):
+    print(f"prefill edge lens={lens}", flush=True)
+    inp = O.make_prefill_inputs(lens, seed=7)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device)
+    for i, L in enumerate(lens):
+        if L == 0:
+            assert np.all(s[i] == 0.0), "zero-length sequence must give a zero state"
+    check(o, s, o_ref, s_ref)
+
+
+def test_prefill_many_sequences_multi_tile_index(cuda_device):
+    # > 1024 sequences: the chunk-index scan runs over several tiles.
+    rng = np.random.default_rng(11)
+    lens = rng.integers(0, 4, 1500).tolist()
+    lens[0] = 70
+    inp = O.make_prefill_inputs(lens, seed=8)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+def test_prefill_config2_1x1024(cuda_device):
+    cfg = O.CONFIGS["prefill_1x1024"]
+    inp = O.make_prefill_inputs(cfg["lens"], seed=cfg["seed"], with_state=cfg["with_state"])
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+def test_prefill_config3_varlen(cuda_device):
+    cfg = O.CONFIGS["prefill_varlen6"]
+    inp = O.make_prefill_inputs(cfg["lens"], seed=cfg["seed"], with_state=cfg["with_state"])
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+def test_prefill_1x8192(cuda_device):
+    cfg = O.CONFIGS["prefill_1x8192"]
+    inp = O.make_prefill_inputs(cfg["lens"], seed=cfg["seed"], with_state=cfg["with_state"])
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+def test_prefill_config4_long_context(cuda_device):
+    cfg = O.CONFIGS["prefill_4x8192"]
+    inp = O.make_prefill_inputs(cfg["lens"], seed=cfg["seed"], with_state=cfg["with_state"],
+                                slow_decay_heads=cfg["slow_decay_heads"])
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+def test_prefill_variants_identical(cuda_device):
+    inp = O.make_prefill_inputs([100, 0, 300], seed=12)
+    d = to_dev(inp, cuda_device)
+    o0, s0 = run_gpu(d, cuda_device, variant=0)
+    o1, s1 = run_gpu(d, cuda_device, variant=1)
+    assert np.array_equal(o0, o1) and np.array_equal(s0, s1)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    check(o0, s0, o_ref, s_ref)
+
+
+def test_prefill_int32_cu_seqlens_state_none_in_place(cuda_device):
+    inp = O.make_prefill_inputs([40, 90], seed=13)
+    d64 = to_dev(inp, cuda_device)
+    d32 = to_dev(inp, cuda_device, cu_dtype=torch.int32)
+    o64, s64 = run_gpu(d64, cuda_device)
+    o32, s32 = run_gpu(d32, cuda_device)
+    assert np.array_equal(o64, o32) and np.array_equal(s64, s32)
+    oi, si = run_gpu(d64, cuda_device, in_place=True)
+    assert np.array_equal(o64, oi) and np.array_equal(s64, si)
+    inp["state"] = None
+    dn = to_dev(inp, cuda_device)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    on, sn = run_gpu(dn, cuda_device)
+    check(on, sn, o_ref, s_ref)
+
+
+def test_prefill_scale_forms(cuda_device):
+    inp = O.make_prefill_inputs([70], seed=14)
+    d = to_dev(inp, cuda_device)
+    o1, _ = run_gpu(dict(d, scale=None), cuda_device)
+    o2, _ = run_gpu(dict(d, scale=0.0), cuda_device)
+    o3, _ = run_gpu(dict(d, scale=torch.tensor(1 / math.sqrt(128))), cuda_device)
+    assert np.array_equal(o1, o2) and np.array_equal(o1, o3)
+    o_ref, s_ref = O.prefill_seq_c(**dict(inp, scale=0.25))
+    o4, s4 = run_gpu(dict(d, scale=0.25), cuda_device)
+    check(o4, s4, o_ref, s_ref)
+
+
+def test_prefill_reference_test_distribution(cuda_device):
+    # The reference's own recipe (tests/test_prefill.py:106-113): q, k, v ~
+    # 0.1 N(0,1) (not normalised), b ~ 0.1 N(0,1), initial state 0.01 N(0,1),
+    # scale 1.0.
+    rng = np.random.default_rng(42)
+    lens = [64, 128]
+    T, N = sum(lens), len(lens)
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    inp = dict(q=O.bf16_round(0.1 * f(T, 4, 128)), k=O.bf16_round(0.1 * f(T, 4, 128)),
+               v=O.bf16_round(0.1 * f(T, 8, 128)), state=0.01 * f(N, 8, 128, 128),
+               A_log=0.1 * f(8), a=O.bf16_round(0.1 * f(T, 8)), dt_bias=0.1 * f(8),
+               b=O.bf16_round(0.1 * f(T, 8)), cu_seqlens=np.array([0, 64, 192]), scale=1.0)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device)
+    check(o, s, o_ref, s_ref)
+
+
+def test_prefill_deterministic(cuda_device):
+    inp = O.make_prefill_inputs([200, 77], seed=15)
+    d = to_dev(inp, cuda_device)
+    runs = [run_gpu(d, cuda_device) for _ in range(3)]
+    for o, s in runs[1:]:
+        assert np.array_equal(o, runs[0][0]) and np.array_equal(s, runs[0][1])
+
+
+def test_prefill_then_decode_continues_the_sequence(cuda_device):
+    # prefill(L) then one decode step == prefill(L + 1)  (the state is the
+    # resumable checkpoint between the two operators)
+    from gdn_amd import decode
+    L = 100
+    inp = O.make_prefill_inputs([L + 1], seed=16)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    first = {n: (x[:L] if n in ("q", "k", "v", "a", "b") else x) for n, x in inp.items()}
+    first["cu_seqlens"] = np.array([0, L])
+    d = to_dev(first, cuda_device)
+    o_pre, s_pre = run_gpu(d, cuda_device)
+    dev = cuda_device
+    st = torch.from_numpy(s_pre).to(dev)
+    step = lambda n: torch.from_numpy(np.ascontiguousarray(inp[n][L:L + 1])).to(dev).to(torch.bfloat16)
+    out = torch.empty((1, 1, 8, 128), dtype=torch.bfloat16, device=dev)
+    decode.kernel(step("q")[None], step("k")[None], step("v")[None], st,
+                  torch.from_numpy(inp["A_log"]).to(dev), step("a")[None],
+                  torch.from_numpy(inp["dt_bias"]).to(dev), step("b")[None], inp["scale"], out, st)
+    torch.cuda.synchronize()
+    o = np.concatenate([o_pre, out.float().cpu().numpy()[0]])
+    check(o, st.cpu().numpy(), o_ref, s_ref)
+
+
+def test_prefill_rejects_bad_arguments(cuda_device):
+    inp = O.make_prefill_inputs([10], seed=17)
+    d = to_dev(inp, cuda_device)
+    out = torch.empty((10, 8, 128), dtype=torch.bfloat16, device=cuda_device)
+    ns = torch.empty((1, 8, 128, 128), dtype=torch.float32, device=cuda_device)
+    with pytest.raises(ValueError, match="cu_seqlens"):
+        kernel(d["q"], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"], d["b"],
+               d["cu_seqlens"].float(), d["scale"], out, ns)
+    with pytest.raises(ValueError, match="shape"):
+        kernel(d["q"][:5], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"], d["b"],
+               d["cu_seqlens"], d["scale"], out, ns)
+
+
+# ------------------------------------------------------------------ stages
+
+def _layout(T, N):
+    """Mirror of the workspace layout of gdn_prefill.hip (prefill_layout)."""
+    nt = O.max_chunks(T, N)
+    off = 0
+    L = {"nt": nt}
+
+    def take(name, nbytes):
+        nonlocal off
+        L[name] = off
+        off = (off + nbytes + 255) // 256 * 256
+
+    take("chunks", nt * 16)
+    take("offsets", (N + 1) * 4)
+    take("G", nt * 8 * 64 * 4)
+    take("beta", nt * 8 * 64 * 4)
+    take("w_hi", nt * 8 * 64 * 128 * 2)
+    take("w_lo", nt * 8 * 64 * 128 * 2)
+    take("u", nt * 8 * 64 * 128 * 4)
+    take("kt", nt * 4 * 128 * 64 * 2)
+    take("ht", nt * 8 * 128 * 128 * 2)
+    take("vnt", nt * 8 * 128 * 64 * 2)
+    L["total"] = off
+    return L
+
+
+def test_prefill_stage_intermediates(cuda_device):
+    from gdn_amd import _lib, prefill
+    lens = [100, 0, 64, 5]
+    inp = O.make_prefill_inputs(lens, seed=18)
+    T, N = sum(lens), len(lens)
+    L = _layout(T, N)
+    assert prefill.workspace_bytes(T, N) == L["total"]
+    d = to_dev(inp, cuda_device)
+    run_gpu(d, cuda_device)
+    ws = prefill._workspace(cuda_device, _stream(cuda_device), 0).cpu().numpy()
+    _, _, it = O.prefill_chunked(**inp, return_intermediates=True)
+    seq, local, offs = O.chunk_index(inp["cu_seqlens"])
+    nt = int(offs[-1])
+
+    def arr(name, dtype, shape):
+        n = int(np.prod(shape))
+        return np.frombuffer(ws[L[name]:L[name] + n * np.dtype(dtype).itemsize].tobytes(),
+                             dtype=dtype).reshape(shape)
+
+    chunks = arr("chunks", np.int32, (L["nt"], 4))
+    assert chunks[:nt, 0].tolist() == seq.tolist()
+    assert chunks[:nt, 3].tolist() == local.tolist()
+    assert (chunks[nt:, 0] == -1).all()
+    assert arr("offsets", np.int32, (N + 1,)).tolist() == offs.tolist()
+    G = arr("G", np.float32, (L["nt"], 8, 64))[:nt]
+    for c in range(nt):
+        C = min(64, lens[seq[c]] - 64 * local[c])
+        assert np.allclose(G[c, :, :C], it["g_cs"][c, :, :C], rtol=1e-5, atol=1e-5)
+    u = arr("u", np.float32, (L["nt"], 8, 64, 128))[:nt]
+    assert np.abs(u - it["u"]).max() <= 1e-4 * np.abs(it["u"]).max()
+    w = (O.bf16_from_bits(arr("w_hi", np.uint16, (L["nt"], 8, 64, 128))[:nt]).astype(np.float64)
+         + O.bf16_from_bits(arr("w_lo", np.uint16, (L["nt"], 8, 64, 128))[:nt]))
+    assert np.abs(w - it["w"]).max() <= 1e-4 * np.abs(it["w"]).max()
+    ht = O.bf16_from_bits(arr("ht", np.uint16, (L["nt"], 8, 128, 128))[:nt])
+    assert np.abs(ht - it["h"].transpose(0, 1, 3, 2)).max() <= 1e-2 * np.abs(it["h"]).max()
+    vnt = O.bf16_from_bits(arr("vnt", np.uint16, (L["nt"], 8, 128, 64))[:nt])
+    assert np.abs(vnt - it["v_new"].transpose(0, 1, 3, 2)).max() <= \
+        1e-2 * np.abs(it["v_new"]).max()
+
+
+def _stream(dev):
+    from gdn_amd._common import stream_of
+    return stream_of(dev)
