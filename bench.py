@@ -106,6 +106,53 @@ def bench_decode(B, steps, warmup, dev, variant=-1):
     return ms_eager, ms_graph
 
 
+def bench_prefill(lens, steps, warmup, dev, variant=-1):
+    """Times `steps` prefill calls on a packed batch with sequence lengths
+    `lens` (the configs[2..4] recipe, zero initial state for one sequence)
+    and returns (eager ms/call, graph ms/call)."""
+    import numpy as np
+    import torch
+    from gdn_amd import prefill
+    from oracle import gdn_oracle as O  # input recipe only
+
+    inp = O.make_prefill_inputs(lens, seed=2, with_state=len(lens) > 1)
+    d = _dev_inputs(inp, dev)
+    cu = torch.from_numpy(inp["cu_seqlens"]).to(dev)
+    T, N = sum(lens), len(lens)
+    out = torch.empty((T, 8, 128), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((N, 8, 128, 128), dtype=torch.float32, device=dev)
+
+    def step():
+        prefill.kernel(d["q"], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"],
+                       d["b"], cu, inp["scale"], out, ns, variant=variant)
+
+    def timed(fn):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record()
+        fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1)
+
+    for _ in range(warmup):
+        step()
+    ms_eager = timed(lambda: [step() for _ in range(steps)]) / steps
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    with torch.cuda.graph(graph):
+        for _ in range(steps):
+            step()
+    graph.replay()
+    ms_graph = min(timed(graph.replay) for _ in range(3)) / steps
+    return ms_eager, ms_graph
+
+
 def cpu_baseline_decode(B, seconds):
     """The reference's decode loop nest restated in numpy (oracle decode_loop),
     one thread, repeated until `seconds` of CPU time have passed."""
@@ -164,6 +211,24 @@ def main():
     log(f"decode B={B}: graph {ms_step * 1e3:.2f} us/step ({gbs_step:.1f} GB/s, "
         f"{gbs_step / HBM_PEAK_GBPS:.1%} of peak); eager {ms_eager * 1e3:.2f} us/step")
 
+    if args.sweep:
+        for lens in ([1024], [6, 49, 294, 1800, 2040, 61], [8192], [8192] * 4, [64], [256]):
+            for var in (-1, 0, 1):
+                pe, pg = bench_prefill(lens, max(5, args.steps // 10), 3, dev, var)
+                T = sum(lens)
+                log(f"sweep prefill lens={lens if len(lens) < 5 else f'{len(lens)}x{lens[0]}'} "
+                    f"variant={var}: eager {pe:.3f} ms, graph {pg:.3f} ms, "
+                    f"{T / (pg * 1e-3) / 1e6:.2f} M tok/s")
+
+    pre_lens = [8192]
+    pre_eager, pre_ms = bench_prefill(pre_lens, max(10, args.steps // 10), 3, dev)
+    T8 = sum(pre_lens)
+    nt8 = sum(-(-L // 64) for L in pre_lens)
+    pre_tflops = O.prefill_flops(nt8) / (pre_ms * 1e-3) / 1e12
+    pre_gbs = O.prefill_bytes(T8, len(pre_lens)) / (pre_ms * 1e-3) / 1e9
+    log(f"prefill 1x8192: graph {pre_ms:.3f} ms ({T8 / (pre_ms * 1e-3) / 1e6:.2f} M tok/s, "
+        f"{pre_tflops:.1f} TFLOP/s, {pre_gbs:.0f} GB/s); eager {pre_eager:.3f} ms")
+
     cpu_s, reps = cpu_baseline_decode(B, args.cpu_seconds)
     cpu_gbs = nbytes / cpu_s / 1e9
     log(f"cpu baseline decode B={B}: {cpu_s * 1e3:.1f} ms/step over {reps} steps")
@@ -186,6 +251,14 @@ def main():
                    "batch": B, "heads_qk": 4, "heads_v": 8, "head_dim": 128},
         "decode_us_per_step": round(ms_step * 1e3, 3),
         "decode_us_per_step_eager": round(ms_eager * 1e3, 3),
+        "prefill_ms_1x8192": round(pre_ms, 4),
+        "prefill_ms_1x8192_eager": round(pre_eager, 4),
+        "prefill_tokens_per_s": round(T8 / (pre_ms * 1e-3), 1),
+        "prefill_roofline": {"bound": "mfma", "achieved": round(pre_tflops, 2), "peak": 2500.0,
+                             "unit": "TFLOP/s", "frac": round(pre_tflops / 2500.0, 5),
+                             "hbm_gbs": round(pre_gbs, 1),
+                             "flops_per_call": O.prefill_flops(nt8),
+                             "bytes_per_call": O.prefill_bytes(T8, len(pre_lens))},
         "roofline": {"bound": "hbm", "achieved": round(gbs_step, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(gbs_step / HBM_PEAK_GBPS, 4),
                      "traffic": None, "kernel": "gdn::decode_kernel",
