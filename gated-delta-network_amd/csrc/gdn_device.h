@@ -20,12 +20,27 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// float -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (torch's choice).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// float -> bf16 bits, round to nearest even (gfx950 v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// Two floats -> packed bf16 pair (a in bits 0..15), one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// Split of two floats into bf16 hi/lo pairs: hi keeps the top 16 bits of each
+// (so x - hi is exact), lo is that remainder rounded to nearest even;
+// x = hi + lo to ~2^-17 relative.
+__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
+  const uint32_t ua = __float_as_uint(a) & 0xffff0000u;
+  const uint32_t ub = __float_as_uint(b) & 0xffff0000u;
+  hi = (ua >> 16) | ub;
+  lo = pk_bf16(a - __uint_as_float(ua), b - __uint_as_float(ub));
 }
 
 // Data-parallel-primitive lane moves.  CTRL is a DPP control word:
@@ -88,13 +103,10 @@ __device__ __forceinline__ f32x4 mfma_bf16(const u32x4 a, const u32x4 b, const f
 __device__ __forceinline__ void split8(const float *x, u32x4 &hi, u32x4 &lo) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t u0 = __float_as_uint(x[2 * i]) & 0xffff0000u;
-    const uint32_t u1 = __float_as_uint(x[2 * i + 1]) & 0xffff0000u;
-    const float r0 = x[2 * i] - __uint_as_float(u0);
-    const float r1 = x[2 * i + 1] - __uint_as_float(u1);
-    hi[i] = (u0 >> 16) | u1;
-    lo[i] = static_cast<uint32_t>(f32_to_bf16(r0)) |
-            (static_cast<uint32_t>(f32_to_bf16(r1)) << 16);
+    uint32_t h, l;
+    split2(x[2 * i], x[2 * i + 1], h, l);
+    hi[i] = h;
+    lo[i] = l;
   }
 }
 
@@ -102,9 +114,7 @@ __device__ __forceinline__ void split8(const float *x, u32x4 &hi, u32x4 &lo) {
 __device__ __forceinline__ u32x4 pack8(const float *x) {
   u32x4 r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    r[i] = static_cast<uint32_t>(f32_to_bf16(x[2 * i])) |
-           (static_cast<uint32_t>(f32_to_bf16(x[2 * i + 1])) << 16);
+  for (int i = 0; i < 4; ++i) r[i] = pk_bf16(x[2 * i], x[2 * i + 1]);
   return r;
 }
 

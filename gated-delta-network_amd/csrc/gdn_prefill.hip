@@ -51,7 +51,7 @@ constexpr int kStrideA = 65;   // f32  [64][64]  tile
 // Workspace layout; every region starts on a 256-byte boundary.
 struct PrefillLayout {
   int nt_max;  // upper bound on the chunk count from (T, N) alone
-  size_t chunks, offsets, G, beta, w_hi, w_lo, u, kt, ht, vnt, total;
+  size_t chunks, offsets, G, dcy, eg, w_hi, w_lo, u, kt, ht, vnt, total;
 };
 
 static long long max_chunks(long long T, long long N) {
@@ -74,7 +74,8 @@ static PrefillLayout prefill_layout(int T, int N) {
   L.chunks = take(n * sizeof(int4));
   L.offsets = take((static_cast<size_t>(N) + 1) * sizeof(int));
   L.G = take(n * kHV * kChunk * 4);
-  L.beta = take(n * kHV * kChunk * 4);
+  L.dcy = take(n * kHV * kChunk * 4);
+  L.eg = take(n * kHV * 4);
   L.w_hi = take(n * kHV * kChunk * kDK * 2);
   L.w_lo = take(n * kHV * kChunk * kDK * 2);
   L.u = take(n * kHV * kChunk * kDV * 4);
@@ -165,8 +166,8 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
-    const int4 *__restrict__ chunks, float *__restrict__ ws_G, float *__restrict__ ws_beta,
-    uint16_t *__restrict__ ws_whi, uint16_t *__restrict__ ws_wlo, float *__restrict__ ws_u,
+    const int4 *__restrict__ chunks, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
+    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_whi, uint16_t *__restrict__ ws_wlo, float *__restrict__ ws_u,
     uint16_t *__restrict__ ws_kt) {
   const int c = blockIdx.x, h = blockIdx.y;
   const int4 ch = chunks[c];
@@ -202,9 +203,14 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
     sG[lane] = G;
     sBeta[lane] = be;
     sBG[lane] = be * expf(G);
+    // Decay factors of the state update: exp(G_last - G_i) per row and
+    // exp(G_last) for the carried state (G_last = G of lane 63; padding
+    // tokens keep G at G_last).
+    const float G_last = __shfl(G, 63);
     const size_t gi = (static_cast<size_t>(c) * kHV + h) * kChunk + lane;
     ws_G[gi] = G;
-    ws_beta[gi] = be;
+    ws_dcy[gi] = expf(G_last - G);
+    if (lane == 0) ws_eg[static_cast<size_t>(c) * kHV + h] = expf(G_last);
   }
 
   // K (q/k head h/2) and V (head h) rows into LDS, zero past the chunk end;
@@ -372,16 +378,58 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
 // blockIdx.x = h + 8 * (vb + NVB * s): every workgroup of one head lands on
 // the same XCD (workgroups are dealt round-robin over the 8 XCDs), so the
 // per-head w and K^T stream through one L2.
-// State tile S[:, v0:v0+BV] ([K=128] x [BV], f32) lives in MFMA accumulators:
-// wave w owns K-rows 32w..32w+31 (two 16-row tiles) for all BV/16 column tiles.
+// The state tile S[:, v0:v0+BV] ([K=128] x [BV], f32) lives in MFMA
+// accumulators: wave w owns K-rows 32w..32w+31 (two 16-row tiles) for all
+// BV/16 column tiles.  Everything a chunk needs that does not depend on the
+// state (w, K^T, u, decay factors) is register-prefetched two chunks ahead,
+// so the serial chain per chunk is two LDS exchanges, two barriers and the
+// MFMAs.  Addresses are a per-chunk scalar base plus a 32-bit lane offset.
 // ---------------------------------------------------------------------------
+template <int NTT>
+struct ChunkFrag {
+  u32x4 wh[4], wl[4];  // w rows 16*wave + (lane & 15), k-steps 0..3 (hi / lo)
+  u32x4 ka[2][2];      // K^T rows 16*(2*wave + mi) + (lane & 15), k-steps 0..1
+  float u[NTT][4];     // u[16*wave + 4*(lane >> 4) + r][v0 + 16*nt + (lane & 15)]
+  f32x4 dcy;           // exp(G_last - G_i) of the lane's four v_new rows
+  float eg;            // exp(G_last)
+};
+
+template <int NTT>
+__device__ __forceinline__ void load_chunk_frag(ChunkFrag<NTT> &f, int c, int h, int v0, int wave,
+                                                int lane, const float *ws_dcy, const float *ws_eg,
+                                                const uint16_t *ws_whi, const uint16_t *ws_wlo,
+                                                const float *ws_u, const uint16_t *ws_kt) {
+  const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
+  const size_t ch_head = static_cast<size_t>(c) * kHV + h;
+  const uint16_t *whi = ws_whi + ch_head * (kChunk * kDK);
+  const uint16_t *wlo = ws_wlo + ch_head * (kChunk * kDK);
+  const int woff = (16 * wave + r16) * kDK + kg;
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    f.wh[kk] = *reinterpret_cast<const u32x4 *>(whi + woff + 32 * kk);
+    f.wl[kk] = *reinterpret_cast<const u32x4 *>(wlo + woff + 32 * kk);
+  }
+  const uint16_t *kt = ws_kt + (static_cast<size_t>(c) * kHQK + (h >> 1)) * (kDK * kChunk);
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+      f.ka[mi][kk] = *reinterpret_cast<const u32x4 *>(
+          kt + (16 * (2 * wave + mi) + r16) * kChunk + 32 * kk + kg);
+  const float *u = ws_u + ch_head * (kChunk * kDV);
+#pragma unroll
+  for (int nt = 0; nt < NTT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) f.u[nt][r] = u[(16 * wave + q4 + r) * kDV + v0 + 16 * nt + r16];
+  f.dcy = *reinterpret_cast<const f32x4 *>(ws_dcy + ch_head * kChunk + 16 * wave + q4);
+  f.eg = ws_eg[ch_head];
+}
+
 template <int BV>
 __global__ __launch_bounds__(256) void prefill_state_kernel(
-    const float *state, float *new_state, const int *__restrict__ offsets,
-    const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_whi,
-    const uint16_t *__restrict__ ws_wlo, const float *__restrict__ ws_u,
-    const uint16_t *__restrict__ ws_kt, uint16_t *__restrict__ ws_ht,
-    uint16_t *__restrict__ ws_vnt) {
+    const float *state, float *new_state, const int *offsets, const float *ws_dcy,
+    const float *ws_eg, const uint16_t *ws_whi, const uint16_t *ws_wlo, const float *ws_u,
+    const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt) {
   constexpr int NVB = kDV / BV;
   constexpr int NTT = BV / 16;
   const int h = blockIdx.x % kHV;
@@ -395,7 +443,6 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
   __shared__ __align__(16) uint16_t sSl[BV * kStrideK];
   __shared__ __align__(16) uint16_t sVh[BV * kStrideT];
   __shared__ __align__(16) uint16_t sVl[BV * kStrideT];
-  __shared__ float sG[kChunk];
 
   const int c0 = offsets[s];
   const int nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
@@ -408,16 +455,16 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
     for (int nt = 0; nt < NTT; ++nt) {
       const int kr = 16 * (2 * wave + mi) + q4, vc = v0 + 16 * nt + r16;
       if (state != nullptr && nch > 0)
-        S[mi][nt] = *reinterpret_cast<const f32x4 *>(state + sbase + static_cast<size_t>(vc) * kDK + kr);
+        S[mi][nt] = *reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + kr);
       else
         S[mi][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-  for (int ci = 0; ci < nch; ++ci) {
-    const int c = c0 + ci;
+  // One chunk of the recurrence, from the prefetched fragments f.
+  auto step = [&](const ChunkFrag<NTT> &f, int c) {
     const size_t ch_head = static_cast<size_t>(c) * kHV + h;
-    if (tid < kChunk) sG[tid] = ws_G[ch_head * kChunk + tid];
-
+    uint16_t *ht = ws_ht + ch_head * (kDV * kDK);
+    uint16_t *vnt = ws_vnt + ch_head * (kDV * kChunk);
     // (a) chunk-start state: split copy into LDS ([v][k]) for w S, and a bf16
     //     copy ([v][k]) for the output kernel.
 #pragma unroll
@@ -425,96 +472,103 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
 #pragma unroll
       for (int nt = 0; nt < NTT; ++nt) {
         const int kr = 16 * (2 * wave + mi) + q4, vl = 16 * nt + r16;
-        u32x2 hi, lo, rn;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float x0 = S[mi][nt][2 * e], x1 = S[mi][nt][2 * e + 1];
-          const uint32_t u0 = __float_as_uint(x0) & 0xffff0000u;
-          const uint32_t u1 = __float_as_uint(x1) & 0xffff0000u;
-          hi[e] = (u0 >> 16) | u1;
-          lo[e] = static_cast<uint32_t>(f32_to_bf16(x0 - __uint_as_float(u0))) |
-                  (static_cast<uint32_t>(f32_to_bf16(x1 - __uint_as_float(u1))) << 16);
-          rn[e] = static_cast<uint32_t>(f32_to_bf16(x0)) |
-                  (static_cast<uint32_t>(f32_to_bf16(x1)) << 16);
-        }
+        uint32_t h0, h1, l0, l1;
+        split2(S[mi][nt][0], S[mi][nt][1], h0, l0);
+        split2(S[mi][nt][2], S[mi][nt][3], h1, l1);
+        const u32x2 hi = {h0, h1}, lo = {l0, l1};
+        const u32x2 rn = {pk_bf16(S[mi][nt][0], S[mi][nt][1]), pk_bf16(S[mi][nt][2], S[mi][nt][3])};
         *reinterpret_cast<u32x2 *>(&sSh[vl * kStrideK + kr]) = hi;
         *reinterpret_cast<u32x2 *>(&sSl[vl * kStrideK + kr]) = lo;
-        *reinterpret_cast<u32x2 *>(ws_ht + (ch_head * kDV + v0 + vl) * kDK + kr) = rn;
+        *reinterpret_cast<u32x2 *>(ht + (v0 + vl) * kDK + kr) = rn;
       }
     __syncthreads();
 
-    // (b) v_new = u - w S for rows 16*wave..+15 (split bf16: 3 MFMAs per k-step).
-    f32x4 P[NTT];
+    // (b) w S for rows 16*wave..+15; three independent accumulation chains
+    //     (hi*hi, hi*lo, lo*hi) shorten the dependent MFMA sequence.
+    f32x4 P0[NTT], P1[NTT], P2[NTT];
 #pragma unroll
-    for (int nt = 0; nt < NTT; ++nt) P[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const size_t wrow = (ch_head * kChunk + 16 * wave + r16) * kDK;
+    for (int nt = 0; nt < NTT; ++nt) {
+      P0[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      P1[nt] = P0[nt];
+      P2[nt] = P0[nt];
+    }
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const u32x4 wh = *reinterpret_cast<const u32x4 *>(ws_whi + wrow + 32 * kk + kg);
-      const u32x4 wl = *reinterpret_cast<const u32x4 *>(ws_wlo + wrow + 32 * kk + kg);
+    for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
       for (int nt = 0; nt < NTT; ++nt) {
         const u32x4 sh = *reinterpret_cast<const u32x4 *>(&sSh[(16 * nt + r16) * kStrideK + 32 * kk + kg]);
         const u32x4 sl = *reinterpret_cast<const u32x4 *>(&sSl[(16 * nt + r16) * kStrideK + 32 * kk + kg]);
-        P[nt] = mfma_bf16(wh, sh, P[nt]);
-        P[nt] = mfma_bf16(wh, sl, P[nt]);
-        P[nt] = mfma_bf16(wl, sh, P[nt]);
+        P0[nt] = mfma_bf16(f.wh[kk], sh, P0[nt]);
+        P1[nt] = mfma_bf16(f.wh[kk], sl, P1[nt]);
+        P2[nt] = mfma_bf16(f.wl[kk], sh, P2[nt]);
       }
-    }
 
-    // (c) v_new -> workspace (bf16, [v][token]) for the output kernel, and
-    //     exp(G_last - G_i) v_new -> LDS (split, [v][token]) for K^T v.
-    const float G_last = sG[kChunk - 1];
+    // (c) v_new = u - w S -> workspace (bf16, [v][token]) for the output
+    //     kernel; exp(G_last - G_i) v_new -> LDS (split, [v][token]) for K^T v.
 #pragma unroll
     for (int nt = 0; nt < NTT; ++nt) {
       const int vl = 16 * nt + r16;
       float vn[4], vs[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 16 * wave + q4 + r;
-        vn[r] = ws_u[(ch_head * kChunk + i) * kDV + v0 + vl] - P[nt][r];
-        vs[r] = expf(G_last - sG[i]) * vn[r];
+        vn[r] = f.u[nt][r] - ((P0[nt][r] + P1[nt][r]) + P2[nt][r]);
+        vs[r] = f.dcy[r] * vn[r];
       }
-      u32x2 rn, hi, lo;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        rn[e] = static_cast<uint32_t>(f32_to_bf16(vn[2 * e])) |
-                (static_cast<uint32_t>(f32_to_bf16(vn[2 * e + 1])) << 16);
-        const uint32_t u0 = __float_as_uint(vs[2 * e]) & 0xffff0000u;
-        const uint32_t u1 = __float_as_uint(vs[2 * e + 1]) & 0xffff0000u;
-        hi[e] = (u0 >> 16) | u1;
-        lo[e] = static_cast<uint32_t>(f32_to_bf16(vs[2 * e] - __uint_as_float(u0))) |
-                (static_cast<uint32_t>(f32_to_bf16(vs[2 * e + 1] - __uint_as_float(u1))) << 16);
-      }
+      const u32x2 rn = {pk_bf16(vn[0], vn[1]), pk_bf16(vn[2], vn[3])};
+      uint32_t h0, h1, l0, l1;
+      split2(vs[0], vs[1], h0, l0);
+      split2(vs[2], vs[3], h1, l1);
+      const u32x2 hi = {h0, h1}, lo = {l0, l1};
       const int i0 = 16 * wave + q4;
-      *reinterpret_cast<u32x2 *>(ws_vnt + (ch_head * kDV + v0 + vl) * kChunk + i0) = rn;
+      *reinterpret_cast<u32x2 *>(vnt + (v0 + vl) * kChunk + i0) = rn;
       *reinterpret_cast<u32x2 *>(&sVh[vl * kStrideT + i0]) = hi;
       *reinterpret_cast<u32x2 *>(&sVl[vl * kStrideT + i0]) = lo;
     }
     __syncthreads();
 
     // (d) S <- exp(G_last) S + K^T (exp(G_last - G) v_new); K is exact in bf16,
-    //     so two MFMAs (hi, lo) per k-step.
-    const float eg = expf(G_last);
-    const uint16_t *kt = ws_kt + (static_cast<size_t>(c) * kHQK + (h >> 1)) * kDK * kChunk;
+    //     so two MFMAs (hi, lo) per k-step, in two independent chains.
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi) {
-      const int mt = 2 * wave + mi;
+    for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-      for (int nt = 0; nt < NTT; ++nt)
+      for (int nt = 0; nt < NTT; ++nt) {
+        f32x4 acc = S[mi][nt];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) S[mi][nt][r] *= eg;
+        for (int r = 0; r < 4; ++r) acc[r] *= f.eg;
+        f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const u32x4 ka = *reinterpret_cast<const u32x4 *>(kt + (16 * mt + r16) * kChunk + 32 * kk + kg);
-#pragma unroll
-        for (int nt = 0; nt < NTT; ++nt) {
+        for (int kk = 0; kk < 2; ++kk) {
           const u32x4 vh = *reinterpret_cast<const u32x4 *>(&sVh[(16 * nt + r16) * kStrideT + 32 * kk + kg]);
           const u32x4 vl = *reinterpret_cast<const u32x4 *>(&sVl[(16 * nt + r16) * kStrideT + 32 * kk + kg]);
-          S[mi][nt] = mfma_bf16(ka, vh, S[mi][nt]);
-          S[mi][nt] = mfma_bf16(ka, vl, S[mi][nt]);
+          acc = mfma_bf16(f.ka[mi][kk], vh, acc);
+          acc2 = mfma_bf16(f.ka[mi][kk], vl, acc2);
         }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[mi][nt][r] = acc[r] + acc2[r];
       }
+  };
+
+  // Ring of three fragment sets: chunk i uses set i % 3 while the sets of
+  // chunks i + 1 and i + 2 are in flight.  Prefetches past the last chunk
+  // re-read the last chunk, so every iteration issues the same loads and the
+  // compiler can wait for exactly the set in use (a conditional load would
+  // make it wait for all outstanding loads).  The workspace pointers carry no
+  // __restrict__ on purpose: that keeps the compiler from sinking these loads
+  // to their first use.
+  if (nch > 0) {
+    auto chunk_at = [&](int i) { return c0 + (i < nch ? i : nch - 1); };
+    ChunkFrag<NTT> fa, fb, fc;
+    load_chunk_frag(fa, chunk_at(0), h, v0, wave, lane, ws_dcy, ws_eg, ws_whi, ws_wlo, ws_u, ws_kt);
+    load_chunk_frag(fb, chunk_at(1), h, v0, wave, lane, ws_dcy, ws_eg, ws_whi, ws_wlo, ws_u, ws_kt);
+    for (int ci = 0; ci < nch; ci += 3) {
+      load_chunk_frag(fc, chunk_at(ci + 2), h, v0, wave, lane, ws_dcy, ws_eg, ws_whi, ws_wlo, ws_u, ws_kt);
+      step(fa, c0 + ci);
+      if (ci + 1 >= nch) break;
+      load_chunk_frag(fa, chunk_at(ci + 3), h, v0, wave, lane, ws_dcy, ws_eg, ws_whi, ws_wlo, ws_u, ws_kt);
+      step(fb, c0 + ci + 1);
+      if (ci + 2 >= nch) break;
+      load_chunk_frag(fb, chunk_at(ci + 4), h, v0, wave, lane, ws_dcy, ws_eg, ws_whi, ws_wlo, ws_u, ws_kt);
+      step(fc, c0 + ci + 2);
     }
   }
 
@@ -524,7 +578,7 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
 #pragma unroll
     for (int nt = 0; nt < NTT; ++nt) {
       const int kr = 16 * (2 * wave + mi) + q4, vc = v0 + 16 * nt + r16;
-      *reinterpret_cast<f32x4 *>(new_state + sbase + static_cast<size_t>(vc) * kDK + kr) = S[mi][nt];
+      *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + kr) = S[mi][nt];
     }
 }
 
@@ -683,7 +737,8 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   int4 *chunks = reinterpret_cast<int4 *>(ws + L.chunks);
   int *offsets = reinterpret_cast<int *>(ws + L.offsets);
   float *wsG = reinterpret_cast<float *>(ws + L.G);
-  float *wsB = reinterpret_cast<float *>(ws + L.beta);
+  float *wsD = reinterpret_cast<float *>(ws + L.dcy);
+  float *wsE = reinterpret_cast<float *>(ws + L.eg);
   uint16_t *whi = reinterpret_cast<uint16_t *>(ws + L.w_hi);
   uint16_t *wlo = reinterpret_cast<uint16_t *>(ws + L.w_lo);
   float *wsu = reinterpret_cast<float *>(ws + L.u);
@@ -697,7 +752,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   if (rc) return rc;
   if (L.nt_max > 0) {
     hipLaunchKernelGGL(prefill_intra_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, k, v, A_log,
-                       a, dt_bias, b, chunks, wsG, wsB, whi, wlo, wsu, kt);
+                       a, dt_bias, b, chunks, wsG, wsD, wsE, whi, wlo, wsu, kt);
     if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
   }
   const int bv = variant == 1 ? 32 : (variant == 0 ? 16 : (N * kHV * (kDV / 32) >= 512 ? 32 : 16));
@@ -705,10 +760,10 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
   if (bv == 32)
     hipLaunchKernelGGL(prefill_state_kernel<32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       stream, state, new_state, offsets, wsG, whi, wlo, wsu, kt, ht, vnt);
+                       stream, state, new_state, offsets, wsD, wsE, whi, wlo, wsu, kt, ht, vnt);
   else
     hipLaunchKernelGGL(prefill_state_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       stream, state, new_state, offsets, wsG, whi, wlo, wsu, kt, ht, vnt);
+                       stream, state, new_state, offsets, wsD, wsE, whi, wlo, wsu, kt, ht, vnt);
   if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
   if (L.nt_max > 0) {
     hipLaunchKernelGGL(prefill_output_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, q, k, chunks,

@@ -260,7 +260,8 @@ def _layout(T, N):
     take("chunks", nt * 16)
     take("offsets", (N + 1) * 4)
     take("G", nt * 8 * 64 * 4)
-    take("beta", nt * 8 * 64 * 4)
+    take("dcy", nt * 8 * 64 * 4)
+    take("eg", nt * 8 * 4)
     take("w_hi", nt * 8 * 64 * 128 * 2)
     take("w_lo", nt * 8 * 64 * 128 * 2)
     take("u", nt * 8 * 64 * 128 * 4)
