@@ -51,7 +51,7 @@ constexpr int kStrideA = 65;   // f32  [64][64]  tile
 // Workspace layout; every region starts on a 256-byte boundary.
 struct PrefillLayout {
   int nt_max;  // upper bound on the chunk count from (T, N) alone
-  size_t chunks, offsets, G, dcy, eg, w_hi, w_lo, u, kt, ht, vnt, total;
+  size_t chunks, offsets, G, dcy, eg, w, u, kt, ht, vnt, total;
 };
 
 static long long max_chunks(long long T, long long N) {
@@ -76,8 +76,7 @@ static PrefillLayout prefill_layout(int T, int N) {
   L.G = take(n * kHV * kChunk * 4);
   L.dcy = take(n * kHV * kChunk * 4);
   L.eg = take(n * kHV * 4);
-  L.w_hi = take(n * kHV * kChunk * kDK * 2);
-  L.w_lo = take(n * kHV * kChunk * kDK * 2);
+  L.w = take(n * kHV * kChunk * kDK * 4);  // hi and lo bf16
   L.u = take(n * kHV * kChunk * kDV * 4);
   L.kt = take(n * kHQK * kDK * kChunk * 2);
   L.ht = take(n * kHV * kDV * kDK * 2);
@@ -153,48 +152,93 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
   for (int c = nt + tid; c < nt_max; c += 1024) chunks[c] = make_int4(-1, 0, 0, 0);
 }
 
-// Index of an off-diagonal 16x16 block (p > q) of T in the sTo scratch.
-__device__ __forceinline__ int offdiag_slot(int p, int q) {
-  const int d = p - q;
-  return d == 1 ? q : (d == 2 ? 3 + q : 5);
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_16x16x16_bf16: A lane l holds A[l & 15][4*(l >> 4) + e], B lane l
+// holds B[4*(l >> 4) + e][l & 15] (e = 0..3), D as for the 16x16x32 form.  D's
+// rows 4*(l >> 4) + r are exactly B's k-rows, so a result tile feeds the next
+// product as its B operand without leaving the lane.
+__device__ __forceinline__ f32x4 mfma16_bf16(const u32x2 a, const u32x2 b, const f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                    __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+}
+
+// Split of four floats into (hi, lo) bf16 pairs for the K=16 MFMA.
+__device__ __forceinline__ void split4(const f32x4 x, u32x2 &hi, u32x2 &lo) {
+  uint32_t h0, h1, l0, l1;
+  split2(x[0], x[1], h0, l0);
+  split2(x[2], x[3], h1, l1);
+  hi = u32x2{h0, h1};
+  lo = u32x2{l0, l1};
+}
+
+// acc += A * B with both operands split (hi*hi + hi*lo + lo*hi).
+__device__ __forceinline__ f32x4 mfma16_x3(const u32x2 ah, const u32x2 al, const u32x2 bh,
+                                           const u32x2 bl, f32x4 acc) {
+  acc = mfma16_bf16(ah, bh, acc);
+  acc = mfma16_bf16(ah, bl, acc);
+  return mfma16_bf16(al, bh, acc);
+}
+
+// Transposed [*][64] bf16 tiles in LDS store each row's eight 8-token blocks
+// in XOR-swizzled order (block b of row n at slot b ^ ((n >> 3) & 7)), so the
+// 16-byte transposed writes of eight consecutive rows hit different banks.
+__device__ __forceinline__ int tsw(int row, int token) {
+  return row * kStrideT + ((((token >> 3) ^ (row >> 3)) & 7) << 3) + (token & 7);
 }
 
 // ---------------------------------------------------------------------------
 // 2. intra-chunk: per (chunk c = blockIdx.x, v-head h = blockIdx.y).
+//   * wave 0: gating, chunk-local cumsum G, decay factors.
+//   * every thread: one 8x8 block of K or V -> row-major K and transposed
+//     K^T / V^T in LDS (8x8 transposes in registers, 16-byte LDS writes).
+//   * A = strictly-lower(beta_i exp(G_i - G_j) K K^T) on MFMA.
+//   * the four 16x16 diagonal blocks of (I + A) inverted by forward
+//     substitution (wave w, block w).
+//   * u = (I + A)^-1 (beta V) and w = (I + A)^-1 (beta exp(G) K) by blocked
+//     forward substitution: wave w owns 64 right-hand-side columns (waves 0-1
+//     u, 2-3 w) and walks the four 16-row block rows,
+//       Y_i = D_i (X_i - sum_{j<i} A_ij Y_j),
+//     on split-bf16 MFMAs with every Y_j kept in registers.
+// Outputs go to the workspace in the exact fragment order the state kernel
+// reads: u as MFMA result tiles, w as hi/lo A-operand fragments, K^T as
+// A-operand fragments.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prefill_intra_kernel(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
     const int4 *__restrict__ chunks, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
-    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_whi, uint16_t *__restrict__ ws_wlo, float *__restrict__ ws_u,
+    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u,
     uint16_t *__restrict__ ws_kt) {
   const int c = blockIdx.x, h = blockIdx.y;
   const int4 ch = chunks[c];
   if (ch.x < 0) return;
   const int start = ch.y, len = ch.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r16 = lane & 15, kg = (lane >> 4) * 8;
+  const int r16 = lane & 15, g = lane >> 4, kg = g * 8;
   const int hq = h >> 1;
+  const size_t ch_head = static_cast<size_t>(c) * kHV + h;
 
-  __shared__ __align__(16) uint16_t sK[kChunk * kStrideK];
+  constexpr int kStrideA4 = 68;  // f32 stride of the 64x64 A tile (16-byte rows)
+  constexpr int kStrideD = 20;   // f32 stride of the 16x16 diagonal inverses
+  __shared__ __align__(16) uint16_t sK[kChunk * kStrideK];  // later: w transpose scratch
   __shared__ __align__(16) uint16_t sKt[kDK * kStrideT];
   __shared__ __align__(16) uint16_t sVt[kDV * kStrideT];
-  __shared__ __align__(16) float sA[kChunk * kStrideA];
-  __shared__ float sTo[6][16 * 17];
-  __shared__ float sM[4][16 * 17];
-  __shared__ float sG[kChunk], sBeta[kChunk], sBG[kChunk];
+  __shared__ __align__(16) float sA[kChunk * kStrideA4];     // later: w transpose scratch
+  __shared__ __align__(16) float sD[4 * 16 * kStrideD];
+  __shared__ __align__(16) float sBeta[kChunk], sBG[kChunk], sG[kChunk];
 
   // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding tokens
   // get g = 0 and beta = 0, so G stays at G_last past the end of the chunk.
   if (wave == 0) {
-    float g = 0.f, be = 0.f;
+    float gl = 0.f, be = 0.f;
     if (lane < len) {
       const size_t t = static_cast<size_t>(start) + lane;
-      g = gdn_log_decay(A_log[h], bf16_to_f32(a[t * kHV + h]), dt_bias[h]);
+      gl = gdn_log_decay(A_log[h], bf16_to_f32(a[t * kHV + h]), dt_bias[h]);
       be = sigmoidf_(bf16_to_f32(b[t * kHV + h]));
     }
-    float G = g;
+    float G = gl;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const float y = __shfl_up(G, off);
@@ -203,44 +247,49 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
     sG[lane] = G;
     sBeta[lane] = be;
     sBG[lane] = be * expf(G);
-    // Decay factors of the state update: exp(G_last - G_i) per row and
-    // exp(G_last) for the carried state (G_last = G of lane 63; padding
-    // tokens keep G at G_last).
     const float G_last = __shfl(G, 63);
-    const size_t gi = (static_cast<size_t>(c) * kHV + h) * kChunk + lane;
-    ws_G[gi] = G;
-    ws_dcy[gi] = expf(G_last - G);
-    if (lane == 0) ws_eg[static_cast<size_t>(c) * kHV + h] = expf(G_last);
+    ws_G[ch_head * kChunk + lane] = G;
+    ws_dcy[ch_head * kChunk + lane] = expf(G_last - G);
+    if (lane == 0) ws_eg[ch_head] = expf(G_last);
   }
 
-  // K (q/k head h/2) and V (head h) rows into LDS, zero past the chunk end;
-  // K row-major (for K K^T) and transposed (for w), V transposed (for u).
-  for (int idx = tid; idx < kChunk * 16; idx += 256) {
-    const int row = idx >> 4, c8 = (idx & 15) * 8;
-    u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-    if (row < len) {
-      const size_t t = static_cast<size_t>(start) + row;
-      kv = *reinterpret_cast<const u32x4 *>(k + (t * kHQK + hq) * kDK + c8);
-      vv = *reinterpret_cast<const u32x4 *>(v + (t * kHV + h) * kDV + c8);
-    }
-    *reinterpret_cast<u32x4 *>(&sK[row * kStrideK + c8]) = kv;
+  // One 8x8 block of K (threads 0..127) or V (128..255) per thread.
+  {
+    const bool isK = tid < 128;
+    const int blk = tid & 127, rb = blk >> 4, cb = blk & 15;
+    u32x4 rows[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      sKt[(c8 + e) * kStrideT + row] = static_cast<uint16_t>(kv[e >> 1] >> (16 * (e & 1)));
-      sVt[(c8 + e) * kStrideT + row] = static_cast<uint16_t>(vv[e >> 1] >> (16 * (e & 1)));
+    for (int i = 0; i < 8; ++i) {
+      const int row = rb * 8 + i;
+      rows[i] = u32x4{0u, 0u, 0u, 0u};
+      if (row < len) {
+        const size_t t = static_cast<size_t>(start) + row;
+        rows[i] = isK ? *reinterpret_cast<const u32x4 *>(k + (t * kHQK + hq) * kDK + cb * 8)
+                      : *reinterpret_cast<const u32x4 *>(v + (t * kHV + h) * kDV + cb * 8);
+      }
+      if (isK) *reinterpret_cast<u32x4 *>(&sK[row * kStrideK + cb * 8]) = rows[i];
+    }
+    uint16_t *dstT = isK ? sKt : sVt;
+    uint16_t *ktf = ws_kt + (static_cast<size_t>(c) * kHQK + hq) * (kDK * kChunk);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      // column j of the block = 8 tokens of feature cb*8 + j
+      u32x4 col;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t x0 = rows[2 * p][j >> 1], x1 = rows[2 * p + 1][j >> 1];
+        col[p] = (j & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
+      }
+      const int n = cb * 8 + j;
+      *reinterpret_cast<u32x4 *>(&dstT[tsw(n, rb * 8)]) = col;
+      // K^T as A-operand fragments of the state kernel: (mt, kk, lane) =
+      // (n / 16, rb / 4, (rb % 4) * 16 + n % 16), 8 tokens each.
+      if (isK && (h & 1) == 0)
+        *reinterpret_cast<u32x4 *>(
+            ktf + ((((n >> 4) * 2 + (rb >> 2)) * 64) + (rb & 3) * 16 + (n & 15)) * 8) = col;
     }
   }
   __syncthreads();
-
-  // K^T of this chunk for the state kernel, once per q/k head.
-  if ((h & 1) == 0) {
-    uint16_t *dst = ws_kt + (static_cast<size_t>(c) * kHQK + hq) * kDK * kChunk;
-    for (int idx = tid; idx < kDK * 8; idx += 256) {
-      const int key = idx >> 3, t8 = (idx & 7) * 8;
-      *reinterpret_cast<u32x4 *>(dst + key * kChunk + t8) =
-          *reinterpret_cast<const u32x4 *>(&sKt[key * kStrideT + t8]);
-    }
-  }
 
   // A = strictly-lower(beta_i exp(G_i - G_j) K K^T); wave w owns rows 16w..16w+15.
   {
@@ -255,120 +304,112 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 16 * mb + 4 * (lane >> 4) + r, j = 16 * nb + r16;
-        const float val = (i > j && i < len) ? sBeta[i] * expf(sG[i] - sG[j]) * acc[r] : 0.f;
-        sA[i * kStrideA + j] = val;
+        const int i = 16 * mb + 4 * g + r, j = 16 * nb + r16;
+        sA[i * kStrideA4 + j] = (i > j && i < len) ? sBeta[i] * expf(sG[i] - sG[j]) * acc[r] : 0.f;
       }
     }
   }
   __syncthreads();
 
-  // T = (I + A)^-1.  Diagonal 16x16 blocks: wave w, lane j < 16 solves column j
-  // of block w by forward substitution and overwrites A's diagonal block.
+  // Diagonal blocks D_w = (I + A_ww)^-1: wave w, lane j < 16 solves column j.
   if (lane < 16) {
     const int base = 16 * wave;
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      float sacc = (i == lane) ? 1.f : 0.f;
+      const float *arow = &sA[(base + i) * kStrideA4 + base];
+      float s0 = (i == lane) ? 1.f : 0.f, s1 = 0.f;
 #pragma unroll
-      for (int m = 0; m < i; ++m) sacc -= sA[(base + i) * kStrideA + base + m] * x[m];
-      x[i] = sacc;
+      for (int m = 0; m < i; m += 2) {
+        s0 -= arow[m] * x[m];
+        if (m + 1 < i) s1 -= arow[m + 1] * x[m + 1];
+      }
+      x[i] = s0 + s1;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sA[(base + i) * kStrideA + base + lane] = x[i];
+    for (int i = 0; i < 16; ++i) sD[(wave * 16 + i) * kStrideD + lane] = x[i];
   }
   __syncthreads();
 
-  // Off-diagonal blocks, nearest the diagonal first:
-  //   T_pq = -T_pp * sum_{r=q}^{p-1} A_pr T_rq      (p > q)
-  // wave w handles block (p, q) = (w + d, w) of distance d; lane -> column
-  // j = lane & 15 and rows 4*(lane >> 4) + 0..3.
-  for (int d = 1; d <= 3; ++d) {
-    if (wave < 4 - d) {
-      const int p = wave + d, q = wave;
-      const int j = lane & 15, i0 = 4 * (lane >> 4);
-      float m4[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int r = q; r < p; ++r) {
-        // T_rq: diagonal block (r == q) lives in sA, the others in sTo.
-        const float *trq = (r == q) ? &sA[(16 * r) * kStrideA + 16 * q] : &sTo[offdiag_slot(r, q)][0];
-        const int trq_stride = (r == q) ? kStrideA : 17;
-#pragma unroll
-        for (int mm = 0; mm < 16; ++mm) {
-          const float t = trq[mm * trq_stride + j];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) m4[e] += sA[(16 * p + i0 + e) * kStrideA + 16 * r + mm] * t;
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sM[wave][(i0 + e) * 17 + j] = m4[e];
-      __builtin_amdgcn_wave_barrier();
-      float t4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int mm = 0; mm < 16; ++mm) {
-        const float mv = sM[wave][mm * 17 + j];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) t4[e] -= sA[(16 * p + i0 + e) * kStrideA + 16 * p + mm] * mv;
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sTo[offdiag_slot(p, q)][(i0 + e) * 17 + j] = t4[e];
-    }
-    __syncthreads();
-  }
-
-  // Assemble the full T in sA: off-diagonal blocks from sTo, zeros above.
-  for (int idx = tid; idx < kChunk * kChunk; idx += 256) {
-    const int i = idx >> 6, j = idx & 63, p = i >> 4, q = j >> 4;
-    if (q > p) sA[i * kStrideA + j] = 0.f;
-    else if (q < p) sA[i * kStrideA + j] = sTo[offdiag_slot(p, q)][(i & 15) * 17 + (j & 15)];
-  }
-  __syncthreads();
-
-  // u = T (beta * V), w = T (beta exp(G) * K), split-bf16 products (3 MFMAs
-  // each); wave w owns rows 16w..16w+15 and all 128 columns.
+  // Blocked forward substitution over 64 right-hand-side columns per wave.
   {
-    const int mb = wave;
-    u32x4 th[2], tl[2];
+    const bool isU = wave < 2;
+    const int col0 = (wave & 1) * 64;            // first V (or K) column of this wave
+    const uint16_t *Xt = isU ? sVt : sKt;         // X^T rows = features
+    const float *scl = isU ? sBeta : sBG;
+    f32x4 Y[4][4];                                // [block row][column tile]
+    u32x2 Yh[4][4], Yl[4][4];                     // their hi/lo splits (B operands)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      float x[8];
+    for (int i = 0; i < 4; ++i) {
+      // Z = X_i - sum_{j<i} A_ij Y_j
+      const f32x4 s4 = *reinterpret_cast<const f32x4 *>(&scl[16 * i + 4 * g]);
+      f32x4 Z[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = sA[(16 * mb + r16) * kStrideA + 32 * kk + kg + e];
-      split8(x, th[kk], tl[kk]);
+      for (int nt = 0; nt < 4; ++nt) {
+        const int n = col0 + 16 * nt + r16;
+        const u32x2 x2 = *reinterpret_cast<const u32x2 *>(&Xt[tsw(n, 16 * i + 4 * g)]);
+        Z[nt] = f32x4{s4[0] * __uint_as_float(x2[0] << 16),
+                      s4[1] * __uint_as_float(x2[0] & 0xffff0000u),
+                      s4[2] * __uint_as_float(x2[1] << 16),
+                      s4[3] * __uint_as_float(x2[1] & 0xffff0000u)};
+      }
+#pragma unroll
+      for (int j = 0; j < i; ++j) {
+        const f32x4 la = *reinterpret_cast<const f32x4 *>(&sA[(16 * i + r16) * kStrideA4 + 16 * j + 4 * g]);
+        u32x2 lh, ll;
+        split4(-la, lh, ll);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) Z[nt] = mfma16_x3(lh, ll, Yh[j][nt], Yl[j][nt], Z[nt]);
+      }
+      // Y_i = D_i Z
+      const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&sD[(i * 16 + r16) * kStrideD + 4 * g]);
+      u32x2 dh, dl;
+      split4(d4, dh, dl);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        u32x2 zh, zl;
+        split4(Z[nt], zh, zl);
+        Y[i][nt] = mfma16_x3(dh, dl, zh, zl, f32x4{0.f, 0.f, 0.f, 0.f});
+        split4(Y[i][nt], Yh[i][nt], Yl[i][nt]);
+      }
     }
-    const size_t row_base = (static_cast<size_t>(c) * kHV + h) * kChunk;
-    for (int nb = 0; nb < 8; ++nb) {
-      f32x4 au = {0.f, 0.f, 0.f, 0.f}, aw = {0.f, 0.f, 0.f, 0.f};
+
+    if (isU) {
+      // u tiles in MFMA result order: [chunk][head][row tile][col tile][lane][4]
+      float *ut = ws_u + ch_head * (kChunk * kDV);
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const int j0 = 32 * kk + kg;
-        float fv[8], fk[8];
-        unpack8(*reinterpret_cast<const u32x4 *>(&sVt[(16 * nb + r16) * kStrideT + j0]), fv);
-        unpack8(*reinterpret_cast<const u32x4 *>(&sKt[(16 * nb + r16) * kStrideT + j0]), fk);
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          fv[e] *= sBeta[j0 + e];
-          fk[e] *= sBG[j0 + e];
+        for (int nt = 0; nt < 4; ++nt)
+          *reinterpret_cast<f32x4 *>(ut + ((i * 8 + (col0 >> 4) + nt) * 64 + lane) * 4) = Y[i][nt];
+    }
+    __syncthreads();  // sK and sA are free from here on: w transpose scratch
+
+    if (!isU) {
+      // w: through LDS to A-operand fragments (row 16*mb + r16, 8 consecutive
+      // k), split hi/lo: [chunk][head][mb][kk][lane][hi 8 | lo 8].
+      float *scr = (wave == 2) ? reinterpret_cast<float *>(sK) : sA;  // [64][68]
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) scr[(16 * i + 4 * g + r) * kStrideA4 + 16 * nt + r16] = Y[i][nt][r];
+      uint16_t *wf = ws_w + ch_head * (kChunk * kDK * 2);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int kk2 = 0; kk2 < 2; ++kk2) {
+          const f32x4 x0 = *reinterpret_cast<const f32x4 *>(&scr[(16 * mb + r16) * kStrideA4 + 32 * kk2 + kg]);
+          const f32x4 x1 = *reinterpret_cast<const f32x4 *>(&scr[(16 * mb + r16) * kStrideA4 + 32 * kk2 + kg + 4]);
+          const float x8[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+          u32x4 hi, lo;
+          split8(x8, hi, lo);
+          const int kk = 2 * (wave - 2) + kk2;
+          uint16_t *dst = wf + ((mb * 4 + kk) * 64 + lane) * 16;
+          *reinterpret_cast<u32x4 *>(dst) = hi;
+          *reinterpret_cast<u32x4 *>(dst + 8) = lo;
         }
-        u32x4 vh, vl, kh, kl;
-        split8(fv, vh, vl);
-        split8(fk, kh, kl);
-        au = mfma_bf16(th[kk], vh, au);
-        au = mfma_bf16(th[kk], vl, au);
-        au = mfma_bf16(tl[kk], vh, au);
-        aw = mfma_bf16(th[kk], kh, aw);
-        aw = mfma_bf16(th[kk], kl, aw);
-        aw = mfma_bf16(tl[kk], kh, aw);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * mb + 4 * (lane >> 4) + r, n = 16 * nb + r16;
-        const size_t o = (row_base + i) * kDV + n;
-        ws_u[o] = au[r];
-        const uint32_t hb = __float_as_uint(aw[r]) & 0xffff0000u;
-        ws_whi[o] = static_cast<uint16_t>(hb >> 16);
-        ws_wlo[o] = f32_to_bf16(aw[r] - __uint_as_float(hb));
-      }
     }
   }
 }
@@ -397,30 +438,33 @@ struct ChunkFrag {
 template <int NTT>
 __device__ __forceinline__ void load_chunk_frag(ChunkFrag<NTT> &f, int c, int h, int v0, int wave,
                                                 int lane, const float *ws_dcy, const float *ws_eg,
-                                                const uint16_t *ws_whi, const uint16_t *ws_wlo,
-                                                const float *ws_u, const uint16_t *ws_kt) {
-  const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
+                                                const uint16_t *ws_w, const float *ws_u,
+                                                const uint16_t *ws_kt) {
+  const int q4 = 4 * (lane >> 4);
   const size_t ch_head = static_cast<size_t>(c) * kHV + h;
-  const uint16_t *whi = ws_whi + ch_head * (kChunk * kDK);
-  const uint16_t *wlo = ws_wlo + ch_head * (kChunk * kDK);
-  const int woff = (16 * wave + r16) * kDK + kg;
+  // w: [mb][kk][lane][hi 8 | lo 8] fragments of this wave's 16 rows
+  const uint16_t *wf = ws_w + ch_head * (kChunk * kDK * 2) + (wave * 4) * (64 * 16);
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
-    f.wh[kk] = *reinterpret_cast<const u32x4 *>(whi + woff + 32 * kk);
-    f.wl[kk] = *reinterpret_cast<const u32x4 *>(wlo + woff + 32 * kk);
+    f.wh[kk] = *reinterpret_cast<const u32x4 *>(wf + (kk * 64 + lane) * 16);
+    f.wl[kk] = *reinterpret_cast<const u32x4 *>(wf + (kk * 64 + lane) * 16 + 8);
   }
+  // K^T: [mt][kk][lane][8] fragments of this wave's two 16-row tiles
   const uint16_t *kt = ws_kt + (static_cast<size_t>(c) * kHQK + (h >> 1)) * (kDK * kChunk);
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
       f.ka[mi][kk] = *reinterpret_cast<const u32x4 *>(
-          kt + (16 * (2 * wave + mi) + r16) * kChunk + 32 * kk + kg);
-  const float *u = ws_u + ch_head * (kChunk * kDV);
+          kt + ((((2 * wave + mi) * 2 + kk) * 64) + lane) * 8);
+  // u: [row tile][col tile][lane][4] result tiles
+  const float *ut = ws_u + ch_head * (kChunk * kDV);
 #pragma unroll
-  for (int nt = 0; nt < NTT; ++nt)
+  for (int nt = 0; nt < NTT; ++nt) {
+    const f32x4 x = *reinterpret_cast<const f32x4 *>(ut + ((wave * 8 + (v0 >> 4) + nt) * 64 + lane) * 4);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) f.u[nt][r] = u[(16 * wave + q4 + r) * kDV + v0 + 16 * nt + r16];
+    for (int r = 0; r < 4; ++r) f.u[nt][r] = x[r];
+  }
   f.dcy = *reinterpret_cast<const f32x4 *>(ws_dcy + ch_head * kChunk + 16 * wave + q4);
   f.eg = ws_eg[ch_head];
 }
@@ -428,7 +472,7 @@ __device__ __forceinline__ void load_chunk_frag(ChunkFrag<NTT> &f, int c, int h,
 template <int BV>
 __global__ __launch_bounds__(256) void prefill_state_kernel(
     const float *state, float *new_state, const int *offsets, const float *ws_dcy,
-    const float *ws_eg, const uint16_t *ws_whi, const uint16_t *ws_wlo, const float *ws_u,
+    const float *ws_eg, const uint16_t *ws_w, const float *ws_u,
     const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt) {
   constexpr int NVB = kDV / BV;
   constexpr int NTT = BV / 16;
@@ -549,7 +593,8 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
   };
 
   // Ring of three fragment sets: chunk i uses set i % 3 while the sets of
-  // chunks i + 1 and i + 2 are in flight.  Prefetches past the last chunk
+  // chunks i + 1 and i + 2 are in flight (the loop header sits where all three
+  // sets are pending, on entry and on the back edge alike).  Prefetches past the last chunk
   // re-read the last chunk, so every iteration issues the same loads and the
   // compiler can wait for exactly the set in use (a conditional load would
   // make it wait for all outstanding loads).  The workspace pointers carry no
@@ -558,17 +603,19 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
   if (nch > 0) {
     auto chunk_at = [&](int i) { return c0 + (i < nch ? i : nch - 1); };
     ChunkFrag<NTT> fa, fb, fc;
-    load_chunk_frag(fa, chunk_at(0), h, v0, wave, lane, ws_dcy, ws_eg, ws_whi, ws_wlo, ws_u, ws_kt);
-    load_chunk_frag(fb, chunk_at(1), h, v0, wave, lane, ws_dcy, ws_eg, ws_whi, ws_wlo, ws_u, ws_kt);
-    for (int ci = 0; ci < nch; ci += 3) {
-      load_chunk_frag(fc, chunk_at(ci + 2), h, v0, wave, lane, ws_dcy, ws_eg, ws_whi, ws_wlo, ws_u, ws_kt);
+    load_chunk_frag(fa, chunk_at(0), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
+    load_chunk_frag(fb, chunk_at(1), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
+    load_chunk_frag(fc, chunk_at(2), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
+    for (int ci = 0;; ci += 3) {
       step(fa, c0 + ci);
       if (ci + 1 >= nch) break;
-      load_chunk_frag(fa, chunk_at(ci + 3), h, v0, wave, lane, ws_dcy, ws_eg, ws_whi, ws_wlo, ws_u, ws_kt);
+      load_chunk_frag(fa, chunk_at(ci + 3), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
       step(fb, c0 + ci + 1);
       if (ci + 2 >= nch) break;
-      load_chunk_frag(fb, chunk_at(ci + 4), h, v0, wave, lane, ws_dcy, ws_eg, ws_whi, ws_wlo, ws_u, ws_kt);
+      load_chunk_frag(fb, chunk_at(ci + 4), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
       step(fc, c0 + ci + 2);
+      if (ci + 3 >= nch) break;
+      load_chunk_frag(fc, chunk_at(ci + 5), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
     }
   }
 
@@ -739,8 +786,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   float *wsG = reinterpret_cast<float *>(ws + L.G);
   float *wsD = reinterpret_cast<float *>(ws + L.dcy);
   float *wsE = reinterpret_cast<float *>(ws + L.eg);
-  uint16_t *whi = reinterpret_cast<uint16_t *>(ws + L.w_hi);
-  uint16_t *wlo = reinterpret_cast<uint16_t *>(ws + L.w_lo);
+  uint16_t *wsw = reinterpret_cast<uint16_t *>(ws + L.w);
   float *wsu = reinterpret_cast<float *>(ws + L.u);
   uint16_t *kt = reinterpret_cast<uint16_t *>(ws + L.kt);
   uint16_t *ht = reinterpret_cast<uint16_t *>(ws + L.ht);
@@ -752,7 +798,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   if (rc) return rc;
   if (L.nt_max > 0) {
     hipLaunchKernelGGL(prefill_intra_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, k, v, A_log,
-                       a, dt_bias, b, chunks, wsG, wsD, wsE, whi, wlo, wsu, kt);
+                       a, dt_bias, b, chunks, wsG, wsD, wsE, wsw, wsu, kt);
     if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
   }
   const int bv = variant == 1 ? 32 : (variant == 0 ? 16 : (N * kHV * (kDV / 32) >= 512 ? 32 : 16));
@@ -760,10 +806,10 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
   if (bv == 32)
     hipLaunchKernelGGL(prefill_state_kernel<32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       stream, state, new_state, offsets, wsD, wsE, whi, wlo, wsu, kt, ht, vnt);
+                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt);
   else
     hipLaunchKernelGGL(prefill_state_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       stream, state, new_state, offsets, wsD, wsE, whi, wlo, wsu, kt, ht, vnt);
+                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt);
   if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
   if (L.nt_max > 0) {
     hipLaunchKernelGGL(prefill_output_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, q, k, chunks,

@@ -262,8 +262,7 @@ def _layout(T, N):
     take("G", nt * 8 * 64 * 4)
     take("dcy", nt * 8 * 64 * 4)
     take("eg", nt * 8 * 4)
-    take("w_hi", nt * 8 * 64 * 128 * 2)
-    take("w_lo", nt * 8 * 64 * 128 * 2)
+    take("w", nt * 8 * 64 * 128 * 4)
     take("u", nt * 8 * 64 * 128 * 4)
     take("kt", nt * 4 * 128 * 64 * 2)
     take("ht", nt * 8 * 128 * 128 * 2)
@@ -300,10 +299,17 @@ def test_prefill_stage_intermediates(cuda_device):
     for c in range(nt):
         C = min(64, lens[seq[c]] - 64 * local[c])
         assert np.allclose(G[c, :, :C], it["g_cs"][c, :, :C], rtol=1e-5, atol=1e-5)
-    u = arr("u", np.float32, (L["nt"], 8, 64, 128))[:nt]
+    # u: MFMA result tiles [c][h][row tile i][col tile n][lane][r] holding
+    # u[16i + 4(lane >> 4) + r][16n + (lane & 15)]
+    ut = arr("u", np.float32, (L["nt"], 8, 4, 8, 4, 16, 4))[:nt]  # lane = (g, r16)
+    u = ut.transpose(0, 1, 2, 4, 6, 3, 5).reshape(nt, 8, 64, 128)
     assert np.abs(u - it["u"]).max() <= 1e-4 * np.abs(it["u"]).max()
-    w = (O.bf16_from_bits(arr("w_hi", np.uint16, (L["nt"], 8, 64, 128))[:nt]).astype(np.float64)
-         + O.bf16_from_bits(arr("w_lo", np.uint16, (L["nt"], 8, 64, 128))[:nt]))
+    # w: A fragments [c][h][mb][kk][lane][hi 8 | lo 8] holding
+    # w[16mb + (lane & 15)][32kk + 8(lane >> 4) + e]
+    wf = arr("w", np.uint16, (L["nt"], 8, 4, 4, 4, 16, 2, 8))[:nt]  # lane = (g, r16)
+    wv = (O.bf16_from_bits(wf[..., 0, :]).astype(np.float64)
+          + O.bf16_from_bits(wf[..., 1, :]))                       # [c,h,mb,kk,g,r16,e]
+    w = wv.transpose(0, 1, 2, 5, 3, 4, 6).reshape(nt, 8, 64, 128)
     assert np.abs(w - it["w"]).max() <= 1e-4 * np.abs(it["w"]).max()
     ht = O.bf16_from_bits(arr("ht", np.uint16, (L["nt"], 8, 128, 128))[:nt])
     assert np.abs(ht - it["h"].transpose(0, 1, 3, 2)).max() <= 1e-2 * np.abs(it["h"]).max()
