@@ -182,6 +182,9 @@ def main():
     ap.add_argument("--sweep", action="store_true",
                     help="also time every decode batch size of configs[1] and every tiling")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 64 MiB device copy 10 times (the known-size "
+                         "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -194,6 +197,15 @@ def main():
     from oracle import gdn_oracle as O
 
     dev = torch.device("cuda", 0)
+    if args.calibrate_copy:
+        nbytes = 64 << 20
+        src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": nbytes, "copies": 10}), flush=True)
+        return
     log(f"device: {torch.cuda.get_device_name(dev)}")
     B = args.batch
 
