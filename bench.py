@@ -153,6 +153,19 @@ def bench_prefill(lens, steps, warmup, dev, variant=-1):
     return ms_eager, ms_graph
 
 
+def measured_traffic(path=os.path.join(ROOT, "profiles", "decode_b64_hbm_traffic.md")):
+    """HBM bytes per decode launch at B=64 from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of known size);
+    None when the summary is absent."""
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline_decode(B, seconds):
     """The reference's decode loop nest restated in numpy (oracle decode_loop),
     one thread, repeated until `seconds` of CPU time have passed."""
@@ -273,7 +286,8 @@ def main():
                              "bytes_per_call": O.prefill_bytes(T8, len(pre_lens))},
         "roofline": {"bound": "hbm", "achieved": round(gbs_step, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(gbs_step / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "kernel": "gdn::decode_kernel",
+                     "traffic": measured_traffic() if (B == 64 and args.variant == -1) else None,
+                     "kernel": "gdn::decode_kernel",
                      "bytes_per_launch": nbytes},
         "cpu_baseline": {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
                          "sample": f"{reps} decode steps at B={B} "
