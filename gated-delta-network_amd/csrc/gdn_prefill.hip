@@ -420,23 +420,24 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
 // the same XCD (workgroups are dealt round-robin over the 8 XCDs), so the
 // per-head w and K^T stream through one L2.
 // The state tile S[:, v0:v0+BV] ([K=128] x [BV], f32) lives in MFMA
-// accumulators: wave w owns K-rows 32w..32w+31 (two 16-row tiles) for all
-// BV/16 column tiles.  Everything a chunk needs that does not depend on the
+// accumulators.  The workgroup has 4 waves per 16-column tile: wave w owns
+// column tile w / 4 and, in it, K-rows 32*(w % 4)..+31 (two 16-row tiles) of
+// the state and v_new rows 16*(w % 4)..+15.  Teams of different column tiles
+// only share the barriers, so with BV = 32 two independent chains share each
+// SIMD and hide each other's latency.  Everything a chunk needs that does not depend on the
 // state (w, K^T, u, decay factors) is register-prefetched two chunks ahead,
 // so the serial chain per chunk is two LDS exchanges, two barriers and the
 // MFMAs.  Addresses are a per-chunk scalar base plus a 32-bit lane offset.
 // ---------------------------------------------------------------------------
-template <int NTT>
 struct ChunkFrag {
   u32x4 wh[4], wl[4];  // w rows 16*wave + (lane & 15), k-steps 0..3 (hi / lo)
   u32x4 ka[2][2];      // K^T rows 16*(2*wave + mi) + (lane & 15), k-steps 0..1
-  float u[NTT][4];     // u[16*wave + 4*(lane >> 4) + r][v0 + 16*nt + (lane & 15)]
+  f32x4 u;             // u[16*rw + 4*(lane >> 4) + r][vw + (lane & 15)]
   f32x4 dcy;           // exp(G_last - G_i) of the lane's four v_new rows
   float eg;            // exp(G_last)
 };
 
-template <int NTT>
-__device__ __forceinline__ void load_chunk_frag(ChunkFrag<NTT> &f, int c, int h, int v0, int wave,
+__device__ __forceinline__ void load_chunk_frag(ChunkFrag &f, int c, int h, int vw, int wave,
                                                 int lane, const float *ws_dcy, const float *ws_eg,
                                                 const uint16_t *ws_w, const float *ws_u,
                                                 const uint16_t *ws_kt) {
@@ -459,29 +460,25 @@ __device__ __forceinline__ void load_chunk_frag(ChunkFrag<NTT> &f, int c, int h,
           kt + ((((2 * wave + mi) * 2 + kk) * 64) + lane) * 8);
   // u: [row tile][col tile][lane][4] result tiles
   const float *ut = ws_u + ch_head * (kChunk * kDV);
-#pragma unroll
-  for (int nt = 0; nt < NTT; ++nt) {
-    const f32x4 x = *reinterpret_cast<const f32x4 *>(ut + ((wave * 8 + (v0 >> 4) + nt) * 64 + lane) * 4);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) f.u[nt][r] = x[r];
-  }
+  f.u = *reinterpret_cast<const f32x4 *>(ut + ((wave * 8 + (vw >> 4)) * 64 + lane) * 4);
   f.dcy = *reinterpret_cast<const f32x4 *>(ws_dcy + ch_head * kChunk + 16 * wave + q4);
   f.eg = ws_eg[ch_head];
 }
 
 template <int BV>
-__global__ __launch_bounds__(256) void prefill_state_kernel(
+__global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
     const float *state, float *new_state, const int *offsets, const float *ws_dcy,
     const float *ws_eg, const uint16_t *ws_w, const float *ws_u,
     const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt) {
   constexpr int NVB = kDV / BV;
-  constexpr int NTT = BV / 16;
   const int h = blockIdx.x % kHV;
   const int rest = blockIdx.x / kHV;
   const int vb = rest % NVB, s = rest / NVB;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = (tid >> 6) & 3, ct = tid >> 8;  // row group, column tile
   const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
-  const int v0 = vb * BV;
+  const int lc = 16 * ct;                          // column tile offset in the block
+  const int vw = vb * BV + lc;                     // first state column of this wave
 
   __shared__ __align__(16) uint16_t sSh[BV * kStrideK];
   __shared__ __align__(16) uint16_t sSl[BV * kStrideK];
@@ -492,70 +489,57 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
   const int nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
   const size_t sbase = (static_cast<size_t>(s) * kHV + h) * kDV * kDK;  // [V][K]
 
-  f32x4 S[2][NTT];
+  f32x4 S[2];
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int nt = 0; nt < NTT; ++nt) {
-      const int kr = 16 * (2 * wave + mi) + q4, vc = v0 + 16 * nt + r16;
-      if (state != nullptr && nch > 0)
-        S[mi][nt] = *reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + kr);
-      else
-        S[mi][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+  for (int mi = 0; mi < 2; ++mi) {
+    const int kr = 16 * (2 * wave + mi) + q4, vc = vw + r16;
+    if (state != nullptr && nch > 0)
+      S[mi] = *reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + kr);
+    else
+      S[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   // One chunk of the recurrence, from the prefetched fragments f.
-  auto step = [&](const ChunkFrag<NTT> &f, int c) {
+  auto step = [&](const ChunkFrag &f, int c) {
     const size_t ch_head = static_cast<size_t>(c) * kHV + h;
     uint16_t *ht = ws_ht + ch_head * (kDV * kDK);
     uint16_t *vnt = ws_vnt + ch_head * (kDV * kChunk);
     // (a) chunk-start state: split copy into LDS ([v][k]) for w S, and a bf16
     //     copy ([v][k]) for the output kernel.
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-      for (int nt = 0; nt < NTT; ++nt) {
-        const int kr = 16 * (2 * wave + mi) + q4, vl = 16 * nt + r16;
-        uint32_t h0, h1, l0, l1;
-        split2(S[mi][nt][0], S[mi][nt][1], h0, l0);
-        split2(S[mi][nt][2], S[mi][nt][3], h1, l1);
-        const u32x2 hi = {h0, h1}, lo = {l0, l1};
-        const u32x2 rn = {pk_bf16(S[mi][nt][0], S[mi][nt][1]), pk_bf16(S[mi][nt][2], S[mi][nt][3])};
-        *reinterpret_cast<u32x2 *>(&sSh[vl * kStrideK + kr]) = hi;
-        *reinterpret_cast<u32x2 *>(&sSl[vl * kStrideK + kr]) = lo;
-        *reinterpret_cast<u32x2 *>(ht + (v0 + vl) * kDK + kr) = rn;
-      }
+    for (int mi = 0; mi < 2; ++mi) {
+      const int kr = 16 * (2 * wave + mi) + q4, vl = lc + r16;
+      uint32_t h0, h1, l0, l1;
+      split2(S[mi][0], S[mi][1], h0, l0);
+      split2(S[mi][2], S[mi][3], h1, l1);
+      const u32x2 hi = {h0, h1}, lo = {l0, l1};
+      const u32x2 rn = {pk_bf16(S[mi][0], S[mi][1]), pk_bf16(S[mi][2], S[mi][3])};
+      *reinterpret_cast<u32x2 *>(&sSh[vl * kStrideK + kr]) = hi;
+      *reinterpret_cast<u32x2 *>(&sSl[vl * kStrideK + kr]) = lo;
+      *reinterpret_cast<u32x2 *>(ht + (vw + r16) * kDK + kr) = rn;
+    }
     __syncthreads();
 
     // (b) w S for rows 16*wave..+15; three independent accumulation chains
     //     (hi*hi, hi*lo, lo*hi) shorten the dependent MFMA sequence.
-    f32x4 P0[NTT], P1[NTT], P2[NTT];
+    f32x4 P0 = {0.f, 0.f, 0.f, 0.f}, P1 = P0, P2 = P0;
 #pragma unroll
-    for (int nt = 0; nt < NTT; ++nt) {
-      P0[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      P1[nt] = P0[nt];
-      P2[nt] = P0[nt];
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 sh = *reinterpret_cast<const u32x4 *>(&sSh[(lc + r16) * kStrideK + 32 * kk + kg]);
+      const u32x4 sl = *reinterpret_cast<const u32x4 *>(&sSl[(lc + r16) * kStrideK + 32 * kk + kg]);
+      P0 = mfma_bf16(f.wh[kk], sh, P0);
+      P1 = mfma_bf16(f.wh[kk], sl, P1);
+      P2 = mfma_bf16(f.wl[kk], sh, P2);
     }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-      for (int nt = 0; nt < NTT; ++nt) {
-        const u32x4 sh = *reinterpret_cast<const u32x4 *>(&sSh[(16 * nt + r16) * kStrideK + 32 * kk + kg]);
-        const u32x4 sl = *reinterpret_cast<const u32x4 *>(&sSl[(16 * nt + r16) * kStrideK + 32 * kk + kg]);
-        P0[nt] = mfma_bf16(f.wh[kk], sh, P0[nt]);
-        P1[nt] = mfma_bf16(f.wh[kk], sl, P1[nt]);
-        P2[nt] = mfma_bf16(f.wl[kk], sh, P2[nt]);
-      }
 
     // (c) v_new = u - w S -> workspace (bf16, [v][token]) for the output
     //     kernel; exp(G_last - G_i) v_new -> LDS (split, [v][token]) for K^T v.
-#pragma unroll
-    for (int nt = 0; nt < NTT; ++nt) {
-      const int vl = 16 * nt + r16;
+    {
+      const int vl = lc + r16;
       float vn[4], vs[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        vn[r] = f.u[nt][r] - ((P0[nt][r] + P1[nt][r]) + P2[nt][r]);
+        vn[r] = f.u[r] - ((P0[r] + P1[r]) + P2[r]);
         vs[r] = f.dcy[r] * vn[r];
       }
       const u32x2 rn = {pk_bf16(vn[0], vn[1]), pk_bf16(vn[2], vn[3])};
@@ -564,7 +548,7 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
       split2(vs[2], vs[3], h1, l1);
       const u32x2 hi = {h0, h1}, lo = {l0, l1};
       const int i0 = 16 * wave + q4;
-      *reinterpret_cast<u32x2 *>(vnt + (v0 + vl) * kChunk + i0) = rn;
+      *reinterpret_cast<u32x2 *>(vnt + (vw + r16) * kChunk + i0) = rn;
       *reinterpret_cast<u32x2 *>(&sVh[vl * kStrideT + i0]) = hi;
       *reinterpret_cast<u32x2 *>(&sVl[vl * kStrideT + i0]) = lo;
     }
@@ -573,28 +557,27 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
     // (d) S <- exp(G_last) S + K^T (exp(G_last - G) v_new); K is exact in bf16,
     //     so two MFMAs (hi, lo) per k-step, in two independent chains.
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < 2; ++mi) {
+      f32x4 acc = S[mi];
 #pragma unroll
-      for (int nt = 0; nt < NTT; ++nt) {
-        f32x4 acc = S[mi][nt];
+      for (int r = 0; r < 4; ++r) acc[r] *= f.eg;
+      f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] *= f.eg;
-        f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const u32x4 vh = *reinterpret_cast<const u32x4 *>(&sVh[(16 * nt + r16) * kStrideT + 32 * kk + kg]);
-          const u32x4 vl = *reinterpret_cast<const u32x4 *>(&sVl[(16 * nt + r16) * kStrideT + 32 * kk + kg]);
-          acc = mfma_bf16(f.ka[mi][kk], vh, acc);
-          acc2 = mfma_bf16(f.ka[mi][kk], vl, acc2);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) S[mi][nt][r] = acc[r] + acc2[r];
+      for (int kk = 0; kk < 2; ++kk) {
+        const u32x4 vh = *reinterpret_cast<const u32x4 *>(&sVh[(lc + r16) * kStrideT + 32 * kk + kg]);
+        const u32x4 vl = *reinterpret_cast<const u32x4 *>(&sVl[(lc + r16) * kStrideT + 32 * kk + kg]);
+        acc = mfma_bf16(f.ka[mi][kk], vh, acc);
+        acc2 = mfma_bf16(f.ka[mi][kk], vl, acc2);
       }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[mi][r] = acc[r] + acc2[r];
+    }
   };
 
   // Ring of three fragment sets: chunk i uses set i % 3 while the sets of
   // chunks i + 1 and i + 2 are in flight (the loop header sits where all three
-  // sets are pending, on entry and on the back edge alike).  Prefetches past the last chunk
+  // sets are pending, on entry and on the back edge alike).  (A fourth set
+  // measured slower: the extra registers push accumulators into AGPRs.)  Prefetches past the last chunk
   // re-read the last chunk, so every iteration issues the same loads and the
   // compiler can wait for exactly the set in use (a conditional load would
   // make it wait for all outstanding loads).  The workspace pointers carry no
@@ -602,31 +585,32 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
   // to their first use.
   if (nch > 0) {
     auto chunk_at = [&](int i) { return c0 + (i < nch ? i : nch - 1); };
-    ChunkFrag<NTT> fa, fb, fc;
-    load_chunk_frag(fa, chunk_at(0), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
-    load_chunk_frag(fb, chunk_at(1), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
-    load_chunk_frag(fc, chunk_at(2), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
+    ChunkFrag fa, fb, fc;
+#define GDN_LOAD(F, I) \
+    load_chunk_frag(F, chunk_at(I), h, vw, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt)
+    GDN_LOAD(fa, 0);
+    GDN_LOAD(fb, 1);
+    GDN_LOAD(fc, 2);
     for (int ci = 0;; ci += 3) {
       step(fa, c0 + ci);
       if (ci + 1 >= nch) break;
-      load_chunk_frag(fa, chunk_at(ci + 3), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
+      GDN_LOAD(fa, ci + 3);
       step(fb, c0 + ci + 1);
       if (ci + 2 >= nch) break;
-      load_chunk_frag(fb, chunk_at(ci + 4), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
+      GDN_LOAD(fb, ci + 4);
       step(fc, c0 + ci + 2);
       if (ci + 3 >= nch) break;
-      load_chunk_frag(fc, chunk_at(ci + 5), h, v0, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
+      GDN_LOAD(fc, ci + 5);
     }
+#undef GDN_LOAD
   }
 
   // Final state (zeros for a zero-length sequence, as the reference).
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int nt = 0; nt < NTT; ++nt) {
-      const int kr = 16 * (2 * wave + mi) + q4, vc = v0 + 16 * nt + r16;
-      *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + kr) = S[mi][nt];
-    }
+  for (int mi = 0; mi < 2; ++mi) {
+    const int kr = 16 * (2 * wave + mi) + q4, vc = vw + r16;
+    *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + kr) = S[mi];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -801,11 +785,11 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
                        a, dt_bias, b, chunks, wsG, wsD, wsE, wsw, wsu, kt);
     if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
   }
-  const int bv = variant == 1 ? 32 : (variant == 0 ? 16 : (N * kHV * (kDV / 32) >= 512 ? 32 : 16));
+  const int bv = variant == 1 ? 32 : 16;  // 16 measured faster at every size
   const long long blocks = static_cast<long long>(N) * kHV * (kDV / bv);
   if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
   if (bv == 32)
-    hipLaunchKernelGGL(prefill_state_kernel<32>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+    hipLaunchKernelGGL(prefill_state_kernel<32>, dim3(static_cast<unsigned>(blocks)), dim3(512), 0,
                        stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt);
   else
     hipLaunchKernelGGL(prefill_state_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,

@@ -115,12 +115,12 @@ int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
 
 /*
  * gdn_prefill_fwd with an explicit tiling of the serial state recurrence:
- * variant 0 = 16-column V blocks (8 workgroups per sequence and head),
- * 1 = 32-column blocks (4 per sequence and head), -1 = the built-in choice
- * (what gdn_prefill_fwd uses).  The counterpart of the reference's autotuned
+ * variant 0 = 16-column V blocks (8 workgroups of 4 waves per sequence and
+ * head), 1 = 32-column blocks (4 workgroups of 8 waves: two 16-column teams
+ * sharing each SIMD), -1 = the built-in choice (what gdn_prefill_fwd uses).  The counterpart of the reference's autotuned
  * BV of chunk_gated_delta_rule_fwd_kernel_h (solutions/
  * gdn_prefill_qk4_v8_d128_k_last/solution/triton/fla_kernels.py:407-426,
- * 1028-1035).  Results agree to rounding for every variant.
+ * 1028-1035).  Results are identical for every variant.
  */
 int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                             const float *state, const float *A_log, const gdn_bf16 *a,
