@@ -153,6 +153,38 @@ def bench_prefill(lens, steps, warmup, dev, variant=-1):
     return ms_eager, ms_graph
 
 
+def bench_prefill_clone(lens, reps, dev):
+    """FlashInfer-Bench's clone mode (OPTIMIZATION_LOG.md:263-300): before each
+    timed call every argument is cloned into fresh memory and the device is
+    idle; the timed region is one DPS call from the host (validation, ctypes,
+    launches) to the end of its last kernel.  Returns the median ms/call."""
+    import statistics
+    import torch
+    from gdn_amd import prefill
+    from oracle import gdn_oracle as O  # input recipe only
+
+    inp = O.make_prefill_inputs(lens, seed=2, with_state=len(lens) > 1)
+    d = _dev_inputs(inp, dev)
+    d["cu_seqlens"] = torch.from_numpy(inp["cu_seqlens"]).to(dev)
+    T, N = sum(lens), len(lens)
+    names = ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu_seqlens")
+    times = []
+    for i in range(reps + 3):
+        c = {n: (None if d[n] is None else d[n].clone()) for n in names}
+        out = torch.empty((T, 8, 128), dtype=torch.bfloat16, device=dev)
+        ns = torch.empty((N, 8, 128, 128), dtype=torch.float32, device=dev)
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record()
+        prefill.kernel(*(c[n] for n in names), inp["scale"], out, ns)
+        t1.record()
+        torch.cuda.synchronize()
+        if i >= 3:
+            times.append(t0.elapsed_time(t1))
+    return statistics.median(times)
+
+
 def measured_traffic(path=os.path.join(ROOT, "profiles", "decode_b64_hbm_traffic.md")):
     """HBM bytes per decode launch at B=64 from the committed rocprofv3 PMC
     summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of known size);
@@ -254,6 +286,12 @@ def main():
     log(f"prefill 1x8192: graph {pre_ms:.3f} ms ({T8 / (pre_ms * 1e-3) / 1e6:.2f} M tok/s, "
         f"{pre_tflops:.1f} TFLOP/s, {pre_gbs:.0f} GB/s); eager {pre_eager:.3f} ms")
 
+    pre_clone = bench_prefill_clone(pre_lens, 20, dev)
+    pre1k_eager, pre1k_ms = bench_prefill([1024], max(10, args.steps // 10), 3, dev)
+    pre1k_clone = bench_prefill_clone([1024], 20, dev)
+    log(f"prefill clone mode: 1x8192 {pre_clone:.3f} ms, 1x1024 {pre1k_clone:.3f} ms; "
+        f"1x1024 graph {pre1k_ms:.3f} ms, eager {pre1k_eager:.3f} ms")
+
     cpu_s, reps = cpu_baseline_decode(B, args.cpu_seconds)
     cpu_gbs = nbytes / cpu_s / 1e9
     log(f"cpu baseline decode B={B}: {cpu_s * 1e3:.1f} ms/step over {reps} steps")
@@ -279,6 +317,9 @@ def main():
         "prefill_ms_1x8192": round(pre_ms, 4),
         "prefill_ms_1x8192_eager": round(pre_eager, 4),
         "prefill_tokens_per_s": round(T8 / (pre_ms * 1e-3), 1),
+        "prefill_ms_1x8192_clone": round(pre_clone, 4),
+        "prefill_ms_1x1024": round(pre1k_ms, 4),
+        "prefill_ms_1x1024_clone": round(pre1k_clone, 4),
         "prefill_roofline": {"bound": "mfma", "achieved": round(pre_tflops, 2), "peak": 2500.0,
                              "unit": "TFLOP/s", "frac": round(pre_tflops / 2500.0, 5),
                              "hbm_gbs": round(pre_gbs, 1),

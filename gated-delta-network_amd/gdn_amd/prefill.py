@@ -11,7 +11,11 @@ from (T, N) alone.
 
 Workspace: device memory from torch's caching allocator, kept per (device,
 stream) and grown on demand, replacing the reference's module-level buffer
-cache (fla_kernels.py:950-957), which was keyed by name only.
+cache (fla_kernels.py:950-957), which was keyed by name only.  A caller that
+must not allocate inside the call (HIP graph capture, a serving loop) passes
+its own buffer as ``workspace=`` (see ``alloc_workspace``); nothing in the
+call then allocates, copies to the host or synchronises, so one captured graph
+serves any batch of the same (T, N), including new cu_seqlens contents.
 """
 
 from __future__ import annotations
@@ -29,6 +33,26 @@ _workspaces: dict = {}
 
 def workspace_bytes(total_tokens: int, num_seqs: int) -> int:
     return int(_lib.load().gdn_prefill_workspace_bytes(int(total_tokens), int(num_seqs)))
+
+
+def alloc_workspace(total_tokens: int, num_seqs: int, device=None) -> torch.Tensor:
+    """A caller-owned workspace for ``kernel(..., workspace=...)``: uint8 bytes
+    sized for any batch of ``total_tokens`` tokens in ``num_seqs`` sequences."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    return torch.empty(max(workspace_bytes(total_tokens, num_seqs), 256), dtype=torch.uint8,
+                       device=dev)
+
+
+def _check_workspace(ws, dev: torch.device, nbytes: int) -> None:
+    if not isinstance(ws, torch.Tensor) or ws.dtype != torch.uint8 or ws.dim() != 1:
+        raise ValueError("workspace must be a 1-D uint8 tensor (see alloc_workspace)")
+    if ws.device != dev:
+        raise ValueError(f"workspace is on {ws.device}, expected {dev}")
+    if not ws.is_contiguous() or ws.data_ptr() % 256:
+        raise ValueError("workspace must be contiguous and 256-byte aligned")
+    if ws.numel() < nbytes:
+        raise _lib.GdnWorkspaceError(
+            f"workspace holds {ws.numel()} bytes; this batch needs {nbytes}")
 
 
 def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
@@ -75,7 +99,7 @@ def _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_stat
 
 
 def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state, *,
-           variant=-1):
+           variant=-1, workspace=None):
     """Chunked GDN prefill over a packed batch, written into ``output`` and
     ``new_state``.
 
@@ -84,7 +108,8 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
     on the device (0 = cu[0] <= ... <= cu[N] = T); scale float, 0-d tensor or
     None; output [T,8,128] bf16; new_state [N,8,128,128] f32 (may be state).
     ``variant`` picks the state-recurrence tiling (gdn_prefill_fwd_variant);
-    the default is the built-in one.
+    the default is the built-in one.  ``workspace``: a caller-owned uint8
+    buffer (``alloc_workspace``) used instead of the per-stream cache.
     """
     lib = _lib.load()
     T, N, dev = _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state)
@@ -95,7 +120,11 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
         dense(t) for t in (q, k, v, a, b, A_log, dt_bias, cu_seqlens))
     stream = stream_of(dev)
     nbytes = int(lib.gdn_prefill_workspace_bytes(T, N))
-    ws = _workspace(dev, stream, nbytes)
+    if workspace is None:
+        ws = _workspace(dev, stream, nbytes)
+    else:
+        _check_workspace(workspace, dev, nbytes)
+        ws = workspace
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), None if state is None else state.data_ptr(),
             A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr(),
             cu_seqlens.data_ptr(), 1 if cu_seqlens.dtype == torch.int64 else 0, N, T, scale,
