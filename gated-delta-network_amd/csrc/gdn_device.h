@@ -74,6 +74,14 @@ __device__ __forceinline__ float gdn_log_decay(float A_log, float a, float dt_bi
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// cu_seqlens[i] (int32 or int64 on the device), clamped to [0, T] so that a
+// malformed batch can never index outside the packed tensors.
+__device__ __forceinline__ int load_cu(const void *cu, int is64, int i, int T) {
+  long long x = is64 ? static_cast<const long long *>(cu)[i] : static_cast<const int *>(cu)[i];
+  x = x < 0 ? 0 : x;
+  return static_cast<int>(x > T ? T : x);
+}
+
 }  // namespace gdn
 
 namespace gdn {

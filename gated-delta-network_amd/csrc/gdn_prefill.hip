@@ -46,7 +46,6 @@ namespace gdn {
 // LDS row strides (elements), padded by 16 bytes against bank conflicts.
 constexpr int kStrideK = 136;  // bf16 [64][128] tiles
 constexpr int kStrideT = 72;   // bf16 [*][64]   tiles
-constexpr int kStrideA = 65;   // f32  [64][64]  tile
 
 // Workspace layout; every region starts on a 256-byte boundary.
 struct PrefillLayout {
@@ -85,22 +84,18 @@ static PrefillLayout prefill_layout(int T, int N) {
   return L;
 }
 
-__device__ __forceinline__ int load_cu(const void *cu, int is64, int i, int T) {
-  long long x = is64 ? static_cast<const long long *>(cu)[i] : static_cast<const int *>(cu)[i];
-  x = x < 0 ? 0 : x;
-  return static_cast<int>(x > T ? T : x);
-}
-
 // ---------------------------------------------------------------------------
 // 1. chunk table: chunks[c] = {sequence, first token, tokens (1..64), chunk
 // number within the sequence} for c < NT, {-1, 0, 0, 0} up to nt_max;
 // offsets[s] = first chunk of sequence s, offsets[N] = NT.  Token bounds are
 // clamped to [0, T] and the chunk count to nt_max, so a malformed cu_seqlens
-// cannot send any later kernel out of bounds.
+// cannot send any later kernel out of bounds.  A sequence of at most rec_max
+// tokens gets no chunks (the token-sequential kernel owns it); rec_max < 0
+// routes every sequence through the chunks.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int cu64, int N, int T,
-                                                              int nt_max, int4 *chunks,
-                                                              int *offsets) {
+                                                              int nt_max, int rec_max,
+                                                              int4 *chunks, int *offsets) {
   __shared__ int s_incl[1024];
   const int tid = threadIdx.x;
   long long carry = 0;
@@ -111,7 +106,7 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
       const int bos = load_cu(cu, cu64, s, T);
       int eos = load_cu(cu, cu64, s + 1, T);
       eos = eos < bos ? bos : eos;
-      n = (eos - bos + kChunk - 1) / kChunk;
+      n = eos - bos > rec_max ? (eos - bos + kChunk - 1) / kChunk : 0;
     }
     s_incl[tid] = n;
     __syncthreads();
@@ -469,7 +464,7 @@ template <int BV>
 __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
     const float *state, float *new_state, const int *offsets, const float *ws_dcy,
     const float *ws_eg, const uint16_t *ws_w, const float *ws_u,
-    const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt) {
+    const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt, int skip_empty) {
   constexpr int NVB = kDV / BV;
   const int h = blockIdx.x % kHV;
   const int rest = blockIdx.x / kHV;
@@ -487,6 +482,7 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
 
   const int c0 = offsets[s];
   const int nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
+  if (nch == 0 && skip_empty) return;  // owned by the token-sequential kernel
   const size_t sbase = (static_cast<size_t>(s) * kHV + h) * kDV * kDK;  // [V][K]
 
   f32x4 S[2];
@@ -712,11 +708,17 @@ __global__ __launch_bounds__(256) void prefill_output_kernel(
   }
 }
 
+// Sequences of at most this many tokens take the token-sequential kernel
+// (gdn_recurrent.hip) instead of the chunked pipeline; from a length sweep of
+// both paths on MI355X.
+constexpr int kRecurrentMaxLen = 256;
+
 static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                           const float *state, const float *A_log, const gdn_bf16 *a,
                           const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
                           int cu64, int N, int T, float scale, gdn_bf16 *output, float *new_state,
-                          void *workspace, size_t ws_bytes, void *stream_ptr, int variant) {
+                          void *workspace, size_t ws_bytes, void *stream_ptr, int variant,
+                          int rec_max, int rec_variant) {
   clear_error();
   if (N < 0 || T < 0) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: num_seqs=%d, total_tokens=%d", N, T);
   if (!cu_seqlens) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: null cu_seqlens");
@@ -733,6 +735,9 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   if (!aligned(cu_seqlens, cu64 ? 8 : 4))
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: cu_seqlens misaligned");
   if (variant < -1 || variant > 1) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown variant %d", variant);
+  if (rec_max < -2) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: recurrent_max_len %d < -2", rec_max);
+  if (rec_variant < -1 || rec_variant >= recurrent_num_variants())
+    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown recurrent tiling %d", rec_variant);
   if (N == 0) return GDN_OK;
 
   const PrefillLayout L = prefill_layout(T, N);
@@ -776,10 +781,24 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   uint16_t *ht = reinterpret_cast<uint16_t *>(ws + L.ht);
   uint16_t *vnt = reinterpret_cast<uint16_t *>(ws + L.vnt);
 
+  // Routing by sequence length (on the device): at most rmax tokens -> the
+  // token-sequential kernel, longer -> the chunked pipeline.  rmax < 0: all
+  // chunked.  When T <= rmax every sequence is short and no chunk work is
+  // launched at all; with one sequence longer than rmax nothing is short.
+  const int rmax = rec_max == -1 ? kRecurrentMaxLen : (rec_max == -2 ? -1 : rec_max);
+  if (rmax >= T)
+    return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0, rmax,
+                            scale, output, new_state, stream, rec_variant, "gdn_prefill_fwd");
+
   hipLaunchKernelGGL(prefill_index_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, cu64, N, T,
-                     L.nt_max, chunks, offsets);
+                     L.nt_max, rmax, chunks, offsets);
   int rc = check_launch("gdn_prefill_fwd(index)");
   if (rc) return rc;
+  if (rmax >= 0 && N > 1) {
+    rc = recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0, rmax,
+                          scale, output, new_state, stream, rec_variant, "gdn_prefill_fwd");
+    if (rc) return rc;
+  }
   if (L.nt_max > 0) {
     hipLaunchKernelGGL(prefill_intra_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, k, v, A_log,
                        a, dt_bias, b, chunks, wsG, wsD, wsE, wsw, wsu, kt);
@@ -788,12 +807,13 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   const int bv = variant == 1 ? 32 : 16;  // 16 measured faster at every size
   const long long blocks = static_cast<long long>(N) * kHV * (kDV / bv);
   if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
+  const int skip_empty = rmax >= 0 ? 1 : 0;
   if (bv == 32)
     hipLaunchKernelGGL(prefill_state_kernel<32>, dim3(static_cast<unsigned>(blocks)), dim3(512), 0,
-                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt);
+                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, skip_empty);
   else
     hipLaunchKernelGGL(prefill_state_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt);
+                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, skip_empty);
   if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
   if (L.nt_max > 0) {
     hipLaunchKernelGGL(prefill_output_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, q, k, chunks,
@@ -818,7 +838,7 @@ extern "C" int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_b
                                size_t workspace_bytes, void *stream) {
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
                              num_seqs, total_tokens, scale, output, new_state, workspace,
-                             workspace_bytes, stream, -1);
+                             workspace_bytes, stream, -1, -1, -1);
 }
 
 extern "C" int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
@@ -830,5 +850,19 @@ extern "C" int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, con
                                        size_t workspace_bytes, void *stream, int variant) {
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
                              num_seqs, total_tokens, scale, output, new_state, workspace,
-                             workspace_bytes, stream, variant);
+                             workspace_bytes, stream, variant, -1, -1);
+}
+
+extern "C" int gdn_prefill_fwd_tuned(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                                     const float *state, const float *A_log, const gdn_bf16 *a,
+                                     const float *dt_bias, const gdn_bf16 *b,
+                                     const void *cu_seqlens, int cu_seqlens_is_int64,
+                                     int num_seqs, int total_tokens, float scale,
+                                     gdn_bf16 *output, float *new_state, void *workspace,
+                                     size_t workspace_bytes, void *stream, int state_tiling,
+                                     int recurrent_max_len, int recurrent_tiling) {
+  return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
+                             num_seqs, total_tokens, scale, output, new_state, workspace,
+                             workspace_bytes, stream, state_tiling, recurrent_max_len,
+                             recurrent_tiling);
 }

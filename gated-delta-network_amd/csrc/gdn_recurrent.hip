@@ -1,0 +1,276 @@
+// Gated DeltaNet token-sequential recurrence: the state of one (sequence,
+// v-head, block of V-rows) lives in registers for the whole sequence and every
+// token is one fused decode step on it.
+//
+// Semantics: the per-token loop of reference/gdn_prefill_ref.py:71-89 (and,
+// for a single token, reference/gdn_decode_ref.py:60-81):
+//   g = exp(-exp(A_log[h]) * softplus(a_t + dt_bias[h])),  beta = sigmoid(b_t)
+//   for every V-row r:  pred = g <S[r,:], k_t>,  v_new = beta (v_t[r] - pred)
+//                       S[r,:] = g S[r,:] + v_new k_t
+//                       o_t[r] = scale <S[r,:], q_t> = scale (g <S_old[r],q_t> + v_new <k_t,q_t>)
+// with q/k head h/2 (GVA without copies).  It serves
+//   * prefill of short sequences, where the chunked pipeline's fixed cost
+//     (four dependent launches, a full chunk of work per sequence) dominates:
+//     the sequential-scan / chunked crossover of OPTIMIZATION_LOG.md:79,
+//     170-184, dispatched per sequence on the device by its length;
+//   * decode of T > 1 tokens per batch row (multi-token / speculative decode),
+//     a fixed-length batch [B, T, ...] that is exactly the packed layout.
+//
+// Work mapping (gfx950, wave64) as in the decode kernel: a state row of 128
+// floats is held by an aligned group of 16 lanes, 8 floats per lane (columns
+// 4c..4c+3 and 64+4c..64+4c+3), so the two row dot products per token are 8
+// FMAs and 4 DPP adds.  A workgroup of WAVES waves owns 4*WAVES*PASSES rows.
+// Per token each lane loads its 8 columns of k and q (two 8-byte loads each)
+// and one bf16 of v per pass, one token ahead of use; the gating of 64 tokens
+// is computed at once, one token per lane, and read back with readlane.
+#include "gdn_device.h"
+#include "gdn_host.h"
+
+namespace gdn {
+
+template <int PASSES>
+struct TokenIn {
+  u16x4 k0, k1, q0, q1;
+  uint16_t v[PASSES];
+};
+
+template <int WAVES, int PASSES>
+__global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
+    const uint16_t *__restrict__ v, const float *state, const float *__restrict__ A_log,
+    const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
+    const uint16_t *__restrict__ b, const void *__restrict__ cu, int cu64, int T, int fixed_len,
+    int max_len, float scale, uint16_t *__restrict__ out, float *new_state) {
+  constexpr int kRows = 4 * WAVES * PASSES;
+  constexpr int kTiles = kDV / kRows;
+  static_assert(kDV % kRows == 0, "row block must divide 128");
+
+  const int h = blockIdx.x % kHV;  // consecutive workgroups: the 8 heads
+  const int rest = blockIdx.x / kHV;
+  const int tile = rest % kTiles, s = rest / kTiles;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c4 = 4 * (lane & 15);
+  const bool leader = (lane & 15) == 0;
+  const int row0 = tile * kRows + wave * 4 * PASSES + (lane >> 4);  // pass p: row0 + 4p
+
+  int bos, len;
+  if (cu != nullptr) {
+    bos = load_cu(cu, cu64, s, T);
+    const int eos = load_cu(cu, cu64, s + 1, T);
+    len = eos > bos ? eos - bos : 0;
+  } else {
+    bos = s * fixed_len;
+    len = fixed_len;
+  }
+  if (len > max_len) return;  // a longer sequence goes through the chunked pipeline
+
+  const int hq = h >> 1;
+  const size_t sbase = (static_cast<size_t>(s) * kHV + h) * kDV * kDK;
+  f32x4 Sa[PASSES], Sb[PASSES];  // columns c4.. and 64 + c4..
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const size_t off = sbase + static_cast<size_t>(row0 + 4 * p) * kDK + c4;
+    if (state != nullptr && len > 0) {
+      Sa[p] = *reinterpret_cast<const f32x4 *>(state + off);
+      Sb[p] = *reinterpret_cast<const f32x4 *>(state + off + 64);
+    } else {
+      Sa[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+      Sb[p] = Sa[p];
+    }
+  }
+
+  if (len > 0) {
+    const float rate = expf(A_log[h]);
+    const float dtb = dt_bias[h];
+    auto load_token = [&](int t, TokenIn<PASSES> &x) {
+      const size_t tok = static_cast<size_t>(bos) + t;
+      const uint16_t *kp = k + (tok * kHQK + hq) * kDK + c4;
+      const uint16_t *qp = q + (tok * kHQK + hq) * kDK + c4;
+      x.k0 = *reinterpret_cast<const u16x4 *>(kp);
+      x.k1 = *reinterpret_cast<const u16x4 *>(kp + 64);
+      x.q0 = *reinterpret_cast<const u16x4 *>(qp);
+      x.q1 = *reinterpret_cast<const u16x4 *>(qp + 64);
+      const uint16_t *vp = v + (tok * kHV + h) * kDV + row0;
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) x.v[p] = vp[4 * p];
+    };
+
+    TokenIn<PASSES> cur, nxt;
+    load_token(0, cur);
+    for (int t0 = 0; t0 < len; t0 += 64) {
+      // Gating of tokens t0 .. t0+63, token t0 + lane in this lane.
+      float gl = 1.f, bl = 0.f;
+      if (t0 + lane < len) {
+        const size_t tok = static_cast<size_t>(bos) + t0 + lane;
+        gl = expf(-rate * softplus20(bf16_to_f32(a[tok * kHV + h]) + dtb));
+        bl = sigmoidf_(bf16_to_f32(b[tok * kHV + h]));
+      }
+      const int n = len - t0 < 64 ? len - t0 : 64;
+      for (int i = 0; i < n; ++i) {
+        const int t = t0 + i;
+        load_token(t + 1 < len ? t + 1 : t, nxt);  // next token, clamped
+        const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gl), i));
+        const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bl), i));
+        float kf[8], qf[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kf[e] = bf16_to_f32(cur.k0[e]);
+          kf[4 + e] = bf16_to_f32(cur.k1[e]);
+          qf[e] = bf16_to_f32(cur.q0[e]);
+          qf[4 + e] = bf16_to_f32(cur.q1[e]);
+        }
+        float pkq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pkq = fmaf(kf[e], qf[e], pkq);
+        const float kq = row16_sum(pkq);
+        uint16_t *op = out + ((static_cast<size_t>(bos) + t) * kHV + h) * kDV + row0;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+          float sk0 = 0.f, sk1 = 0.f, sq0 = 0.f, sq1 = 0.f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sk0 = fmaf(Sa[p][e], kf[e], sk0);
+            sk1 = fmaf(Sb[p][e], kf[4 + e], sk1);
+            sq0 = fmaf(Sa[p][e], qf[e], sq0);
+            sq1 = fmaf(Sb[p][e], qf[4 + e], sq1);
+          }
+          const float sk = row16_sum(sk0 + sk1);
+          const float sq = row16_sum(sq0 + sq1);
+          const float vn = beta * (bf16_to_f32(cur.v[p]) - g * sk);
+          const float o = scale * fmaf(g, sq, vn * kq);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            Sa[p][e] = fmaf(vn, kf[e], g * Sa[p][e]);
+            Sb[p][e] = fmaf(vn, kf[4 + e], g * Sb[p][e]);
+          }
+          if (leader) op[4 * p] = f32_to_bf16(o);
+        }
+        cur = nxt;
+      }
+    }
+  }
+
+  // Final state; all zeros for a zero-length sequence (gdn_prefill_ref.py:61-62).
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const size_t off = sbase + static_cast<size_t>(row0 + 4 * p) * kDK + c4;
+    *reinterpret_cast<f32x4 *>(new_state + off) = Sa[p];
+    *reinterpret_cast<f32x4 *>(new_state + off + 64) = Sb[p];
+  }
+}
+
+namespace {
+
+struct RecVariant {
+  int waves, passes;
+};
+// rows per workgroup = 4 * waves * passes
+constexpr RecVariant kRecVariants[] = {
+    {1, 1}, {2, 1}, {4, 1}, {1, 2}, {2, 2}, {4, 2}, {1, 4}, {4, 4}, {1, 8}, {1, 16}};
+constexpr int kNumRecVariants = sizeof(kRecVariants) / sizeof(kRecVariants[0]);
+
+template <int W, int P>
+void launch_rec(long long groups, hipStream_t stream, const uint16_t *q, const uint16_t *k,
+                const uint16_t *v, const float *state, const float *A_log, const uint16_t *a,
+                const float *dt_bias, const uint16_t *b, const void *cu, int cu64, int T,
+                int fixed_len, int max_len, float scale, uint16_t *out, float *new_state) {
+  const long long blocks = groups * (kDV / (4 * W * P));
+  hipLaunchKernelGGL((recurrent_kernel<W, P>), dim3(static_cast<unsigned>(blocks)), dim3(64 * W),
+                     0, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T, fixed_len,
+                     max_len, scale, out, new_state);
+}
+
+}  // namespace
+
+int recurrent_num_variants() { return kNumRecVariants; }
+
+// Built-in tiling: few (sequence, head) groups -> small row blocks, so that
+// more workgroups share the serial token loop; many -> larger blocks.
+int recurrent_default_variant(long long groups) {
+  if (groups <= 64) return 2;    // 16 rows, 4 waves
+  if (groups <= 512) return 5;   // 32 rows, 4 waves
+  return 7;                      // 64 rows, 4 waves
+}
+
+// Launches the recurrence over `num_groups` = sequences (or batch rows) x 8
+// heads.  cu == nullptr means fixed-length sequences [s*fixed_len, ...).
+// Sequences longer than max_len are skipped (left to the chunked pipeline).
+int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
+                     const float *A_log, const uint16_t *a, const float *dt_bias,
+                     const uint16_t *b, const void *cu, int cu64, int num_seqs, int T,
+                     int fixed_len, int max_len, float scale, uint16_t *out, float *new_state,
+                     hipStream_t stream, int variant, const char *what) {
+  const long long groups = static_cast<long long>(num_seqs) * kHV;
+  if (variant < 0) variant = recurrent_default_variant(groups);
+  if (variant >= kNumRecVariants)
+    return fail(GDN_ERR_INVALID, "%s: recurrent tiling %d out of range", what, variant);
+  const RecVariant rv = kRecVariants[variant];
+  if (groups * (kDV / (4 * rv.waves * rv.passes)) > 0x7fffffffLL)
+    return fail(GDN_ERR_INVALID, "%s: too many sequences for one launch", what);
+#define GDN_REC(W, P)                                                                          \
+  if (rv.waves == W && rv.passes == P)                                                        \
+    launch_rec<W, P>(groups, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T,       \
+                     fixed_len, max_len, scale, out, new_state);
+  GDN_REC(1, 1)
+  GDN_REC(2, 1)
+  GDN_REC(4, 1)
+  GDN_REC(1, 2)
+  GDN_REC(2, 2)
+  GDN_REC(4, 2)
+  GDN_REC(1, 4)
+  GDN_REC(4, 4)
+  GDN_REC(1, 8)
+  GDN_REC(1, 16)
+#undef GDN_REC
+  return check_launch(what);
+}
+
+}  // namespace gdn
+
+extern "C" int gdn_decode_multi_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                                    const float *state, const float *A_log, const gdn_bf16 *a,
+                                    const float *dt_bias, const gdn_bf16 *b, float scale,
+                                    gdn_bf16 *output, float *new_state, int batch, int tokens,
+                                    void *stream, int variant) {
+  using namespace gdn;
+  clear_error();
+  if (batch < 0 || tokens < 1)
+    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: batch=%d, tokens=%d", batch, tokens);
+  if (!q || !k || !v || !A_log || !a || !dt_bias || !b || !output || !new_state)
+    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: null pointer argument");
+  if (!(scale > 0.0f) || scale == __builtin_inff())
+    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: scale must be finite and > 0");
+  if (!aligned(new_state, 16) || (state && !aligned(state, 16)))
+    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: state/new_state must be 16-byte aligned");
+  if (!aligned(q, 8) || !aligned(k, 8))
+    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: q/k must be 8-byte aligned");
+  if (variant < -1 || variant >= recurrent_num_variants())
+    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: unknown variant %d", variant);
+  const long long total = static_cast<long long>(batch) * tokens;
+  if (total > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: batch*tokens too large");
+  if (batch == 0) return GDN_OK;
+  const size_t nb = static_cast<size_t>(batch), nt = static_cast<size_t>(total);
+  const size_t state_bytes = nb * kHV * kDV * kDK * sizeof(float);
+  const size_t out_bytes = nt * kHV * kDV * sizeof(uint16_t);
+  if (state != new_state && overlaps(state, state_bytes, new_state, state_bytes))
+    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: new_state partially overlaps state");
+  const void *ins[] = {q, k, v, a, b, A_log, dt_bias, state};
+  const size_t in_bytes[] = {nt * kHQK * kDK * 2, nt * kHQK * kDK * 2, nt * kHV * kDV * 2,
+                             nt * kHV * 2,        nt * kHV * 2,        kHV * 4,
+                             kHV * 4,             state ? state_bytes : 0};
+  for (int i = 0; i < 8; ++i) {
+    if (overlaps(output, out_bytes, ins[i], in_bytes[i]))
+      return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: output overlaps an input");
+    if (i < 7 && overlaps(new_state, state_bytes, ins[i], in_bytes[i]))
+      return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: new_state overlaps an input");
+  }
+  if (overlaps(output, out_bytes, new_state, state_bytes))
+    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: output overlaps new_state");
+  // One token per row is the plain decode step, whose kernel is tuned for it.
+  if (tokens == 1 && variant == -1)
+    return gdn_decode_fwd(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
+                          stream);
+  return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, nullptr, 0, batch,
+                          static_cast<int>(total), tokens, 0x7fffffff, scale, output, new_state,
+                          static_cast<hipStream_t>(stream), variant, "gdn_decode_multi_fwd");
+}

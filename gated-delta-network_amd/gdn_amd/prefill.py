@@ -99,7 +99,7 @@ def _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_stat
 
 
 def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state, *,
-           variant=-1, workspace=None):
+           variant=-1, workspace=None, recurrent_max_len=-1, recurrent_variant=-1):
     """Chunked GDN prefill over a packed batch, written into ``output`` and
     ``new_state``.
 
@@ -110,6 +110,9 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
     ``variant`` picks the state-recurrence tiling (gdn_prefill_fwd_variant);
     the default is the built-in one.  ``workspace``: a caller-owned uint8
     buffer (``alloc_workspace``) used instead of the per-stream cache.
+    ``recurrent_max_len``: sequences of at most this many tokens run token by
+    token instead of through the chunks (-1 built-in, -2 never);
+    ``recurrent_variant``: that kernel's row tiling (gdn_prefill_fwd_tuned).
     """
     lib = _lib.load()
     T, N, dev = _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state)
@@ -129,7 +132,10 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
             A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr(),
             cu_seqlens.data_ptr(), 1 if cu_seqlens.dtype == torch.int64 else 0, N, T, scale,
             output.data_ptr(), new_state.data_ptr(), ws.data_ptr(), ws.numel(), stream)
-    if variant == -1:
+    if recurrent_max_len != -1 or recurrent_variant != -1:
+        rc = lib.gdn_prefill_fwd_tuned(*args, int(variant), int(recurrent_max_len),
+                                       int(recurrent_variant))
+    elif variant == -1:
         rc = lib.gdn_prefill_fwd(*args)
     else:
         rc = lib.gdn_prefill_fwd_variant(*args, int(variant))

@@ -77,6 +77,30 @@ int gdn_decode_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 
                            int variant);
 
 /*
+ * Decode of `tokens` >= 1 consecutive tokens per batch row (multi-token /
+ * speculative decode): for each row, the T = 1 step of gdn_decode_fwd applied
+ * token after token, the state carried in registers between tokens and written
+ * once at the end.  No counterpart in the reference, whose decode asserts
+ * T == 1 (reference/gdn_decode_ref.py:32-36); it extends the same entry point
+ * kernel(q, k, v, state, ...) of solutions/gdn_decode_qk4_v8_d128_k_last/
+ * solution/triton/kernel.py:85 to T > 1, and equals gdn_prefill_fwd on `batch`
+ * sequences of `tokens` tokens each (reference/gdn_prefill_ref.py:71-89).
+ *
+ *   q, k      [B, T, 4, 128] bf16      v         [B, T, 8, 128] bf16
+ *   a, b      [B, T, 8] bf16           output    [B, T, 8, 128] bf16
+ *   state, new_state, A_log, dt_bias, scale as for gdn_decode_fwd.
+ *
+ * variant: row tiling of the token-sequential kernel (0..9: 4, 8, 16, 8, 16,
+ * 32, 16, 64, 32, 64 rows per workgroup with 64, 128, 256, 64, 128, 256, 64,
+ * 256, 64, 64 threads), -1 = built-in (tokens == 1 then runs gdn_decode_fwd).
+ */
+int gdn_decode_multi_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                         const float *state, const float *A_log, const gdn_bf16 *a,
+                         const float *dt_bias, const gdn_bf16 *b, float scale,
+                         gdn_bf16 *output, float *new_state, int batch, int tokens, void *stream,
+                         int variant);
+
+/*
  * Bytes of device workspace gdn_prefill_fwd needs for a packed batch of
  * total_tokens tokens in num_seqs sequences.  The bound does not depend on the
  * individual lengths (they stay on the device), so a caller can size it once.
@@ -105,6 +129,12 @@ size_t gdn_prefill_workspace_bytes(int total_tokens, int num_seqs);
  * unspecified but never accesses memory out of bounds).  A zero-length
  * sequence gets an all-zero new_state, as the reference does.  new_state may
  * alias state; output must not overlap any input.
+ *
+ * Each sequence is routed on the device by its length: short ones (up to a
+ * built-in length) run token by token with the state in registers, the others
+ * through the chunk-64 pipeline; results agree within the stated tolerance
+ * either way (the reference measured the same crossover between its
+ * sequential scan and chunked kernels, OPTIMIZATION_LOG.md:79,170-184).
  */
 int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                     const float *state, const float *A_log, const gdn_bf16 *a,
@@ -120,7 +150,8 @@ int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
  * sharing each SIMD), -1 = the built-in choice (what gdn_prefill_fwd uses).  The counterpart of the reference's autotuned
  * BV of chunk_gated_delta_rule_fwd_kernel_h (solutions/
  * gdn_prefill_qk4_v8_d128_k_last/solution/triton/fla_kernels.py:407-426,
- * 1028-1035).  Results are identical for every variant.
+ * 1028-1035).  Results are identical for every variant (sequences routed
+ * to the token-sequential kernel do not depend on it).
  */
 int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                             const float *state, const float *A_log, const gdn_bf16 *a,
@@ -128,6 +159,21 @@ int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16
                             int cu_seqlens_is_int64, int num_seqs, int total_tokens, float scale,
                             gdn_bf16 *output, float *new_state, void *workspace,
                             size_t workspace_bytes, void *stream, int variant);
+
+/*
+ * gdn_prefill_fwd with every tuning choice explicit (for sweeps and tests):
+ *   state_tiling       as the variant of gdn_prefill_fwd_variant (-1 built-in)
+ *   recurrent_max_len  sequences of at most this many tokens run token by
+ *                      token; -1 = built-in, -2 = none (all chunked)
+ *   recurrent_tiling   as the variant of gdn_decode_multi_fwd (-1 built-in)
+ */
+int gdn_prefill_fwd_tuned(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                          const float *state, const float *A_log, const gdn_bf16 *a,
+                          const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
+                          int cu_seqlens_is_int64, int num_seqs, int total_tokens, float scale,
+                          gdn_bf16 *output, float *new_state, void *workspace,
+                          size_t workspace_bytes, void *stream, int state_tiling,
+                          int recurrent_max_len, int recurrent_tiling);
 
 #ifdef __cplusplus
 }

@@ -128,3 +128,47 @@ def test_prefill_rejects_bad_arguments(over, needle, code):
 def test_prefill_no_sequences_is_a_no_op():
     lib = _lib.load()
     assert lib.gdn_prefill_fwd(*_prefill_args(N=0, T=0)) == _lib.GDN_OK
+
+
+def _multi_args(**over):
+    args = dict(q=1 << 20, k=2 << 20, v=3 << 20, state=None, A_log=4 << 20, a=5 << 20,
+                dt_bias=6 << 20, b=7 << 20, scale=0.1, output=8 << 20, new_state=16 << 20,
+                batch=2, tokens=3, stream=None, variant=-1)
+    args.update(over)
+    return list(args.values())
+
+
+@pytest.mark.parametrize("over, needle", [
+    (dict(tokens=0), "tokens"),
+    (dict(batch=-1), "batch"),
+    (dict(v=None), "null"),
+    (dict(scale=0.0), "scale"),
+    (dict(variant=10), "variant"),
+    (dict(variant=-2), "variant"),
+    (dict(new_state=(16 << 20) + 8), "aligned"),
+    # output is [B*T, 8, 128] bf16 = 12 KiB: ending inside v
+    (dict(output=(3 << 20) - 4096), "overlap"),
+    (dict(state=(16 << 20) + 4096), "overlap"),
+])
+def test_decode_multi_rejects_bad_arguments(over, needle):
+    lib = _lib.load()
+    rc = lib.gdn_decode_multi_fwd(*_multi_args(**over))
+    assert rc == _lib.GDN_ERR_INVALID
+    assert needle in _lib.last_error()
+
+
+def test_decode_multi_zero_batch_is_a_no_op():
+    lib = _lib.load()
+    assert lib.gdn_decode_multi_fwd(*_multi_args(batch=0)) == _lib.GDN_OK
+
+
+@pytest.mark.parametrize("tuning, needle", [
+    ((-1, -3, -1), "recurrent_max_len"),
+    ((-1, -1, 10), "recurrent tiling"),
+    ((2, -1, -1), "variant"),
+])
+def test_prefill_tuned_rejects_bad_tuning(tuning, needle):
+    lib = _lib.load()
+    rc = lib.gdn_prefill_fwd_tuned(*_prefill_args(), *tuning)
+    assert rc == _lib.GDN_ERR_INVALID
+    assert needle in _lib.last_error()

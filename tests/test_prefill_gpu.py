@@ -47,18 +47,24 @@ def to_dev(inp, dev, cu_dtype=torch.int64):
     return d
 
 
-def run_gpu(d, dev, in_place=False, variant=None):
+# "auto": the built-in per-sequence routing (short sequences token by token);
+# "chunked": every sequence through the chunk-64 pipeline.
+ROUTES = {"auto": -1, "chunked": -2}
+
+
+def run_gpu(d, dev, in_place=False, variant=None, route="auto"):
     T = d["q"].shape[0]
     N = d["cu_seqlens"].numel() - 1
     out = torch.empty((T, 8, 128), dtype=torch.bfloat16, device=dev)
     ns = d["state"] if in_place else torch.empty((N, 8, 128, 128), dtype=torch.float32, device=dev)
     args = (d["q"], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"], d["b"],
             d["cu_seqlens"], d["scale"], out, ns)
-    if variant is None:
+    if variant is None and route == "auto":
         kernel(*args)
     else:
         from gdn_amd import prefill
-        prefill.kernel(*args, variant=variant)
+        prefill.kernel(*args, variant=-1 if variant is None else variant,
+                       recurrent_max_len=ROUTES[route])
     torch.cuda.synchronize()
     return out.float().cpu().numpy(), ns.cpu().numpy()
 
@@ -79,36 +85,40 @@ REFERENCE_CASES = [
 ]
 
 
+@pytest.mark.parametrize("route", list(ROUTES))
 @pytest.mark.parametrize("lens, with_state", REFERENCE_CASES)
-def test_prefill_reference_cases(cuda_device, lens, with_state):
-    print(f"prefill parity lens={lens} state={with_state}", flush=True)
+def test_prefill_reference_cases(cuda_device, lens, with_state, route):
+    print(f"prefill parity lens={lens} state={with_state} route={route}", flush=True)
     inp = O.make_prefill_inputs(lens, seed=100 + len(lens), with_state=with_state)
     o_ref, s_ref = O.prefill_seq_c(**inp)
-    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, route=route)
     check(o, s, o_ref, s_ref)
 
 
+@pytest.mark.parametrize("route", list(ROUTES))
 @pytest.mark.parametrize("lens", [[1], [2, 1, 3], [63], [0, 5, 0, 70], [0], [0, 0, 17],
                                   [129, 0, 1, 64, 65]])
-def test_prefill_edge_lengths(cuda_device, lens):
-    print(f"prefill edge lens={lens}", flush=True)
+def test_prefill_edge_lengths(cuda_device, lens, route):
+    print(f"prefill edge lens={lens} route={route}", flush=True)
     inp = O.make_prefill_inputs(lens, seed=7)
     o_ref, s_ref = O.prefill_seq_c(**inp)
-    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, route=route)
     for i, L in enumerate(lens):
         if L == 0:
             assert np.all(s[i] == 0.0), "zero-length sequence must give a zero state"
     check(o, s, o_ref, s_ref)
 
 
-def test_prefill_many_sequences_multi_tile_index(cuda_device):
+@pytest.mark.parametrize("route", list(ROUTES))
+def test_prefill_many_sequences_multi_tile_index(cuda_device, route):
     # > 1024 sequences: the chunk-index scan runs over several tiles.
     rng = np.random.default_rng(11)
     lens = rng.integers(0, 4, 1500).tolist()
     lens[0] = 70
+    lens[700] = 300
     inp = O.make_prefill_inputs(lens, seed=8)
     o_ref, s_ref = O.prefill_seq_c(**inp)
-    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, route=route)
     check(o, s, o_ref, s_ref)
 
 
@@ -148,26 +158,27 @@ def test_prefill_config4_long_context(cuda_device):
 def test_prefill_variants_identical(cuda_device):
     inp = O.make_prefill_inputs([100, 0, 300], seed=12)
     d = to_dev(inp, cuda_device)
-    o0, s0 = run_gpu(d, cuda_device, variant=0)
-    o1, s1 = run_gpu(d, cuda_device, variant=1)
+    o0, s0 = run_gpu(d, cuda_device, variant=0, route="chunked")
+    o1, s1 = run_gpu(d, cuda_device, variant=1, route="chunked")
     assert np.array_equal(o0, o1) and np.array_equal(s0, s1)
     o_ref, s_ref = O.prefill_seq_c(**inp)
     check(o0, s0, o_ref, s_ref)
 
 
-def test_prefill_int32_cu_seqlens_state_none_in_place(cuda_device):
-    inp = O.make_prefill_inputs([40, 90], seed=13)
+@pytest.mark.parametrize("route", list(ROUTES))
+def test_prefill_int32_cu_seqlens_state_none_in_place(cuda_device, route):
+    inp = O.make_prefill_inputs([40, 90, 300], seed=13)
     d64 = to_dev(inp, cuda_device)
     d32 = to_dev(inp, cuda_device, cu_dtype=torch.int32)
-    o64, s64 = run_gpu(d64, cuda_device)
-    o32, s32 = run_gpu(d32, cuda_device)
+    o64, s64 = run_gpu(d64, cuda_device, route=route)
+    o32, s32 = run_gpu(d32, cuda_device, route=route)
     assert np.array_equal(o64, o32) and np.array_equal(s64, s32)
-    oi, si = run_gpu(d64, cuda_device, in_place=True)
+    oi, si = run_gpu(d64, cuda_device, in_place=True, route=route)
     assert np.array_equal(o64, oi) and np.array_equal(s64, si)
     inp["state"] = None
     dn = to_dev(inp, cuda_device)
     o_ref, s_ref = O.prefill_seq_c(**inp)
-    on, sn = run_gpu(dn, cuda_device)
+    on, sn = run_gpu(dn, cuda_device, route=route)
     check(on, sn, o_ref, s_ref)
 
 
@@ -200,10 +211,11 @@ def test_prefill_reference_test_distribution(cuda_device):
     check(o, s, o_ref, s_ref)
 
 
-def test_prefill_deterministic(cuda_device):
-    inp = O.make_prefill_inputs([200, 77], seed=15)
+@pytest.mark.parametrize("route", list(ROUTES))
+def test_prefill_deterministic(cuda_device, route):
+    inp = O.make_prefill_inputs([200, 77, 400], seed=15)
     d = to_dev(inp, cuda_device)
-    runs = [run_gpu(d, cuda_device) for _ in range(3)]
+    runs = [run_gpu(d, cuda_device, route=route) for _ in range(3)]
     for o, s in runs[1:]:
         assert np.array_equal(o, runs[0][0]) and np.array_equal(s, runs[0][1])
 
@@ -279,7 +291,7 @@ def test_prefill_stage_intermediates(cuda_device):
     L = _layout(T, N)
     assert prefill.workspace_bytes(T, N) == L["total"]
     d = to_dev(inp, cuda_device)
-    run_gpu(d, cuda_device)
+    run_gpu(d, cuda_device, route="chunked")
     ws = prefill._workspace(cuda_device, _stream(cuda_device), 0).cpu().numpy()
     _, _, it = O.prefill_chunked(**inp, return_intermediates=True)
     seq, local, offs = O.chunk_index(inp["cu_seqlens"])

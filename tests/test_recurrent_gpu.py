@@ -1,0 +1,192 @@
+"""The token-sequential kernel on the GPU: short-sequence prefill (routed per
+sequence by length), the routing itself, and multi-token decode (T > 1).
+
+Oracle: the sequential recurrence of reference/gdn_prefill_ref.py:71-89
+(oracle/gdn_seq.c through O.prefill_seq_c, pinned in tests/test_oracle.py).
+Tolerance as everywhere (conftest.py): bf16 output atol = rtol = 1e-2; f32
+state atol = 1e-3 * max|state_ref|.  The token-sequential kernel computes in
+f32 in the reference's order, so its state is also held to 1e-5 * max|ref|.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_output_close, assert_state_close
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+from gdn_amd import decode, prefill  # noqa: E402
+
+
+def _to_dev(inp, dev, cu_dtype=torch.int64):
+    bf = torch.bfloat16
+    d = {n: torch.from_numpy(np.ascontiguousarray(inp[n])).to(dev).to(bf)
+         for n in ("q", "k", "v", "a", "b")}
+    for n in ("A_log", "dt_bias"):
+        d[n] = torch.from_numpy(inp[n]).to(dev)
+    d["state"] = None if inp["state"] is None else torch.from_numpy(inp["state"]).to(dev)
+    if "cu_seqlens" in inp:
+        d["cu_seqlens"] = torch.from_numpy(inp["cu_seqlens"]).to(dev).to(cu_dtype)
+    d["scale"] = inp["scale"]
+    return d
+
+
+def _prefill(d, dev, in_place=False, **kw):
+    T = d["q"].shape[0]
+    N = d["cu_seqlens"].numel() - 1
+    out = torch.empty((T, 8, 128), dtype=torch.bfloat16, device=dev)
+    ns = d["state"] if in_place else torch.empty((N, 8, 128, 128), dtype=torch.float32,
+                                                 device=dev)
+    prefill.kernel(d["q"], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"],
+                   d["b"], d["cu_seqlens"], d["scale"], out, ns, **kw)
+    torch.cuda.synchronize()
+    return out, ns
+
+
+def _check(out, ns, inp, tight=False):
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o = out.float().cpu().numpy()
+    s = ns.cpu().numpy()
+    assert_output_close(o, o_ref)
+    assert_state_close(s, s_ref)
+    if tight:
+        assert_state_close(s, s_ref, rel_atol=1e-5, what="state (f32 sequential bound)")
+
+
+# Short batches: every sequence is at most the built-in routing length, so the
+# whole call is the token-sequential kernel.
+SHORT_CASES = [
+    ([1], True), ([2], False), ([16], True), ([63], True), ([64], False), ([65], True),
+    ([200], True), ([256], True), ([6, 49, 61], True), ([0, 5, 0, 100], True), ([0], True),
+    ([1] * 40, True), ([3, 0, 7, 250], False),
+]
+
+
+@pytest.mark.parametrize("lens, with_state", SHORT_CASES)
+def test_short_prefill_matches_oracle(cuda_device, lens, with_state):
+    print(f"short prefill lens={lens if len(lens) < 8 else f'{len(lens)}x{lens[0]}'} "
+          f"state={with_state}", flush=True)
+    inp = O.make_prefill_inputs(lens, seed=7 + len(lens), with_state=with_state)
+    out, ns = _prefill(_to_dev(inp, cuda_device), cuda_device)
+    _check(out, ns, inp, tight=True)
+
+
+def test_short_prefill_int32_cu_and_in_place(cuda_device):
+    lens = [6, 49, 0, 61]
+    inp = O.make_prefill_inputs(lens, seed=12)
+    d = _to_dev(inp, cuda_device, cu_dtype=torch.int32)
+    out, ns = _prefill(d, cuda_device, in_place=True)
+    assert ns.data_ptr() == d["state"].data_ptr()
+    _check(out, ns, inp, tight=True)
+
+
+# configs[3] lengths, routed three ways: a mix (short ones token by token,
+# long ones through the chunks), all chunked, all token by token.
+@pytest.mark.parametrize("rec_max", [64, 300, -2, 4096, 0])
+def test_routing_of_a_mixed_batch(cuda_device, rec_max):
+    lens = [6, 49, 294, 1800, 2040, 61]
+    print(f"routing rec_max={rec_max}", flush=True)
+    inp = O.make_prefill_inputs(lens, seed=3)
+    out, ns = _prefill(_to_dev(inp, cuda_device), cuda_device, recurrent_max_len=rec_max)
+    _check(out, ns, inp)
+
+
+def test_routing_zero_length_sequences_get_zero_state(cuda_device):
+    lens = [0, 300, 0, 20, 0]
+    inp = O.make_prefill_inputs(lens, seed=13)
+    for rec_max in (-2, -1, 0, 64):
+        out, ns = _prefill(_to_dev(inp, cuda_device), cuda_device, recurrent_max_len=rec_max)
+        s = ns.cpu().numpy()
+        assert not s[[0, 2, 4]].any(), f"rec_max={rec_max}"
+        _check(out, ns, inp)
+
+
+def test_recurrent_tilings_are_identical(cuda_device):
+    lens = [6, 49, 200, 1]
+    inp = O.make_prefill_inputs(lens, seed=14)
+    d = _to_dev(inp, cuda_device)
+    ref_o, ref_s = _prefill(d, cuda_device, recurrent_variant=0)
+    _check(ref_o, ref_s, inp, tight=True)
+    for var in range(1, 10):
+        o, s = _prefill(d, cuda_device, recurrent_variant=var)
+        assert torch.equal(o, ref_o), f"tiling {var}: output differs"
+        assert torch.equal(s, ref_s), f"tiling {var}: state differs"
+
+
+# ---------------------------------------------------------------------------
+# multi-token decode
+# ---------------------------------------------------------------------------
+
+def _multi_inputs(B, T, seed, with_state=True):
+    """[B, T, ...] decode inputs and the same data as a packed prefill batch
+    of B sequences of T tokens (the oracle's form)."""
+    inp = O.make_prefill_inputs([T] * B, seed=seed, with_state=with_state)
+    dec = dict(inp)
+    for n, tail in (("q", (4, 128)), ("k", (4, 128)), ("v", (8, 128)), ("a", (8,)),
+                    ("b", (8,))):
+        dec[n] = inp[n].reshape((B, T) + tail)
+    del dec["cu_seqlens"]
+    return inp, dec
+
+
+def _decode_multi(d, B, T, dev, in_place=False, variant=-1):
+    out = torch.empty((B, T, 8, 128), dtype=torch.bfloat16, device=dev)
+    ns = d["state"] if in_place else torch.empty((B, 8, 128, 128), dtype=torch.float32,
+                                                 device=dev)
+    decode.kernel(d["q"], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"], d["b"],
+                  d["scale"], out, ns, variant=variant)
+    torch.cuda.synchronize()
+    return out, ns
+
+
+@pytest.mark.parametrize("B, T", [(1, 2), (3, 5), (16, 4), (64, 2), (64, 8)])
+def test_multi_token_decode_matches_oracle(cuda_device, B, T):
+    print(f"multi-token decode B={B} T={T}", flush=True)
+    inp, dec = _multi_inputs(B, T, seed=20 + B + T)
+    out, ns = _decode_multi(_to_dev(dec, cuda_device), B, T, cuda_device)
+    _check(out.reshape(B * T, 8, 128), ns, inp, tight=True)
+
+
+def test_multi_token_decode_equals_successive_steps(cuda_device):
+    B, T = 8, 4
+    inp, dec = _multi_inputs(B, T, seed=31)
+    d = _to_dev(dec, cuda_device)
+    out, ns = _decode_multi(d, B, T, cuda_device)
+    state = d["state"].clone()
+    for t in range(T):
+        o1 = torch.empty((B, 1, 8, 128), dtype=torch.bfloat16, device=cuda_device)
+        s1 = torch.empty_like(state)
+        sl = slice(t, t + 1)
+        decode.kernel(d["q"][:, sl].contiguous(), d["k"][:, sl].contiguous(),
+                      d["v"][:, sl].contiguous(), state, d["A_log"], d["a"][:, sl].contiguous(),
+                      d["dt_bias"], d["b"][:, sl].contiguous(), d["scale"], o1, s1)
+        assert_output_close(out[:, sl].float().cpu().numpy(), o1.float().cpu().numpy(),
+                            atol=1e-2, rtol=1e-2, what=f"token {t}")
+        state = s1
+    torch.cuda.synchronize()
+    assert_state_close(ns.cpu().numpy(), state.cpu().numpy(), rel_atol=1e-5)
+
+
+def test_multi_token_decode_in_place_and_no_state(cuda_device):
+    B, T = 4, 3
+    inp, dec = _multi_inputs(B, T, seed=32)
+    d = _to_dev(dec, cuda_device)
+    out, ns = _decode_multi(d, B, T, cuda_device, in_place=True)
+    assert ns.data_ptr() == d["state"].data_ptr()
+    _check(out.reshape(B * T, 8, 128), ns, inp, tight=True)
+    inp0, dec0 = _multi_inputs(B, T, seed=33, with_state=False)
+    out0, ns0 = _decode_multi(_to_dev(dec0, cuda_device), B, T, cuda_device)
+    _check(out0.reshape(B * T, 8, 128), ns0, inp0, tight=True)
+
+
+def test_multi_token_decode_tilings_are_identical(cuda_device):
+    B, T = 5, 3
+    inp, dec = _multi_inputs(B, T, seed=34)
+    d = _to_dev(dec, cuda_device)
+    ref_o, ref_s = _decode_multi(d, B, T, cuda_device, variant=0)
+    for var in range(1, 10):
+        o, s = _decode_multi(d, B, T, cuda_device, variant=var)
+        assert torch.equal(o, ref_o) and torch.equal(s, ref_s), f"tiling {var}"
+    _check(ref_o.reshape(B * T, 8, 128), ref_s, inp, tight=True)
