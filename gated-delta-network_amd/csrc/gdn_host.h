@@ -5,6 +5,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+
 #include "gdn_amd.h"
 
 namespace gdn {
@@ -32,13 +33,14 @@ inline bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
 
 // Token-sequential recurrence (gdn_recurrent.hip) over num_seqs sequences:
 // packed by cu (int32/int64 on the device) or, with cu == nullptr, of
-// fixed_len tokens each.  Sequences longer than max_len are left untouched.
-// variant: row tiling index, -1 = built-in.  Error messages start with `what`.
+// fixed_len tokens each.  With a non-null `enable`, the kernel does nothing
+// unless *enable (on the device) is non-zero.  variant: row tiling index, -1 =
+// built-in.  Error messages start with `what`.
 int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
                      const float *A_log, const uint16_t *a, const float *dt_bias,
                      const uint16_t *b, const void *cu, int cu64, int num_seqs, int T,
-                     int fixed_len, int max_len, float scale, uint16_t *out, float *new_state,
-                     hipStream_t stream, int variant, const char *what);
+                     int fixed_len, const int *enable, float scale, uint16_t *out,
+                     float *new_state, hipStream_t stream, int variant, const char *what);
 int recurrent_num_variants();
 
 }  // namespace gdn

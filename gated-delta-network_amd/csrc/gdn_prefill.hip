@@ -71,7 +71,7 @@ static PrefillLayout prefill_layout(int T, int N) {
   };
   const size_t n = static_cast<size_t>(nt);
   L.chunks = take(n * sizeof(int4));
-  L.offsets = take((static_cast<size_t>(N) + 1) * sizeof(int));
+  L.offsets = take((static_cast<size_t>(N) + 2) * sizeof(int));  // + the path flag
   L.G = take(n * kHV * kChunk * 4);
   L.dcy = take(n * kHV * kChunk * 4);
   L.eg = take(n * kHV * 4);
@@ -89,24 +89,53 @@ static PrefillLayout prefill_layout(int T, int N) {
 // number within the sequence} for c < NT, {-1, 0, 0, 0} up to nt_max;
 // offsets[s] = first chunk of sequence s, offsets[N] = NT.  Token bounds are
 // clamped to [0, T] and the chunk count to nt_max, so a malformed cu_seqlens
-// cannot send any later kernel out of bounds.  A sequence of at most rec_max
-// tokens gets no chunks (the token-sequential kernel owns it); rec_max < 0
-// routes every sequence through the chunks.
+// cannot send any later kernel out of bounds.
+//
+// Path choice (choose != 0): the token-sequential kernel takes the whole batch
+// when choose == 1 and no sequence is longer than rec_max tokens, or when
+// choose == 2 and the cost model below favours it.  Then every sequence gets
+// zero chunks and the path flag offsets[N + 1] is 1 (else 0).
+// Cost model (microseconds, fitted on MI355X): token by token
+//   0.24 * longest + 0.024 * T + 0.17 * N      (serial tokens, VALU work, state traffic)
+// chunked
+//   20 + 1.05 * ceil(longest / 64) + 1.05 * N  (fixed launches, serial chunks, per-sequence work)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int cu64, int N, int T,
-                                                              int nt_max, int rec_max,
+                                                              int nt_max, int choose, int rec_max,
                                                               int4 *chunks, int *offsets) {
   __shared__ int s_incl[1024];
+  __shared__ int s_longest;
   const int tid = threadIdx.x;
+  if (tid == 0) s_longest = 0;
+  __syncthreads();
+  if (choose != 0) {
+    int longest = 0;
+    for (int s = tid; s < N; s += 1024) {
+      const int len = load_cu(cu, cu64, s + 1, T) - load_cu(cu, cu64, s, T);
+      longest = len > longest ? len : longest;
+    }
+    atomicMax(&s_longest, longest);
+  }
+  __syncthreads();
+  bool sequential = false;
+  if (choose == 1) {
+    sequential = s_longest <= rec_max;
+  } else if (choose == 2) {
+    const float L = static_cast<float>(s_longest);
+    const float by_token = 0.24f * L + 0.024f * static_cast<float>(T) + 0.17f * static_cast<float>(N);
+    const float by_chunk = 20.0f + 1.05f * ceilf(L / kChunk) + 1.05f * static_cast<float>(N);
+    sequential = by_token <= by_chunk;
+  }
+  if (tid == 0) offsets[N + 1] = sequential ? 1 : 0;
   long long carry = 0;
   for (int base = 0; base < N; base += 1024) {
     const int s = base + tid;
     int n = 0;
-    if (s < N) {
+    if (s < N && !sequential) {
       const int bos = load_cu(cu, cu64, s, T);
       int eos = load_cu(cu, cu64, s + 1, T);
       eos = eos < bos ? bos : eos;
-      n = eos - bos > rec_max ? (eos - bos + kChunk - 1) / kChunk : 0;
+      n = (eos - bos + kChunk - 1) / kChunk;
     }
     s_incl[tid] = n;
     __syncthreads();
@@ -464,7 +493,7 @@ template <int BV>
 __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
     const float *state, float *new_state, const int *offsets, const float *ws_dcy,
     const float *ws_eg, const uint16_t *ws_w, const float *ws_u,
-    const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt, int skip_empty) {
+    const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt, int N) {
   constexpr int NVB = kDV / BV;
   const int h = blockIdx.x % kHV;
   const int rest = blockIdx.x / kHV;
@@ -482,7 +511,7 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
 
   const int c0 = offsets[s];
   const int nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
-  if (nch == 0 && skip_empty) return;  // owned by the token-sequential kernel
+  if (offsets[N + 1]) return;  // the token-sequential kernel owns the batch
   const size_t sbase = (static_cast<size_t>(s) * kHV + h) * kDV * kDK;  // [V][K]
 
   f32x4 S[2];
@@ -708,10 +737,14 @@ __global__ __launch_bounds__(256) void prefill_output_kernel(
   }
 }
 
-// Sequences of at most this many tokens take the token-sequential kernel
-// (gdn_recurrent.hip) instead of the chunked pipeline; from a length sweep of
-// both paths on MI355X.
-constexpr int kRecurrentMaxLen = 256;
+// Path choice between the token-sequential kernel (gdn_recurrent.hip) and the
+// chunk pipeline, from a sweep of both on MI355X.  A batch of at most
+// kRecurrentMaxLen tokens runs token by token (one sequence of 64 tokens:
+// 18.6 us vs 25.9 us chunked; of 128: 33.7 vs 27.9 us).  Batches with a mean
+// sequence length above kCandidateMeanLen always take the chunks; the others
+// are decided on the device from their longest sequence (index kernel).
+constexpr int kRecurrentMaxLen = 96;
+constexpr int kCandidateMeanLen = 32;
 
 static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                           const float *state, const float *A_log, const gdn_bf16 *a,
@@ -781,22 +814,37 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   uint16_t *ht = reinterpret_cast<uint16_t *>(ws + L.ht);
   uint16_t *vnt = reinterpret_cast<uint16_t *>(ws + L.vnt);
 
-  // Routing by sequence length (on the device): at most rmax tokens -> the
-  // token-sequential kernel, longer -> the chunked pipeline.  rmax < 0: all
-  // chunked.  When T <= rmax every sequence is short and no chunk work is
-  // launched at all; with one sequence longer than rmax nothing is short.
-  const int rmax = rec_max == -1 ? kRecurrentMaxLen : (rec_max == -2 ? -1 : rec_max);
-  if (rmax >= T)
-    return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0, rmax,
-                            scale, output, new_state, stream, rec_variant, "gdn_prefill_fwd");
-
+  // Path choice: the whole batch runs token by token (one launch) or through
+  // the chunk pipeline.  Decided on the host when T and N settle it, else on
+  // the device by the index kernel, which then sets the path flag read by the
+  // token-sequential and state kernels (and leaves the chunk table empty).
+  //   rec_max >= 0 (explicit): token by token iff the longest sequence has at
+  //                            most rec_max tokens;
+  //   rec_max == -2:           always chunks;
+  //   rec_max == -1 (built in): token by token if T <= kRecurrentMaxLen; chunks
+  //                            for one longer sequence or a mean length above
+  //                            kCandidateMeanLen; else the device cost model.
+  int choose = 0;  // 0 chunks, 1 by rec_max, 2 by cost model
+  bool host_sequential = false;
+  if (rec_max >= 0) {
+    host_sequential = rec_max >= T;
+    choose = N > 1 ? 1 : 0;
+  } else if (rec_max == -1) {
+    host_sequential = T <= kRecurrentMaxLen;
+    choose = (N > 1 && static_cast<long long>(T) <= static_cast<long long>(kCandidateMeanLen) * N) ? 2 : 0;
+  }
+  if (host_sequential)
+    return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
+                            nullptr, scale, output, new_state, stream, rec_variant,
+                            "gdn_prefill_fwd");
   hipLaunchKernelGGL(prefill_index_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, cu64, N, T,
-                     L.nt_max, rmax, chunks, offsets);
+                     L.nt_max, choose, rec_max, chunks, offsets);
   int rc = check_launch("gdn_prefill_fwd(index)");
   if (rc) return rc;
-  if (rmax >= 0 && N > 1) {
-    rc = recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0, rmax,
-                          scale, output, new_state, stream, rec_variant, "gdn_prefill_fwd");
+  if (choose != 0) {
+    rc = recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
+                          offsets + N + 1, scale, output, new_state, stream, rec_variant,
+                          "gdn_prefill_fwd");
     if (rc) return rc;
   }
   if (L.nt_max > 0) {
@@ -807,13 +855,12 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   const int bv = variant == 1 ? 32 : 16;  // 16 measured faster at every size
   const long long blocks = static_cast<long long>(N) * kHV * (kDV / bv);
   if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
-  const int skip_empty = rmax >= 0 ? 1 : 0;
   if (bv == 32)
     hipLaunchKernelGGL(prefill_state_kernel<32>, dim3(static_cast<unsigned>(blocks)), dim3(512), 0,
-                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, skip_empty);
+                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N);
   else
     hipLaunchKernelGGL(prefill_state_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, skip_empty);
+                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N);
   if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
   if (L.nt_max > 0) {
     hipLaunchKernelGGL(prefill_output_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, q, k, chunks,

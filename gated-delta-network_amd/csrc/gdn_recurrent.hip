@@ -9,10 +9,11 @@
 //                       S[r,:] = g S[r,:] + v_new k_t
 //                       o_t[r] = scale <S[r,:], q_t> = scale (g <S_old[r],q_t> + v_new <k_t,q_t>)
 // with q/k head h/2 (GVA without copies).  It serves
-//   * prefill of short sequences, where the chunked pipeline's fixed cost
-//     (four dependent launches, a full chunk of work per sequence) dominates:
-//     the sequential-scan / chunked crossover of OPTIMIZATION_LOG.md:79,
-//     170-184, dispatched per sequence on the device by its length;
+//   * prefill of batches of short sequences, where the chunked pipeline's
+//     fixed cost (four dependent launches, a full chunk of work per sequence)
+//     dominates: the sequential-scan / chunked crossover of
+//     OPTIMIZATION_LOG.md:79,170-184, chosen on the device from the longest
+//     sequence of the batch;
 //   * decode of T > 1 tokens per batch row (multi-token / speculative decode),
 //     a fixed-length batch [B, T, ...] that is exactly the packed layout.
 //
@@ -21,8 +22,9 @@
 // 4c..4c+3 and 64+4c..64+4c+3), so the two row dot products per token are 8
 // FMAs and 4 DPP adds.  A workgroup of WAVES waves owns 4*WAVES*PASSES rows.
 // Per token each lane loads its 8 columns of k and q (two 8-byte loads each)
-// and one bf16 of v per pass, one token ahead of use; the gating of 64 tokens
-// is computed at once, one token per lane, and read back with readlane.
+// and one bf16 of v per pass, 2-8 tokens ahead of use (a register ring); the
+// gating of a ring turn's tokens is computed at once, one token per lane, and
+// read back with readlane.
 #include "gdn_device.h"
 #include "gdn_host.h"
 
@@ -40,17 +42,17 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
     const uint16_t *__restrict__ v, const float *state, const float *__restrict__ A_log,
     const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
     const uint16_t *__restrict__ b, const void *__restrict__ cu, int cu64, int T, int fixed_len,
-    int max_len, float scale, uint16_t *__restrict__ out, float *new_state) {
+    const int *__restrict__ enable, float scale, uint16_t *__restrict__ out, float *new_state) {
   constexpr int kRows = 4 * WAVES * PASSES;
   constexpr int kTiles = kDV / kRows;
   static_assert(kDV % kRows == 0, "row block must divide 128");
 
+  if (enable != nullptr && *enable == 0) return;  // the batch went through the chunks
   const int h = blockIdx.x % kHV;  // consecutive workgroups: the 8 heads
   const int rest = blockIdx.x / kHV;
   const int tile = rest % kTiles, s = rest / kTiles;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c4 = 4 * (lane & 15);
-  const bool leader = (lane & 15) == 0;
   const int row0 = tile * kRows + wave * 4 * PASSES + (lane >> 4);  // pass p: row0 + 4p
 
   int bos, len;
@@ -62,8 +64,6 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
     bos = s * fixed_len;
     len = fixed_len;
   }
-  if (len > max_len) return;  // a longer sequence goes through the chunked pipeline
-
   const int hq = h >> 1;
   const size_t sbase = (static_cast<size_t>(s) * kHV + h) * kDV * kDK;
   f32x4 Sa[PASSES], Sb[PASSES];  // columns c4.. and 64 + c4..
@@ -95,57 +95,94 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
       for (int p = 0; p < PASSES; ++p) x.v[p] = vp[4 * p];
     };
 
-    TokenIn<PASSES> cur, nxt;
-    load_token(0, cur);
-    for (int t0 = 0; t0 < len; t0 += 64) {
-      // Gating of tokens t0 .. t0+63, token t0 + lane in this lane.
-      float gl = 1.f, bl = 0.f;
-      if (t0 + lane < len) {
-        const size_t tok = static_cast<size_t>(bos) + t0 + lane;
-        gl = expf(-rate * softplus20(bf16_to_f32(a[tok * kHV + h]) + dtb));
-        bl = sigmoidf_(bf16_to_f32(b[tok * kHV + h]));
+    // One token: x holds its k, q, v; (g, beta) its gating.  Every lane of a
+    // row group holds the row's o, so all 16 store the same two bytes (one
+    // coalesced write) and no lane needs a branch.
+    auto step = [&](const TokenIn<PASSES> &x, int t, float g, float beta) {
+      float kf[8], qf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kf[e] = bf16_to_f32(x.k0[e]);
+        kf[4 + e] = bf16_to_f32(x.k1[e]);
+        qf[e] = bf16_to_f32(x.q0[e]);
+        qf[4 + e] = bf16_to_f32(x.q1[e]);
       }
-      const int n = len - t0 < 64 ? len - t0 : 64;
-      for (int i = 0; i < n; ++i) {
-        const int t = t0 + i;
-        load_token(t + 1 < len ? t + 1 : t, nxt);  // next token, clamped
-        const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gl), i));
-        const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bl), i));
-        float kf[8], qf[8];
+      float pkq = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pkq = fmaf(kf[e], qf[e], pkq);
+      const float kq = row16_sum(pkq);
+      uint16_t *op = out + ((static_cast<size_t>(bos) + t) * kHV + h) * kDV + row0;
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) {
+        float sk0 = 0.f, sk1 = 0.f, sq0 = 0.f, sq1 = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          kf[e] = bf16_to_f32(cur.k0[e]);
-          kf[4 + e] = bf16_to_f32(cur.k1[e]);
-          qf[e] = bf16_to_f32(cur.q0[e]);
-          qf[4 + e] = bf16_to_f32(cur.q1[e]);
+          sk0 = fmaf(Sa[p][e], kf[e], sk0);
+          sk1 = fmaf(Sb[p][e], kf[4 + e], sk1);
+          sq0 = fmaf(Sa[p][e], qf[e], sq0);
+          sq1 = fmaf(Sb[p][e], qf[4 + e], sq1);
         }
-        float pkq = 0.f;
+        const float sk = row16_sum(sk0 + sk1);
+        const float sq = row16_sum(sq0 + sq1);
+        const float vn = beta * (bf16_to_f32(x.v[p]) - g * sk);
+        const float o = scale * fmaf(g, sq, vn * kq);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pkq = fmaf(kf[e], qf[e], pkq);
-        const float kq = row16_sum(pkq);
-        uint16_t *op = out + ((static_cast<size_t>(bos) + t) * kHV + h) * kDV + row0;
-#pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-          float sk0 = 0.f, sk1 = 0.f, sq0 = 0.f, sq1 = 0.f;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            sk0 = fmaf(Sa[p][e], kf[e], sk0);
-            sk1 = fmaf(Sb[p][e], kf[4 + e], sk1);
-            sq0 = fmaf(Sa[p][e], qf[e], sq0);
-            sq1 = fmaf(Sb[p][e], qf[4 + e], sq1);
-          }
-          const float sk = row16_sum(sk0 + sk1);
-          const float sq = row16_sum(sq0 + sq1);
-          const float vn = beta * (bf16_to_f32(cur.v[p]) - g * sk);
-          const float o = scale * fmaf(g, sq, vn * kq);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            Sa[p][e] = fmaf(vn, kf[e], g * Sa[p][e]);
-            Sb[p][e] = fmaf(vn, kf[4 + e], g * Sb[p][e]);
-          }
-          if (leader) op[4 * p] = f32_to_bf16(o);
+        for (int e = 0; e < 4; ++e) {
+          Sa[p][e] = fmaf(vn, kf[e], g * Sa[p][e]);
+          Sb[p][e] = fmaf(vn, kf[4 + e], g * Sb[p][e]);
         }
-        cur = nxt;
+        op[4 * p] = f32_to_bf16(o);
+      }
+    };
+
+    // Everything is loaded ahead of use by unconditional loads (indices past
+    // the end are clamped to the last token), so the compiler can wait for
+    // exactly the data in use: token t sits in ring slot t % kDepth, refilled
+    // with token t + kDepth right after use, and the raw gating inputs of a
+    // ring turn arrive one turn ahead.  The main loop runs whole turns as
+    // straight-line code (no branch, so the pending-load bookkeeping at its
+    // header is exact); the last len % kDepth tokens follow it.
+    constexpr int kDepth = PASSES <= 2 ? 8 : (PASSES <= 4 ? 4 : 2);
+    const int last = len - 1;
+    auto gate_idx = [&](int t0) {  // gating input of token t0 + lane (clamped)
+      const int t = t0 + (lane & (kDepth - 1));
+      return (static_cast<size_t>(bos) + (t < last ? t : last)) * kHV + h;
+    };
+    uint16_t a_raw = a[gate_idx(0)], b_raw = b[gate_idx(0)];
+    TokenIn<PASSES> ring[kDepth];
+#pragma unroll
+    for (int r = 0; r < kDepth; ++r) load_token(r < last ? r : last, ring[r]);
+    // Gating of the turn's tokens, token t0 + (lane % kDepth) in each lane.
+    auto gate = [&](float &gl, float &bl) {
+      gl = expf(-rate * softplus20(bf16_to_f32(a_raw) + dtb));
+      bl = sigmoidf_(bf16_to_f32(b_raw));
+    };
+    const int full = len - len % kDepth;
+    int t0 = 0;
+    for (; t0 < full; t0 += kDepth) {
+      float gl, bl;
+      gate(gl, bl);
+      a_raw = a[gate_idx(t0 + kDepth)];
+      b_raw = b[gate_idx(t0 + kDepth)];
+#pragma unroll
+      for (int r = 0; r < kDepth; ++r) {
+        const int t = t0 + r;
+        const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gl), r));
+        const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bl), r));
+        step(ring[r], t, g, beta);
+        load_token(t + kDepth < last ? t + kDepth : last, ring[r]);
+      }
+    }
+    if (t0 < len) {  // the remaining len - full tokens, already in slots 0..
+      float gl, bl;
+      gate(gl, bl);
+#pragma unroll
+      for (int r = 0; r < kDepth - 1; ++r) {
+        if (t0 + r < len) {
+          const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gl), r));
+          const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bl), r));
+          step(ring[r], t0 + r, g, beta);
+        }
       }
     }
   }
@@ -173,33 +210,31 @@ template <int W, int P>
 void launch_rec(long long groups, hipStream_t stream, const uint16_t *q, const uint16_t *k,
                 const uint16_t *v, const float *state, const float *A_log, const uint16_t *a,
                 const float *dt_bias, const uint16_t *b, const void *cu, int cu64, int T,
-                int fixed_len, int max_len, float scale, uint16_t *out, float *new_state) {
+                int fixed_len, const int *enable, float scale, uint16_t *out, float *new_state) {
   const long long blocks = groups * (kDV / (4 * W * P));
   hipLaunchKernelGGL((recurrent_kernel<W, P>), dim3(static_cast<unsigned>(blocks)), dim3(64 * W),
                      0, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T, fixed_len,
-                     max_len, scale, out, new_state);
+                     enable, scale, out, new_state);
 }
 
 }  // namespace
 
 int recurrent_num_variants() { return kNumRecVariants; }
 
-// Built-in tiling: few (sequence, head) groups -> small row blocks, so that
-// more workgroups share the serial token loop; many -> larger blocks.
+// Built-in tiling from a sweep on MI355X: few (sequence, head) groups -> the
+// smallest row blocks (the serial token loop is spread over the most waves);
+// many -> 64-row blocks (fewer waves repeat the per-token overhead).
 int recurrent_default_variant(long long groups) {
-  if (groups <= 64) return 2;    // 16 rows, 4 waves
-  if (groups <= 512) return 5;   // 32 rows, 4 waves
+  if (groups <= 32) return 0;    // 4 rows, 1 wave
+  if (groups <= 128) return 5;   // 32 rows, 4 waves
   return 7;                      // 64 rows, 4 waves
 }
 
-// Launches the recurrence over `num_groups` = sequences (or batch rows) x 8
-// heads.  cu == nullptr means fixed-length sequences [s*fixed_len, ...).
-// Sequences longer than max_len are skipped (left to the chunked pipeline).
 int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
                      const float *A_log, const uint16_t *a, const float *dt_bias,
                      const uint16_t *b, const void *cu, int cu64, int num_seqs, int T,
-                     int fixed_len, int max_len, float scale, uint16_t *out, float *new_state,
-                     hipStream_t stream, int variant, const char *what) {
+                     int fixed_len, const int *enable, float scale, uint16_t *out,
+                     float *new_state, hipStream_t stream, int variant, const char *what) {
   const long long groups = static_cast<long long>(num_seqs) * kHV;
   if (variant < 0) variant = recurrent_default_variant(groups);
   if (variant >= kNumRecVariants)
@@ -210,7 +245,7 @@ int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, co
 #define GDN_REC(W, P)                                                                          \
   if (rv.waves == W && rv.passes == P)                                                        \
     launch_rec<W, P>(groups, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T,       \
-                     fixed_len, max_len, scale, out, new_state);
+                     fixed_len, enable, scale, out, new_state);
   GDN_REC(1, 1)
   GDN_REC(2, 1)
   GDN_REC(4, 1)
@@ -271,6 +306,6 @@ extern "C" int gdn_decode_multi_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const 
     return gdn_decode_fwd(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
                           stream);
   return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, nullptr, 0, batch,
-                          static_cast<int>(total), tokens, 0x7fffffff, scale, output, new_state,
+                          static_cast<int>(total), tokens, nullptr, scale, output, new_state,
                           static_cast<hipStream_t>(stream), variant, "gdn_decode_multi_fwd");
 }

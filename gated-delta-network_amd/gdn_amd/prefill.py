@@ -110,8 +110,9 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
     ``variant`` picks the state-recurrence tiling (gdn_prefill_fwd_variant);
     the default is the built-in one.  ``workspace``: a caller-owned uint8
     buffer (``alloc_workspace``) used instead of the per-stream cache.
-    ``recurrent_max_len``: sequences of at most this many tokens run token by
-    token instead of through the chunks (-1 built-in, -2 never);
+    ``recurrent_max_len``: a batch whose longest sequence has at most this
+    many tokens runs token by token instead of through the chunks (-1
+    built-in, -2 never);
     ``recurrent_variant``: that kernel's row tiling (gdn_prefill_fwd_tuned).
     """
     lib = _lib.load()

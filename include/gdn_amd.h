@@ -130,9 +130,12 @@ size_t gdn_prefill_workspace_bytes(int total_tokens, int num_seqs);
  * sequence gets an all-zero new_state, as the reference does.  new_state may
  * alias state; output must not overlap any input.
  *
- * Each sequence is routed on the device by its length: short ones (up to a
- * built-in length) run token by token with the state in registers, the others
- * through the chunk-64 pipeline; results agree within the stated tolerance
+ * The batch takes one of two paths: every sequence token by token with the
+ * state in registers (one launch), or all through the chunk-64 pipeline.  A
+ * batch of at most 96 tokens goes token by token; one with a mean sequence
+ * length above 32 tokens through the chunks; for the others (many short
+ * sequences) the device compares a cost model of both paths, evaluated from
+ * the longest sequence, T and N.  Results agree within the stated tolerance
  * either way (the reference measured the same crossover between its
  * sequential scan and chunked kernels, OPTIMIZATION_LOG.md:79,170-184).
  */
@@ -150,8 +153,8 @@ int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
  * sharing each SIMD), -1 = the built-in choice (what gdn_prefill_fwd uses).  The counterpart of the reference's autotuned
  * BV of chunk_gated_delta_rule_fwd_kernel_h (solutions/
  * gdn_prefill_qk4_v8_d128_k_last/solution/triton/fla_kernels.py:407-426,
- * 1028-1035).  Results are identical for every variant (sequences routed
- * to the token-sequential kernel do not depend on it).
+ * 1028-1035).  Results are identical for every variant (a batch that runs
+ * token by token does not depend on it).
  */
 int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                             const float *state, const float *A_log, const gdn_bf16 *a,
@@ -163,8 +166,9 @@ int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16
 /*
  * gdn_prefill_fwd with every tuning choice explicit (for sweeps and tests):
  *   state_tiling       as the variant of gdn_prefill_fwd_variant (-1 built-in)
- *   recurrent_max_len  sequences of at most this many tokens run token by
- *                      token; -1 = built-in, -2 = none (all chunked)
+ *   recurrent_max_len  a batch whose longest sequence has at most this many
+ *                      tokens runs token by token; -1 = built-in, -2 = never
+ *                      (always chunked)
  *   recurrent_tiling   as the variant of gdn_decode_multi_fwd (-1 built-in)
  */
 int gdn_prefill_fwd_tuned(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,

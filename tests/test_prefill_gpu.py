@@ -270,7 +270,7 @@ def _layout(T, N):
         off = (off + nbytes + 255) // 256 * 256
 
     take("chunks", nt * 16)
-    take("offsets", (N + 1) * 4)
+    take("offsets", (N + 2) * 4)  # offsets[0..N], then the path flag
     take("G", nt * 8 * 64 * 4)
     take("dcy", nt * 8 * 64 * 4)
     take("eg", nt * 8 * 4)

@@ -1,5 +1,7 @@
-"""The token-sequential kernel on the GPU: short-sequence prefill (routed per
-sequence by length), the routing itself, and multi-token decode (T > 1).
+"""The token-sequential kernel on the GPU: prefill of batches of short
+sequences (the path chosen from the longest sequence, on the host when T
+decides it, else on the device), the path choice itself, and multi-token
+decode (T > 1).
 
 Oracle: the sequential recurrence of reference/gdn_prefill_ref.py:71-89
 (oracle/gdn_seq.c through O.prefill_seq_c, pinned in tests/test_oracle.py).
@@ -7,6 +9,8 @@ Tolerance as everywhere (conftest.py): bf16 output atol = rtol = 1e-2; f32
 state atol = 1e-3 * max|state_ref|.  The token-sequential kernel computes in
 f32 in the reference's order, so its state is also held to 1e-5 * max|ref|.
 """
+
+import math
 
 import numpy as np
 import pytest
@@ -55,8 +59,9 @@ def _check(out, ns, inp, tight=False):
         assert_state_close(s, s_ref, rel_atol=1e-5, what="state (f32 sequential bound)")
 
 
-# Short batches: every sequence is at most the built-in routing length, so the
-# whole call is the token-sequential kernel.
+# The whole call through the token-sequential kernel (routing length above T).
+ALL_SEQUENTIAL = 1 << 30
+
 SHORT_CASES = [
     ([1], True), ([2], False), ([16], True), ([63], True), ([64], False), ([65], True),
     ([200], True), ([256], True), ([6, 49, 61], True), ([0, 5, 0, 100], True), ([0], True),
@@ -69,7 +74,7 @@ def test_short_prefill_matches_oracle(cuda_device, lens, with_state):
     print(f"short prefill lens={lens if len(lens) < 8 else f'{len(lens)}x{lens[0]}'} "
           f"state={with_state}", flush=True)
     inp = O.make_prefill_inputs(lens, seed=7 + len(lens), with_state=with_state)
-    out, ns = _prefill(_to_dev(inp, cuda_device), cuda_device)
+    out, ns = _prefill(_to_dev(inp, cuda_device), cuda_device, recurrent_max_len=ALL_SEQUENTIAL)
     _check(out, ns, inp, tight=True)
 
 
@@ -77,15 +82,16 @@ def test_short_prefill_int32_cu_and_in_place(cuda_device):
     lens = [6, 49, 0, 61]
     inp = O.make_prefill_inputs(lens, seed=12)
     d = _to_dev(inp, cuda_device, cu_dtype=torch.int32)
-    out, ns = _prefill(d, cuda_device, in_place=True)
+    out, ns = _prefill(d, cuda_device, in_place=True, recurrent_max_len=ALL_SEQUENTIAL)
     assert ns.data_ptr() == d["state"].data_ptr()
     _check(out, ns, inp, tight=True)
 
 
-# configs[3] lengths, routed three ways: a mix (short ones token by token,
-# long ones through the chunks), all chunked, all token by token.
-@pytest.mark.parametrize("rec_max", [64, 300, -2, 4096, 0])
-def test_routing_of_a_mixed_batch(cuda_device, rec_max):
+# configs[3] lengths under several path lengths: chunked (-1 = built-in, 64,
+# 300, -2 = never sequential, 0), token by token decided on the device (4096:
+# longest 2040 <= 4096 < T) and on the host (ALL_SEQUENTIAL >= T).
+@pytest.mark.parametrize("rec_max", [-1, 64, 300, -2, 4096, 0, ALL_SEQUENTIAL])
+def test_path_choice_on_configs3(cuda_device, rec_max):
     lens = [6, 49, 294, 1800, 2040, 61]
     print(f"routing rec_max={rec_max}", flush=True)
     inp = O.make_prefill_inputs(lens, seed=3)
@@ -96,21 +102,69 @@ def test_routing_of_a_mixed_batch(cuda_device, rec_max):
 def test_routing_zero_length_sequences_get_zero_state(cuda_device):
     lens = [0, 300, 0, 20, 0]
     inp = O.make_prefill_inputs(lens, seed=13)
-    for rec_max in (-2, -1, 0, 64):
+    for rec_max in (-2, -1, 0, 64, 310):  # 310: sequential, decided on the device
         out, ns = _prefill(_to_dev(inp, cuda_device), cuda_device, recurrent_max_len=rec_max)
         s = ns.cpu().numpy()
         assert not s[[0, 2, 4]].any(), f"rec_max={rec_max}"
         _check(out, ns, inp)
 
 
+def _expected_sequential(lens):
+    """The built-in path choice of gdn_prefill_fwd (gdn_prefill.hip), restated."""
+    T, N, L = sum(lens), len(lens), max(lens)
+    if T <= 96:
+        return True
+    if N == 1 or T > 32 * N:
+        return False
+    by_token = 0.24 * L + 0.024 * T + 0.17 * N
+    by_chunk = 20.0 + 1.05 * math.ceil(L / 64) + 1.05 * N
+    return by_token <= by_chunk
+
+
+def _path_flag(dev, T, N):
+    """The path flag the index kernel leaves in the per-stream workspace."""
+    ws = prefill._workspace(dev, torch.cuda.current_stream(dev).cuda_stream, 0)
+    chunks_bytes = (O.max_chunks(T, N) * 16 + 255) // 256 * 256
+    flag_at = chunks_bytes + (N + 1) * 4
+    return int(ws[flag_at:flag_at + 4].cpu().numpy().view(np.int32)[0])
+
+
+def _lens_1500():
+    lens = np.random.default_rng(5).integers(0, 4, 1500).tolist()
+    lens[3] = 70
+    return lens
+
+
+# Batches the host leaves to the device (mean length <= 32, T > 96).
+DEVICE_CHOICE = {
+    "256x1": [1] * 256,
+    "64x16": [16] * 64,
+    "mixed40": [3, 17, 96, 0, 40] * 8,
+    "1500": _lens_1500(),
+    "10x2+200": [2] * 10 + [200],
+}
+
+
+@pytest.mark.parametrize("name", list(DEVICE_CHOICE))
+def test_device_path_choice(cuda_device, name):
+    lens = DEVICE_CHOICE[name]
+    T, N = sum(lens), len(lens)
+    want = _expected_sequential(lens)
+    print(f"device path choice {name}: T={T} N={N} sequential={want}", flush=True)
+    inp = O.make_prefill_inputs(lens, seed=15)
+    out, ns = _prefill(_to_dev(inp, cuda_device), cuda_device)
+    assert _path_flag(cuda_device, T, N) == int(want)
+    _check(out, ns, inp, tight=want)
+
+
 def test_recurrent_tilings_are_identical(cuda_device):
     lens = [6, 49, 200, 1]
     inp = O.make_prefill_inputs(lens, seed=14)
     d = _to_dev(inp, cuda_device)
-    ref_o, ref_s = _prefill(d, cuda_device, recurrent_variant=0)
+    ref_o, ref_s = _prefill(d, cuda_device, recurrent_variant=0, recurrent_max_len=ALL_SEQUENTIAL)
     _check(ref_o, ref_s, inp, tight=True)
     for var in range(1, 10):
-        o, s = _prefill(d, cuda_device, recurrent_variant=var)
+        o, s = _prefill(d, cuda_device, recurrent_variant=var, recurrent_max_len=ALL_SEQUENTIAL)
         assert torch.equal(o, ref_o), f"tiling {var}: output differs"
         assert torch.equal(s, ref_s), f"tiling {var}: state differs"
 
