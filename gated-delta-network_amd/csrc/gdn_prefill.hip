@@ -176,6 +176,16 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
   for (int c = nt + tid; c < nt_max; c += 1024) chunks[c] = make_int4(-1, 0, 0, 0);
 }
 
+// Chunk c of the table; for a single sequence (single_T = its length T >= 0)
+// there is no table and the entry is computed directly.
+__device__ __forceinline__ int4 chunk_info(const int4 *chunks, int c, int single_T) {
+  if (single_T >= 0) {
+    const int start = c * kChunk, rest = single_T - start;
+    return rest > 0 ? make_int4(0, start, rest < kChunk ? rest : kChunk, c) : make_int4(-1, 0, 0, 0);
+  }
+  return chunks[c];
+}
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // v_mfma_f32_16x16x16_bf16: A lane l holds A[l & 15][4*(l >> 4) + e], B lane l
@@ -232,11 +242,11 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
-    const int4 *__restrict__ chunks, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
-    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u,
-    uint16_t *__restrict__ ws_kt) {
+    const int4 *__restrict__ chunks, int single_T, float *__restrict__ ws_G,
+    float *__restrict__ ws_dcy, float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w,
+    float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
   const int c = blockIdx.x, h = blockIdx.y;
-  const int4 ch = chunks[c];
+  const int4 ch = chunk_info(chunks, c, single_T);
   if (ch.x < 0) return;
   const int start = ch.y, len = ch.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -493,7 +503,7 @@ template <int BV>
 __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
     const float *state, float *new_state, const int *offsets, const float *ws_dcy,
     const float *ws_eg, const uint16_t *ws_w, const float *ws_u,
-    const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt, int N) {
+    const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt, int N, int single_T) {
   constexpr int NVB = kDV / BV;
   const int h = blockIdx.x % kHV;
   const int rest = blockIdx.x / kHV;
@@ -509,9 +519,12 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
   __shared__ __align__(16) uint16_t sVh[BV * kStrideT];
   __shared__ __align__(16) uint16_t sVl[BV * kStrideT];
 
-  const int c0 = offsets[s];
-  const int nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
-  if (offsets[N + 1]) return;  // the token-sequential kernel owns the batch
+  int c0 = 0, nch = (single_T + kChunk - 1) / kChunk;  // one sequence: no table
+  if (single_T < 0) {
+    if (offsets[N + 1]) return;  // the token-sequential kernel owns the batch
+    c0 = offsets[s];
+    nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
+  }
   const size_t sbase = (static_cast<size_t>(s) * kHV + h) * kDV * kDK;  // [V][K]
 
   f32x4 S[2];
@@ -645,11 +658,11 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prefill_output_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
-    const int4 *__restrict__ chunks, const float *__restrict__ ws_G,
+    const int4 *__restrict__ chunks, int single_T, const float *__restrict__ ws_G,
     const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
     uint16_t *__restrict__ out) {
   const int c = blockIdx.x, h = blockIdx.y;
-  const int4 ch = chunks[c];
+  const int4 ch = chunk_info(chunks, c, single_T);
   if (ch.x < 0) return;
   const int start = ch.y, len = ch.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -837,10 +850,15 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
                             nullptr, scale, output, new_state, stream, rec_variant,
                             "gdn_prefill_fwd");
-  hipLaunchKernelGGL(prefill_index_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, cu64, N, T,
-                     L.nt_max, choose, rec_max, chunks, offsets);
-  int rc = check_launch("gdn_prefill_fwd(index)");
-  if (rc) return rc;
+  // One sequence is [0, T) by the cu_seqlens contract: its chunks follow
+  // from T, and the kernels compute them instead of reading a table.
+  const int single_T = (N == 1 && choose == 0) ? T : -1;
+  int rc = GDN_OK;
+  if (single_T < 0) {
+    hipLaunchKernelGGL(prefill_index_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, cu64, N, T,
+                       L.nt_max, choose, rec_max, chunks, offsets);
+    if ((rc = check_launch("gdn_prefill_fwd(index)"))) return rc;
+  }
   if (choose != 0) {
     rc = recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
                           offsets + N + 1, scale, output, new_state, stream, rec_variant,
@@ -849,7 +867,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   }
   if (L.nt_max > 0) {
     hipLaunchKernelGGL(prefill_intra_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, k, v, A_log,
-                       a, dt_bias, b, chunks, wsG, wsD, wsE, wsw, wsu, kt);
+                       a, dt_bias, b, chunks, single_T, wsG, wsD, wsE, wsw, wsu, kt);
     if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
   }
   const int bv = variant == 1 ? 32 : 16;  // 16 measured faster at every size
@@ -857,14 +875,14 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
   if (bv == 32)
     hipLaunchKernelGGL(prefill_state_kernel<32>, dim3(static_cast<unsigned>(blocks)), dim3(512), 0,
-                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N);
+                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N, single_T);
   else
     hipLaunchKernelGGL(prefill_state_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N);
+                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N, single_T);
   if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
   if (L.nt_max > 0) {
     hipLaunchKernelGGL(prefill_output_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, q, k, chunks,
-                       wsG, ht, vnt, scale, output);
+                       single_T, wsG, ht, vnt, scale, output);
     if ((rc = check_launch("gdn_prefill_fwd(output)"))) return rc;
   }
   return GDN_OK;
