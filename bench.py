@@ -52,9 +52,22 @@ def _dev_inputs(inp, dev):
     return d
 
 
-def bench_decode(B, steps, warmup, dev, variant=-1):
-    """Times `steps` decode steps at batch B two ways and returns
-    (eager ms/step, graph ms/step).
+# Single workloads for `--only` (profiling): decode (batch, tokens per row)
+# or prefill sequence lengths.
+ONLY_WORKLOADS = {
+    "decode_b64": ("decode", (64, 1)),
+    "decode_b64_t4": ("decode", (64, 4)),
+    "prefill_1x8192": ("prefill", [8192]),
+    "prefill_4x8192": ("prefill", [8192] * 4),
+    "prefill_1x1024": ("prefill", [1024]),
+    "prefill_64x16": ("prefill", [16] * 64),
+    "prefill_configs3": ("prefill", [6, 49, 294, 1800, 2040, 61]),
+}
+
+
+def bench_decode(B, steps, warmup, dev, variant=-1, tokens=1):
+    """Times `steps` decode calls at batch B (`tokens` tokens per row; 1 is the
+    plain decode step) two ways and returns (eager ms/call, graph ms/call).
 
     eager: back-to-back calls of the DPS entry point (validation, ctypes call
     and launch on the host each time).  graph: the same `steps` launches
@@ -67,11 +80,17 @@ def bench_decode(B, steps, warmup, dev, variant=-1):
     from gdn_amd import decode
     from oracle import gdn_oracle as O  # input recipe only
 
-    inp = O.make_decode_inputs(B, seed=1)
+    if tokens == 1:
+        inp = O.make_decode_inputs(B, seed=1)
+    else:  # B sequences of `tokens` tokens, viewed as [B, T, ...]
+        inp = O.make_prefill_inputs([tokens] * B, seed=1)
+        for n, tail in (("q", (4, 128)), ("k", (4, 128)), ("v", (8, 128)), ("a", (8,)),
+                        ("b", (8,))):
+            inp[n] = inp[n].reshape((B, tokens) + tail)
     d = _dev_inputs(inp, dev)
     states = [d["state"].clone() for _ in range(ROTATE)]
     new_states = [torch.empty_like(d["state"]) for _ in range(ROTATE)]
-    out = torch.empty((B, 1, 8, 128), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((B, tokens, 8, 128), dtype=torch.bfloat16, device=dev)
     args = (d["q"], d["k"], d["v"])
     tail = (d["A_log"], d["a"], d["dt_bias"], d["b"], inp["scale"], out)
 
@@ -227,6 +246,9 @@ def main():
     ap.add_argument("--sweep", action="store_true",
                     help="also time every decode batch size of configs[1] and every tiling")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", choices=sorted(ONLY_WORKLOADS),
+                    help="profiling mode: time only this workload (eager and graph) and "
+                         "print one line; for rocprofv3 summaries of single workloads")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 64 MiB device copy 10 times (the known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling)")
@@ -253,6 +275,14 @@ def main():
         return
     log(f"device: {torch.cuda.get_device_name(dev)}")
     B = args.batch
+    if args.only:
+        kind, arg = ONLY_WORKLOADS[args.only]
+        if kind == "decode":
+            me, mg = bench_decode(arg[0], args.steps, args.warmup, dev, tokens=arg[1])
+        else:
+            me, mg = bench_prefill(arg, args.steps, args.warmup, dev)
+        log(f"{args.only}: eager {me * 1e3:.2f} us, graph {mg * 1e3:.2f} us per call")
+        return
 
     if args.sweep:
         for b in (1, 2, 4, 8, 16, 32, 48, 64):
@@ -292,6 +322,17 @@ def main():
     log(f"prefill clone mode: 1x8192 {pre_clone:.3f} ms, 1x1024 {pre1k_clone:.3f} ms; "
         f"1x1024 graph {pre1k_ms:.3f} ms, eager {pre1k_eager:.3f} ms")
 
+    mtp = {}
+    for T in (2, 4, 8):
+        _, mg = bench_decode(64, 50, 5, dev, tokens=T)
+        mtp[f"B64_T{T}"] = round(mg * 1e3, 2)
+    log(f"multi-token decode B=64 (us per call): {mtp}")
+    short = {}
+    for name, lens in (("256x1", [1] * 256), ("64x16", [16] * 64), ("1x64", [64])):
+        _, pg = bench_prefill(lens, 20, 3, dev)
+        short[name] = round(pg, 4)
+    log(f"short-sequence prefill (ms per call): {short}")
+
     cpu_s, reps = cpu_baseline_decode(B, args.cpu_seconds)
     cpu_gbs = nbytes / cpu_s / 1e9
     log(f"cpu baseline decode B={B}: {cpu_s * 1e3:.1f} ms/step over {reps} steps")
@@ -320,6 +361,8 @@ def main():
         "prefill_ms_1x8192_clone": round(pre_clone, 4),
         "prefill_ms_1x1024": round(pre1k_ms, 4),
         "prefill_ms_1x1024_clone": round(pre1k_clone, 4),
+        "decode_multi_token_us": mtp,
+        "prefill_ms_short_batches": short,
         "prefill_roofline": {"bound": "mfma", "achieved": round(pre_tflops, 2), "peak": 2500.0,
                              "unit": "TFLOP/s", "frac": round(pre_tflops / 2500.0, 5),
                              "hbm_gbs": round(pre_gbs, 1),

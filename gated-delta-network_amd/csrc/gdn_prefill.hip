@@ -214,11 +214,13 @@ __device__ __forceinline__ f32x4 mfma16_x3(const u32x2 ah, const u32x2 al, const
   return mfma16_bf16(al, bh, acc);
 }
 
-// Transposed [*][64] bf16 tiles in LDS store each row's eight 8-token blocks
-// in XOR-swizzled order (block b of row n at slot b ^ ((n >> 3) & 7)), so the
-// 16-byte transposed writes of eight consecutive rows hit different banks.
+// Transposed [*][64] bf16 tiles in LDS (rows of 128 bytes, no padding) store
+// each row's eight 8-token blocks in XOR-swizzled order (block b of row n at
+// slot b ^ ((n >> 3) & 7)), so the 16-byte transposed writes of eight
+// consecutive rows hit different banks.
+constexpr int kStrideTT = 64;
 __device__ __forceinline__ int tsw(int row, int token) {
-  return row * kStrideT + ((((token >> 3) ^ (row >> 3)) & 7) << 3) + (token & 7);
+  return row * kStrideTT + ((((token >> 3) ^ (row >> 3)) & 7) << 3) + (token & 7);
 }
 
 // ---------------------------------------------------------------------------
@@ -255,13 +257,20 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
   const size_t ch_head = static_cast<size_t>(c) * kHV + h;
 
   constexpr int kStrideA4 = 68;  // f32 stride of the 64x64 A tile (16-byte rows)
-  constexpr int kStrideD = 20;   // f32 stride of the 16x16 diagonal inverses
-  __shared__ __align__(16) uint16_t sK[kChunk * kStrideK];  // later: w transpose scratch
-  __shared__ __align__(16) uint16_t sKt[kDK * kStrideT];
-  __shared__ __align__(16) uint16_t sVt[kDV * kStrideT];
-  __shared__ __align__(16) float sA[kChunk * kStrideA4];     // later: w transpose scratch
-  __shared__ __align__(16) float sD[4 * 16 * kStrideD];
+  // 52 KB of LDS, so three workgroups share a CU:
+  //   sKV: K row-major until A is built, then V^T, then (wave 2) w scratch;
+  //   sA:  strictly lower blocks of A; the unused upper blocks hold the four
+  //        16x16 diagonal inverses (D_w at block kDiagBlock[w]); at the end
+  //        (wave 3) w scratch.
+  __shared__ __align__(16) uint16_t sKV[kChunk * kStrideK];
+  __shared__ __align__(16) uint16_t sKt[kDK * kStrideTT];
+  __shared__ __align__(16) float sA[kChunk * kStrideA4];
   __shared__ __align__(16) float sBeta[kChunk], sBG[kChunk], sG[kChunk];
+  uint16_t *const sK = sKV, *const sVt = sKV;
+  static_assert(kDV * kStrideTT <= kChunk * kStrideK, "V^T must fit in the K tile");
+  // D_w lives at row block w, column block dcol(w): (0,1), (1,2), (2,3), (0,2).
+  auto dcol = [](int w) { return w == 3 ? 2 : w + 1; };
+  auto drow = [](int w) { return w == 3 ? 0 : w; };
 
   // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding tokens
   // get g = 0 and beta = 0, so G stays at G_last past the end of the chunk.
@@ -287,27 +296,27 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
     if (lane == 0) ws_eg[ch_head] = expf(G_last);
   }
 
-  // One 8x8 block of K (threads 0..127) or V (128..255) per thread.
-  {
-    const bool isK = tid < 128;
-    const int blk = tid & 127, rb = blk >> 4, cb = blk & 15;
-    u32x4 rows[8];
+  // One 8x8 block of K (threads 0..127) or V (128..255) per thread, loaded
+  // now; K goes to LDS (row-major and transposed) at once, V's transpose waits
+  // in registers until A is built (it reuses the K tile's space).
+  const bool isK = tid < 128;
+  const int blk = tid & 127, rb = blk >> 4, cb = blk & 15;
+  u32x4 rows[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = rb * 8 + i;
-      rows[i] = u32x4{0u, 0u, 0u, 0u};
-      if (row < len) {
-        const size_t t = static_cast<size_t>(start) + row;
-        rows[i] = isK ? *reinterpret_cast<const u32x4 *>(k + (t * kHQK + hq) * kDK + cb * 8)
-                      : *reinterpret_cast<const u32x4 *>(v + (t * kHV + h) * kDV + cb * 8);
-      }
-      if (isK) *reinterpret_cast<u32x4 *>(&sK[row * kStrideK + cb * 8]) = rows[i];
+  for (int i = 0; i < 8; ++i) {
+    const int row = rb * 8 + i;
+    rows[i] = u32x4{0u, 0u, 0u, 0u};
+    if (row < len) {
+      const size_t t = static_cast<size_t>(start) + row;
+      rows[i] = isK ? *reinterpret_cast<const u32x4 *>(k + (t * kHQK + hq) * kDK + cb * 8)
+                    : *reinterpret_cast<const u32x4 *>(v + (t * kHV + h) * kDV + cb * 8);
     }
-    uint16_t *dstT = isK ? sKt : sVt;
+  }
+  // Column j of the block = 8 tokens of feature cb*8 + j, into transposed LDS.
+  auto transpose_into = [&](uint16_t *dstT, bool kt_frags) {
     uint16_t *ktf = ws_kt + (static_cast<size_t>(c) * kHQK + hq) * (kDK * kChunk);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      // column j of the block = 8 tokens of feature cb*8 + j
       u32x4 col;
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
@@ -318,10 +327,16 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
       *reinterpret_cast<u32x4 *>(&dstT[tsw(n, rb * 8)]) = col;
       // K^T as A-operand fragments of the state kernel: (mt, kk, lane) =
       // (n / 16, rb / 4, (rb % 4) * 16 + n % 16), 8 tokens each.
-      if (isK && (h & 1) == 0)
+      if (kt_frags)
         *reinterpret_cast<u32x4 *>(
             ktf + ((((n >> 4) * 2 + (rb >> 2)) * 64) + (rb & 3) * 16 + (n & 15)) * 8) = col;
     }
+  };
+  if (isK) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      *reinterpret_cast<u32x4 *>(&sK[(rb * 8 + i) * kStrideK + cb * 8]) = rows[i];
+    transpose_into(sKt, (h & 1) == 0);
   }
   __syncthreads();
 
@@ -343,7 +358,9 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
       }
     }
   }
-  __syncthreads();
+  __syncthreads();  // K row-major is dead: its space takes V^T
+
+  if (!isK) transpose_into(sVt, false);
 
   // Diagonal blocks D_w = (I + A_ww)^-1: wave w, lane j < 16 solves column j.
   if (lane < 16) {
@@ -361,7 +378,8 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
       x[i] = s0 + s1;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sD[(wave * 16 + i) * kStrideD + lane] = x[i];
+    for (int i = 0; i < 16; ++i)
+      sA[(16 * drow(wave) + i) * kStrideA4 + 16 * dcol(wave) + lane] = x[i];
   }
   __syncthreads();
 
@@ -396,7 +414,8 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
         for (int nt = 0; nt < 4; ++nt) Z[nt] = mfma16_x3(lh, ll, Yh[j][nt], Yl[j][nt], Z[nt]);
       }
       // Y_i = D_i Z
-      const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&sD[(i * 16 + r16) * kStrideD + 4 * g]);
+      const f32x4 d4 = *reinterpret_cast<const f32x4 *>(
+          &sA[(16 * drow(i) + r16) * kStrideA4 + 16 * dcol(i) + 4 * g]);
       u32x2 dh, dl;
       split4(d4, dh, dl);
 #pragma unroll
@@ -417,12 +436,12 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
         for (int nt = 0; nt < 4; ++nt)
           *reinterpret_cast<f32x4 *>(ut + ((i * 8 + (col0 >> 4) + nt) * 64 + lane) * 4) = Y[i][nt];
     }
-    __syncthreads();  // sK and sA are free from here on: w transpose scratch
+    __syncthreads();  // sKV and sA are free from here on: w transpose scratch
 
     if (!isU) {
       // w: through LDS to A-operand fragments (row 16*mb + r16, 8 consecutive
       // k), split hi/lo: [chunk][head][mb][kk][lane][hi 8 | lo 8].
-      float *scr = (wave == 2) ? reinterpret_cast<float *>(sK) : sA;  // [64][68]
+      float *scr = (wave == 2) ? reinterpret_cast<float *>(sKV) : sA;  // [64][68]
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
