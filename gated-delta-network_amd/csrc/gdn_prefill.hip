@@ -758,14 +758,25 @@ __global__ __launch_bounds__(256) void prefill_output_kernel(
         O[mb][nt] = mfma_bf16(pa, vb, O[mb][nt]);
       }
     }
+  }
+  // o = scale * O through LDS (the Q tile's space), so that every global
+  // store is 16 contiguous bytes of one token row.
+  __syncthreads();
+  uint16_t *sO = sQ;  // [64][kStrideK]
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int n = 16 * (2 * wave + nt) + r16;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * mb + q4 + r;
-        if (i < len)
-          out[((static_cast<size_t>(start) + i) * kHV + h) * kDV + n] = f32_to_bf16(scale * O[mb][nt][r]);
-      }
+      for (int r = 0; r < 4; ++r) sO[(16 * mb + q4 + r) * kStrideK + n] = f32_to_bf16(scale * O[mb][nt][r]);
+  }
+  __syncthreads();
+  for (int idx = tid; idx < kChunk * 16; idx += 256) {
+    const int row = idx >> 4, c8 = (idx & 15) * 8;
+    if (row < len)
+      *reinterpret_cast<u32x4 *>(out + ((static_cast<size_t>(start) + row) * kHV + h) * kDV + c8) =
+          *reinterpret_cast<const u32x4 *>(&sO[row * kStrideK + c8]);
   }
 }
 
