@@ -26,6 +26,6 @@ int check_launch(const char *what) {
 
 }  // namespace gdn
 
-extern "C" int gdn_abi_version(void) { return 2; }
+extern "C" int gdn_abi_version(void) { return 3; }
 
 extern "C" const char *gdn_last_error(void) { return gdn::g_last_error; }

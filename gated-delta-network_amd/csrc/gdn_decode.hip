@@ -26,16 +26,17 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
     const uint16_t *__restrict__ v, const float *state, const float *__restrict__ A_log,
     const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
-    const uint16_t *__restrict__ b, float scale, uint16_t *__restrict__ out, float *new_state) {
+    const uint16_t *__restrict__ b, float scale, uint16_t *__restrict__ out, float *new_state,
+    Heads H) {
   constexpr int kRowsPerPass = 4 * WAVES;
   constexpr int kRows = kRowsPerPass * PASSES;
   constexpr int kTiles = kDV / kRows;
   static_assert(kDV % kRows == 0, "row tile must divide 128");
 
   const int tile = blockIdx.x % kTiles;
-  const int nh = blockIdx.x / kTiles;  // n * 8 + h
-  const int h = nh % kHV;
-  const int n = nh / kHV;
+  const int nh = blockIdx.x / kTiles;  // n * H.v + h
+  const int h = nh % H.v;
+  const int n = nh / H.v;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15;
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(
   const float beta = sigmoidf_(bf16_to_f32(b[nh]));
 
   // This lane's 8 columns of q and k (q/k head h/2).
-  const int qk_off = (n * kHQK + h / 2) * kDK;
+  const int qk_off = (n * H.qk + h / H.ratio) * kDK;
   const u16x4 qa = *reinterpret_cast<const u16x4 *>(q + qk_off + 4 * c);
   const u16x4 qb = *reinterpret_cast<const u16x4 *>(q + qk_off + 64 + 4 * c);
   const u16x4 ka = *reinterpret_cast<const u16x4 *>(k + qk_off + 4 * c);
@@ -135,7 +136,7 @@ namespace {
 
 typedef void (*decode_fn)(const uint16_t *, const uint16_t *, const uint16_t *, const float *,
                           const float *, const uint16_t *, const float *, const uint16_t *,
-                          float, uint16_t *, float *);
+                          float, uint16_t *, float *, Heads);
 
 struct DecodeVariant {
   int waves, passes;
@@ -179,53 +180,56 @@ int default_variant(int batch) {
 
 }  // namespace
 
-static int decode_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
-                         const float *state, const float *A_log, const gdn_bf16 *a,
-                         const float *dt_bias, const gdn_bf16 *b, float scale, gdn_bf16 *output,
-                         float *new_state, int batch, void *stream, int variant) {
+int decode_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v, const float *state,
+                  const float *A_log, const gdn_bf16 *a, const float *dt_bias, const gdn_bf16 *b,
+                  float scale, gdn_bf16 *output, float *new_state, int batch, void *stream,
+                  int variant, const Heads &H, const char *what) {
   clear_error();
-  if (batch < 0) return fail(GDN_ERR_INVALID, "gdn_decode_fwd: batch=%d < 0", batch);
+  if (batch < 0) return fail(GDN_ERR_INVALID, "%s: batch=%d < 0", what, batch);
   if (!q || !k || !v || !A_log || !a || !dt_bias || !b || !output || !new_state)
-    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: null pointer argument");
+    return fail(GDN_ERR_INVALID, "%s: null pointer argument", what);
   if (!(scale > 0.0f) || scale == __builtin_inff())
-    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: scale must be finite and > 0");
+    return fail(GDN_ERR_INVALID, "%s: scale must be finite and > 0", what);
   if (!aligned(new_state, 16) || (state && !aligned(state, 16)))
-    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: state/new_state must be 16-byte aligned");
+    return fail(GDN_ERR_INVALID, "%s: state/new_state must be 16-byte aligned", what);
   if (!aligned(q, 8) || !aligned(k, 8))
-    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: q/k must be 8-byte aligned");
+    return fail(GDN_ERR_INVALID, "%s: q/k must be 8-byte aligned", what);
   if (batch == 0) return GDN_OK;
   const size_t nb = static_cast<size_t>(batch);
-  const size_t state_bytes = nb * kHV * kDV * kDK * sizeof(float);
-  const size_t out_bytes = nb * kHV * kDV * sizeof(uint16_t);
+  const size_t nV = static_cast<size_t>(H.v), nQK = static_cast<size_t>(H.qk);
+  const size_t state_bytes = nb * nV * kDV * kDK * sizeof(float);
+  const size_t out_bytes = nb * nV * kDV * sizeof(uint16_t);
   // new_state may be exactly state (in-place); no other overlap is allowed.
   if (state != new_state && overlaps(state, state_bytes, new_state, state_bytes))
-    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: new_state partially overlaps state");
+    return fail(GDN_ERR_INVALID, "%s: new_state partially overlaps state", what);
   const void *ins[] = {q, k, v, a, b, A_log, dt_bias, state};
-  const size_t in_bytes[] = {nb * kHQK * kDK * 2, nb * kHQK * kDK * 2, nb * kHV * kDV * 2,
-                             nb * kHV * 2,        nb * kHV * 2,        kHV * 4,
-                             kHV * 4,             state ? state_bytes : 0};
+  const size_t in_bytes[] = {nb * nQK * kDK * 2, nb * nQK * kDK * 2, nb * nV * kDV * 2,
+                             nb * nV * 2,        nb * nV * 2,        nV * 4,
+                             nV * 4,             state ? state_bytes : 0};
   for (int i = 0; i < 8; ++i) {
     if (overlaps(output, out_bytes, ins[i], in_bytes[i]))
-      return fail(GDN_ERR_INVALID, "gdn_decode_fwd: output overlaps an input");
+      return fail(GDN_ERR_INVALID, "%s: output overlaps an input", what);
     if (i < 7 && overlaps(new_state, state_bytes, ins[i], in_bytes[i]))
-      return fail(GDN_ERR_INVALID, "gdn_decode_fwd: new_state overlaps an input");
+      return fail(GDN_ERR_INVALID, "%s: new_state overlaps an input", what);
   }
   if (overlaps(output, out_bytes, new_state, state_bytes))
-    return fail(GDN_ERR_INVALID, "gdn_decode_fwd: output overlaps new_state");
+    return fail(GDN_ERR_INVALID, "%s: output overlaps new_state", what);
 
-  if (variant < 0) variant = default_variant(batch);
+  // The built-in tiling depends on the number of state rows, counted in
+  // batch rows of the reference layout (8 v-heads).
+  if (variant < 0) variant = default_variant(static_cast<int>((static_cast<long long>(batch) * H.v + kHV - 1) / kHV));
   const int nt = (variant & kNontemporalFlag) ? 1 : 0;
   const int vi = variant & (kNontemporalFlag - 1);
-  if (vi >= kNumVariants) return fail(GDN_ERR_INVALID, "gdn_decode_fwd: unknown variant %d", variant);
+  if (vi >= kNumVariants) return fail(GDN_ERR_INVALID, "%s: unknown variant %d", what, variant);
   const DecodeVariant &cfg = kVariants[vi];
   const int rows = 4 * cfg.waves * cfg.passes;
-  const long long blocks = static_cast<long long>(batch) * kHV * (kDV / rows);
-  if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_decode_fwd: batch too large");
+  const long long blocks = static_cast<long long>(batch) * H.v * (kDV / rows);
+  if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "%s: batch too large", what);
   decode_fn fn = state ? cfg.with_state[nt] : cfg.no_state[nt];
   hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(64 * cfg.waves), 0,
                      static_cast<hipStream_t>(stream), q, k, v, state, A_log, a, dt_bias, b,
-                     scale, output, new_state);
-  return check_launch("gdn_decode_fwd");
+                     scale, output, new_state, H);
+  return check_launch(what);
 }
 
 }  // namespace gdn
@@ -235,7 +239,8 @@ extern "C" int gdn_decode_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf
                               const float *dt_bias, const gdn_bf16 *b, float scale,
                               gdn_bf16 *output, float *new_state, int batch, void *stream) {
   return gdn::decode_launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
-                            stream, -1);
+                            stream, -1, gdn::Heads{gdn::kHQK, gdn::kHV, gdn::kHV / gdn::kHQK},
+                            "gdn_decode_fwd");
 }
 
 extern "C" int gdn_decode_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
@@ -244,5 +249,6 @@ extern "C" int gdn_decode_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, cons
                                       gdn_bf16 *output, float *new_state, int batch, void *stream,
                                       int variant) {
   return gdn::decode_launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
-                            stream, variant);
+                            stream, variant, gdn::Heads{gdn::kHQK, gdn::kHV, gdn::kHV / gdn::kHQK},
+                            "gdn_decode_fwd");
 }

@@ -7,6 +7,7 @@
 
 
 #include "gdn_amd.h"
+#include "gdn_device.h"
 
 namespace gdn {
 
@@ -31,6 +32,17 @@ inline bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
   return x < y + nb && y < x + na;
 }
 
+// Validates a head layout (q/k heads hqk >= 1, v-heads hv a multiple of hqk,
+// at most kMaxHeads) into H; GDN_ERR_INVALID with a message otherwise.
+constexpr int kMaxHeads = 1024;
+inline int make_heads(int hqk, int hv, const char *what, Heads &H) {
+  if (hqk < 1 || hv < 1 || hv > kMaxHeads || hv % hqk != 0)
+    return fail(GDN_ERR_INVALID, "%s: heads %d q/k, %d v (need v a multiple of q/k, <= %d)", what,
+                hqk, hv, kMaxHeads);
+  H = Heads{hqk, hv, hv / hqk};
+  return GDN_OK;
+}
+
 // Token-sequential recurrence (gdn_recurrent.hip) over num_seqs sequences:
 // packed by cu (int32/int64 on the device) or, with cu == nullptr, of
 // fixed_len tokens each.  With a non-null `enable`, the kernel does nothing
@@ -39,8 +51,16 @@ inline bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
 int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
                      const float *A_log, const uint16_t *a, const float *dt_bias,
                      const uint16_t *b, const void *cu, int cu64, int num_seqs, int T,
-                     int fixed_len, const int *enable, float scale, uint16_t *out,
-                     float *new_state, hipStream_t stream, int variant, const char *what);
+                     int fixed_len, const int *enable, const Heads &H, float scale,
+                     uint16_t *out, float *new_state, hipStream_t stream, int variant,
+                     const char *what);
 int recurrent_num_variants();
+
+// One decode step (gdn_decode.hip) with head layout H; variant as in
+// gdn_decode_fwd_variant.  Validates its arguments; messages start with `what`.
+int decode_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v, const float *state,
+                  const float *A_log, const gdn_bf16 *a, const float *dt_bias, const gdn_bf16 *b,
+                  float scale, gdn_bf16 *output, float *new_state, int batch, void *stream,
+                  int variant, const Heads &H, const char *what);
 
 }  // namespace gdn

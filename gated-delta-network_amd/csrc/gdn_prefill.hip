@@ -59,7 +59,7 @@ static long long max_chunks(long long T, long long N) {
   return bound < T ? bound : T;
 }
 
-static PrefillLayout prefill_layout(int T, int N) {
+static PrefillLayout prefill_layout(int T, int N, const Heads &H) {
   PrefillLayout L{};
   const long long nt = max_chunks(T, N);
   L.nt_max = static_cast<int>(nt);
@@ -72,14 +72,15 @@ static PrefillLayout prefill_layout(int T, int N) {
   const size_t n = static_cast<size_t>(nt);
   L.chunks = take(n * sizeof(int4));
   L.offsets = take((static_cast<size_t>(N) + 2) * sizeof(int));  // + the path flag
-  L.G = take(n * kHV * kChunk * 4);
-  L.dcy = take(n * kHV * kChunk * 4);
-  L.eg = take(n * kHV * 4);
-  L.w = take(n * kHV * kChunk * kDK * 4);  // hi and lo bf16
-  L.u = take(n * kHV * kChunk * kDV * 4);
-  L.kt = take(n * kHQK * kDK * kChunk * 2);
-  L.ht = take(n * kHV * kDV * kDK * 2);
-  L.vnt = take(n * kHV * kDV * kChunk * 2);
+  const size_t hv = static_cast<size_t>(H.v), hqk = static_cast<size_t>(H.qk);
+  L.G = take(n * hv * kChunk * 4);
+  L.dcy = take(n * hv * kChunk * 4);
+  L.eg = take(n * hv * 4);
+  L.w = take(n * hv * kChunk * kDK * 4);  // hi and lo bf16
+  L.u = take(n * hv * kChunk * kDV * 4);
+  L.kt = take(n * hqk * kDK * kChunk * 2);
+  L.ht = take(n * hv * kDV * kDK * 2);
+  L.vnt = take(n * hv * kDV * kChunk * 2);
   L.total = off;
   return L;
 }
@@ -244,7 +245,7 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
-    const int4 *__restrict__ chunks, int single_T, float *__restrict__ ws_G,
+    const int4 *__restrict__ chunks, int single_T, Heads H, float *__restrict__ ws_G,
     float *__restrict__ ws_dcy, float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w,
     float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
   const int c = blockIdx.x, h = blockIdx.y;
@@ -253,8 +254,8 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
   const int start = ch.y, len = ch.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4, kg = g * 8;
-  const int hq = h >> 1;
-  const size_t ch_head = static_cast<size_t>(c) * kHV + h;
+  const int hq = h / H.ratio;
+  const size_t ch_head = static_cast<size_t>(c) * H.v + h;
 
   constexpr int kStrideA4 = 68;  // f32 stride of the 64x64 A tile (16-byte rows)
   // 52 KB of LDS, so three workgroups share a CU:
@@ -278,8 +279,8 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
     float gl = 0.f, be = 0.f;
     if (lane < len) {
       const size_t t = static_cast<size_t>(start) + lane;
-      gl = gdn_log_decay(A_log[h], bf16_to_f32(a[t * kHV + h]), dt_bias[h]);
-      be = sigmoidf_(bf16_to_f32(b[t * kHV + h]));
+      gl = gdn_log_decay(A_log[h], bf16_to_f32(a[t * H.v + h]), dt_bias[h]);
+      be = sigmoidf_(bf16_to_f32(b[t * H.v + h]));
     }
     float G = gl;
 #pragma unroll
@@ -308,13 +309,13 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
     rows[i] = u32x4{0u, 0u, 0u, 0u};
     if (row < len) {
       const size_t t = static_cast<size_t>(start) + row;
-      rows[i] = isK ? *reinterpret_cast<const u32x4 *>(k + (t * kHQK + hq) * kDK + cb * 8)
-                    : *reinterpret_cast<const u32x4 *>(v + (t * kHV + h) * kDV + cb * 8);
+      rows[i] = isK ? *reinterpret_cast<const u32x4 *>(k + (t * H.qk + hq) * kDK + cb * 8)
+                    : *reinterpret_cast<const u32x4 *>(v + (t * H.v + h) * kDV + cb * 8);
     }
   }
   // Column j of the block = 8 tokens of feature cb*8 + j, into transposed LDS.
   auto transpose_into = [&](uint16_t *dstT, bool kt_frags) {
-    uint16_t *ktf = ws_kt + (static_cast<size_t>(c) * kHQK + hq) * (kDK * kChunk);
+    uint16_t *ktf = ws_kt + (static_cast<size_t>(c) * H.qk + hq) * (kDK * kChunk);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       u32x4 col;
@@ -336,7 +337,7 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       *reinterpret_cast<u32x4 *>(&sK[(rb * 8 + i) * kStrideK + cb * 8]) = rows[i];
-    transpose_into(sKt, (h & 1) == 0);
+    transpose_into(sKt, h % H.ratio == 0);  // one v-head per q/k head writes K^T
   }
   __syncthreads();
 
@@ -490,12 +491,12 @@ struct ChunkFrag {
   float eg;            // exp(G_last)
 };
 
-__device__ __forceinline__ void load_chunk_frag(ChunkFrag &f, int c, int h, int vw, int wave,
-                                                int lane, const float *ws_dcy, const float *ws_eg,
-                                                const uint16_t *ws_w, const float *ws_u,
-                                                const uint16_t *ws_kt) {
+__device__ __forceinline__ void load_chunk_frag(ChunkFrag &f, int c, int h, const Heads &H,
+                                                int vw, int wave, int lane, const float *ws_dcy,
+                                                const float *ws_eg, const uint16_t *ws_w,
+                                                const float *ws_u, const uint16_t *ws_kt) {
   const int q4 = 4 * (lane >> 4);
-  const size_t ch_head = static_cast<size_t>(c) * kHV + h;
+  const size_t ch_head = static_cast<size_t>(c) * H.v + h;
   // w: [mb][kk][lane][hi 8 | lo 8] fragments of this wave's 16 rows
   const uint16_t *wf = ws_w + ch_head * (kChunk * kDK * 2) + (wave * 4) * (64 * 16);
 #pragma unroll
@@ -504,7 +505,7 @@ __device__ __forceinline__ void load_chunk_frag(ChunkFrag &f, int c, int h, int 
     f.wl[kk] = *reinterpret_cast<const u32x4 *>(wf + (kk * 64 + lane) * 16 + 8);
   }
   // K^T: [mt][kk][lane][8] fragments of this wave's two 16-row tiles
-  const uint16_t *kt = ws_kt + (static_cast<size_t>(c) * kHQK + (h >> 1)) * (kDK * kChunk);
+  const uint16_t *kt = ws_kt + (static_cast<size_t>(c) * H.qk + h / H.ratio) * (kDK * kChunk);
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -522,10 +523,10 @@ template <int BV>
 __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
     const float *state, float *new_state, const int *offsets, const float *ws_dcy,
     const float *ws_eg, const uint16_t *ws_w, const float *ws_u,
-    const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt, int N, int single_T) {
+    const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt, int N, int single_T, Heads H) {
   constexpr int NVB = kDV / BV;
-  const int h = blockIdx.x % kHV;
-  const int rest = blockIdx.x / kHV;
+  const int h = blockIdx.x % H.v;
+  const int rest = blockIdx.x / H.v;
   const int vb = rest % NVB, s = rest / NVB;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = (tid >> 6) & 3, ct = tid >> 8;  // row group, column tile
@@ -544,7 +545,7 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
     c0 = offsets[s];
     nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
   }
-  const size_t sbase = (static_cast<size_t>(s) * kHV + h) * kDV * kDK;  // [V][K]
+  const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;  // [V][K]
 
   f32x4 S[2];
 #pragma unroll
@@ -558,7 +559,7 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
 
   // One chunk of the recurrence, from the prefetched fragments f.
   auto step = [&](const ChunkFrag &f, int c) {
-    const size_t ch_head = static_cast<size_t>(c) * kHV + h;
+    const size_t ch_head = static_cast<size_t>(c) * H.v + h;
     uint16_t *ht = ws_ht + ch_head * (kDV * kDK);
     uint16_t *vnt = ws_vnt + ch_head * (kDV * kChunk);
     // (a) chunk-start state: split copy into LDS ([v][k]) for w S, and a bf16
@@ -644,7 +645,7 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
     auto chunk_at = [&](int i) { return c0 + (i < nch ? i : nch - 1); };
     ChunkFrag fa, fb, fc;
 #define GDN_LOAD(F, I) \
-    load_chunk_frag(F, chunk_at(I), h, vw, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt)
+    load_chunk_frag(F, chunk_at(I), h, H, vw, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt)
     GDN_LOAD(fa, 0);
     GDN_LOAD(fb, 1);
     GDN_LOAD(fc, 2);
@@ -677,7 +678,7 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prefill_output_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
-    const int4 *__restrict__ chunks, int single_T, const float *__restrict__ ws_G,
+    const int4 *__restrict__ chunks, int single_T, Heads H, const float *__restrict__ ws_G,
     const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
     uint16_t *__restrict__ out) {
   const int c = blockIdx.x, h = blockIdx.y;
@@ -686,8 +687,8 @@ __global__ __launch_bounds__(256) void prefill_output_kernel(
   const int start = ch.y, len = ch.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
-  const int hq = h >> 1;
-  const size_t ch_head = static_cast<size_t>(c) * kHV + h;
+  const int hq = h / H.ratio;
+  const size_t ch_head = static_cast<size_t>(c) * H.v + h;
 
   __shared__ __align__(16) uint16_t sQ[kChunk * kStrideK];
   __shared__ __align__(16) uint16_t sK[kChunk * kStrideK];
@@ -700,8 +701,8 @@ __global__ __launch_bounds__(256) void prefill_output_kernel(
     u32x4 qv = {0u, 0u, 0u, 0u}, kv = {0u, 0u, 0u, 0u};
     if (row < len) {
       const size_t t = static_cast<size_t>(start) + row;
-      qv = *reinterpret_cast<const u32x4 *>(q + (t * kHQK + hq) * kDK + c8);
-      kv = *reinterpret_cast<const u32x4 *>(k + (t * kHQK + hq) * kDK + c8);
+      qv = *reinterpret_cast<const u32x4 *>(q + (t * H.qk + hq) * kDK + c8);
+      kv = *reinterpret_cast<const u32x4 *>(k + (t * H.qk + hq) * kDK + c8);
     }
     *reinterpret_cast<u32x4 *>(&sQ[row * kStrideK + c8]) = qv;
     *reinterpret_cast<u32x4 *>(&sK[row * kStrideK + c8]) = kv;
@@ -775,7 +776,7 @@ __global__ __launch_bounds__(256) void prefill_output_kernel(
   for (int idx = tid; idx < kChunk * 16; idx += 256) {
     const int row = idx >> 4, c8 = (idx & 15) * 8;
     if (row < len)
-      *reinterpret_cast<u32x4 *>(out + ((static_cast<size_t>(start) + row) * kHV + h) * kDV + c8) =
+      *reinterpret_cast<u32x4 *>(out + ((static_cast<size_t>(start) + row) * H.v + h) * kDV + c8) =
           *reinterpret_cast<const u32x4 *>(&sO[row * kStrideK + c8]);
   }
 }
@@ -794,8 +795,10 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
                           const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
                           int cu64, int N, int T, float scale, gdn_bf16 *output, float *new_state,
                           void *workspace, size_t ws_bytes, void *stream_ptr, int variant,
-                          int rec_max, int rec_variant) {
+                          int rec_max, int rec_variant, int hqk, int hv) {
   clear_error();
+  Heads H;
+  if (int rc = make_heads(hqk, hv, "gdn_prefill_fwd", H)) return rc;
   if (N < 0 || T < 0) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: num_seqs=%d, total_tokens=%d", N, T);
   if (!cu_seqlens) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: null cu_seqlens");
   if (!A_log || !dt_bias) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: null pointer argument");
@@ -816,18 +819,19 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown recurrent tiling %d", rec_variant);
   if (N == 0) return GDN_OK;
 
-  const PrefillLayout L = prefill_layout(T, N);
+  const PrefillLayout L = prefill_layout(T, N, H);
   if (!workspace || ws_bytes < L.total)
     return fail(GDN_ERR_WORKSPACE, "gdn_prefill_fwd: workspace of %zu bytes, %zu needed", ws_bytes, L.total);
   if (!aligned(workspace, 256)) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: workspace must be 256-byte aligned");
 
   const size_t nT = static_cast<size_t>(T), nN = static_cast<size_t>(N);
-  const size_t state_bytes = nN * kHV * kDV * kDK * 4;
-  const size_t out_bytes = nT * kHV * kDV * 2;
+  const size_t nV = static_cast<size_t>(H.v), nQK = static_cast<size_t>(H.qk);
+  const size_t state_bytes = nN * nV * kDV * kDK * 4;
+  const size_t out_bytes = nT * nV * kDV * 2;
   const void *ins[] = {q, k, v, a, b, A_log, dt_bias, cu_seqlens, state};
-  const size_t in_bytes[] = {nT * kHQK * kDK * 2, nT * kHQK * kDK * 2, nT * kHV * kDV * 2,
-                             nT * kHV * 2,        nT * kHV * 2,        kHV * 4,
-                             kHV * 4,             (nN + 1) * (cu64 ? 8 : 4),
+  const size_t in_bytes[] = {nT * nQK * kDK * 2, nT * nQK * kDK * 2, nT * nV * kDV * 2,
+                             nT * nV * 2,        nT * nV * 2,        nV * 4,
+                             nV * 4,             (nN + 1) * (cu64 ? 8 : 4),
                              state ? state_bytes : 0};
   for (int i = 0; i < 9; ++i) {
     if (overlaps(output, out_bytes, ins[i], in_bytes[i]))
@@ -878,7 +882,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   }
   if (host_sequential)
     return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
-                            nullptr, scale, output, new_state, stream, rec_variant,
+                            nullptr, H, scale, output, new_state, stream, rec_variant,
                             "gdn_prefill_fwd");
   // One sequence is [0, T) by the cu_seqlens contract: its chunks follow
   // from T, and the kernels compute them instead of reading a table.
@@ -891,28 +895,28 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   }
   if (choose != 0) {
     rc = recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
-                          offsets + N + 1, scale, output, new_state, stream, rec_variant,
+                          offsets + N + 1, H, scale, output, new_state, stream, rec_variant,
                           "gdn_prefill_fwd");
     if (rc) return rc;
   }
   if (L.nt_max > 0) {
-    hipLaunchKernelGGL(prefill_intra_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, k, v, A_log,
-                       a, dt_bias, b, chunks, single_T, wsG, wsD, wsE, wsw, wsu, kt);
+    hipLaunchKernelGGL(prefill_intra_kernel, dim3(L.nt_max, H.v), dim3(256), 0, stream, k, v, A_log,
+                       a, dt_bias, b, chunks, single_T, H, wsG, wsD, wsE, wsw, wsu, kt);
     if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
   }
   const int bv = variant == 1 ? 32 : 16;  // 16 measured faster at every size
-  const long long blocks = static_cast<long long>(N) * kHV * (kDV / bv);
+  const long long blocks = static_cast<long long>(N) * H.v * (kDV / bv);
   if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
   if (bv == 32)
     hipLaunchKernelGGL(prefill_state_kernel<32>, dim3(static_cast<unsigned>(blocks)), dim3(512), 0,
-                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N, single_T);
+                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N, single_T, H);
   else
     hipLaunchKernelGGL(prefill_state_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N, single_T);
+                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N, single_T, H);
   if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
   if (L.nt_max > 0) {
-    hipLaunchKernelGGL(prefill_output_kernel, dim3(L.nt_max, kHV), dim3(256), 0, stream, q, k, chunks,
-                       single_T, wsG, ht, vnt, scale, output);
+    hipLaunchKernelGGL(prefill_output_kernel, dim3(L.nt_max, H.v), dim3(256), 0, stream, q, k, chunks,
+                       single_T, H, wsG, ht, vnt, scale, output);
     if ((rc = check_launch("gdn_prefill_fwd(output)"))) return rc;
   }
   return GDN_OK;
@@ -921,8 +925,16 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
 }  // namespace gdn
 
 extern "C" size_t gdn_prefill_workspace_bytes(int total_tokens, int num_seqs) {
-  if (total_tokens < 0 || num_seqs < 0) return 0;
-  return gdn::prefill_layout(total_tokens, num_seqs).total;
+  return gdn_prefill_workspace_bytes_heads(total_tokens, num_seqs, gdn::kHQK, gdn::kHV);
+}
+
+extern "C" size_t gdn_prefill_workspace_bytes_heads(int total_tokens, int num_seqs,
+                                                    int num_qk_heads, int num_v_heads) {
+  if (total_tokens < 0 || num_seqs < 0 || num_qk_heads < 1 || num_v_heads < 1 ||
+      num_v_heads > gdn::kMaxHeads || num_v_heads % num_qk_heads != 0)
+    return 0;
+  const gdn::Heads H{num_qk_heads, num_v_heads, num_v_heads / num_qk_heads};
+  return gdn::prefill_layout(total_tokens, num_seqs, H).total;
 }
 
 extern "C" int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
@@ -933,7 +945,7 @@ extern "C" int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_b
                                size_t workspace_bytes, void *stream) {
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
                              num_seqs, total_tokens, scale, output, new_state, workspace,
-                             workspace_bytes, stream, -1, -1, -1);
+                             workspace_bytes, stream, -1, -1, -1, gdn::kHQK, gdn::kHV);
 }
 
 extern "C" int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
@@ -945,7 +957,7 @@ extern "C" int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, con
                                        size_t workspace_bytes, void *stream, int variant) {
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
                              num_seqs, total_tokens, scale, output, new_state, workspace,
-                             workspace_bytes, stream, variant, -1, -1);
+                             workspace_bytes, stream, variant, -1, -1, gdn::kHQK, gdn::kHV);
 }
 
 extern "C" int gdn_prefill_fwd_tuned(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
@@ -959,5 +971,20 @@ extern "C" int gdn_prefill_fwd_tuned(const gdn_bf16 *q, const gdn_bf16 *k, const
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
                              num_seqs, total_tokens, scale, output, new_state, workspace,
                              workspace_bytes, stream, state_tiling, recurrent_max_len,
-                             recurrent_tiling);
+                             recurrent_tiling, gdn::kHQK, gdn::kHV);
+}
+
+extern "C" int gdn_prefill_fwd_heads(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                                     const float *state, const float *A_log, const gdn_bf16 *a,
+                                     const float *dt_bias, const gdn_bf16 *b,
+                                     const void *cu_seqlens, int cu_seqlens_is_int64,
+                                     int num_seqs, int total_tokens, int num_qk_heads,
+                                     int num_v_heads, float scale, gdn_bf16 *output,
+                                     float *new_state, void *workspace, size_t workspace_bytes,
+                                     void *stream, int state_tiling, int recurrent_max_len,
+                                     int recurrent_tiling) {
+  return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
+                             num_seqs, total_tokens, scale, output, new_state, workspace,
+                             workspace_bytes, stream, state_tiling, recurrent_max_len,
+                             recurrent_tiling, num_qk_heads, num_v_heads);
 }

@@ -42,14 +42,15 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
     const uint16_t *__restrict__ v, const float *state, const float *__restrict__ A_log,
     const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
     const uint16_t *__restrict__ b, const void *__restrict__ cu, int cu64, int T, int fixed_len,
-    const int *__restrict__ enable, float scale, uint16_t *__restrict__ out, float *new_state) {
+    const int *__restrict__ enable, Heads H, float scale, uint16_t *__restrict__ out,
+    float *new_state) {
   constexpr int kRows = 4 * WAVES * PASSES;
   constexpr int kTiles = kDV / kRows;
   static_assert(kDV % kRows == 0, "row block must divide 128");
 
   if (enable != nullptr && *enable == 0) return;  // the batch went through the chunks
-  const int h = blockIdx.x % kHV;  // consecutive workgroups: the 8 heads
-  const int rest = blockIdx.x / kHV;
+  const int h = blockIdx.x % H.v;  // consecutive workgroups: the v-heads
+  const int rest = blockIdx.x / H.v;
   const int tile = rest % kTiles, s = rest / kTiles;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c4 = 4 * (lane & 15);
@@ -64,8 +65,8 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
     bos = s * fixed_len;
     len = fixed_len;
   }
-  const int hq = h >> 1;
-  const size_t sbase = (static_cast<size_t>(s) * kHV + h) * kDV * kDK;
+  const int hq = h / H.ratio;
+  const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;
   f32x4 Sa[PASSES], Sb[PASSES];  // columns c4.. and 64 + c4..
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
@@ -84,13 +85,13 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
     const float dtb = dt_bias[h];
     auto load_token = [&](int t, TokenIn<PASSES> &x) {
       const size_t tok = static_cast<size_t>(bos) + t;
-      const uint16_t *kp = k + (tok * kHQK + hq) * kDK + c4;
-      const uint16_t *qp = q + (tok * kHQK + hq) * kDK + c4;
+      const uint16_t *kp = k + (tok * H.qk + hq) * kDK + c4;
+      const uint16_t *qp = q + (tok * H.qk + hq) * kDK + c4;
       x.k0 = *reinterpret_cast<const u16x4 *>(kp);
       x.k1 = *reinterpret_cast<const u16x4 *>(kp + 64);
       x.q0 = *reinterpret_cast<const u16x4 *>(qp);
       x.q1 = *reinterpret_cast<const u16x4 *>(qp + 64);
-      const uint16_t *vp = v + (tok * kHV + h) * kDV + row0;
+      const uint16_t *vp = v + (tok * H.v + h) * kDV + row0;
 #pragma unroll
       for (int p = 0; p < PASSES; ++p) x.v[p] = vp[4 * p];
     };
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) pkq = fmaf(kf[e], qf[e], pkq);
       const float kq = row16_sum(pkq);
-      uint16_t *op = out + ((static_cast<size_t>(bos) + t) * kHV + h) * kDV + row0;
+      uint16_t *op = out + ((static_cast<size_t>(bos) + t) * H.v + h) * kDV + row0;
 #pragma unroll
       for (int p = 0; p < PASSES; ++p) {
         float sk0 = 0.f, sk1 = 0.f, sq0 = 0.f, sq1 = 0.f;
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
     const int last = len - 1;
     auto gate_idx = [&](int t0) {  // gating input of token t0 + lane (clamped)
       const int t = t0 + (lane & (kDepth - 1));
-      return (static_cast<size_t>(bos) + (t < last ? t : last)) * kHV + h;
+      return (static_cast<size_t>(bos) + (t < last ? t : last)) * H.v + h;
     };
     uint16_t a_raw = a[gate_idx(0)], b_raw = b[gate_idx(0)];
     TokenIn<PASSES> ring[kDepth];
@@ -210,11 +211,12 @@ template <int W, int P>
 void launch_rec(long long groups, hipStream_t stream, const uint16_t *q, const uint16_t *k,
                 const uint16_t *v, const float *state, const float *A_log, const uint16_t *a,
                 const float *dt_bias, const uint16_t *b, const void *cu, int cu64, int T,
-                int fixed_len, const int *enable, float scale, uint16_t *out, float *new_state) {
+                int fixed_len, const int *enable, const Heads &H, float scale, uint16_t *out,
+                float *new_state) {
   const long long blocks = groups * (kDV / (4 * W * P));
   hipLaunchKernelGGL((recurrent_kernel<W, P>), dim3(static_cast<unsigned>(blocks)), dim3(64 * W),
                      0, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T, fixed_len,
-                     enable, scale, out, new_state);
+                     enable, H, scale, out, new_state);
 }
 
 }  // namespace
@@ -233,9 +235,10 @@ int recurrent_default_variant(long long groups) {
 int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
                      const float *A_log, const uint16_t *a, const float *dt_bias,
                      const uint16_t *b, const void *cu, int cu64, int num_seqs, int T,
-                     int fixed_len, const int *enable, float scale, uint16_t *out,
-                     float *new_state, hipStream_t stream, int variant, const char *what) {
-  const long long groups = static_cast<long long>(num_seqs) * kHV;
+                     int fixed_len, const int *enable, const Heads &H, float scale,
+                     uint16_t *out, float *new_state, hipStream_t stream, int variant,
+                     const char *what) {
+  const long long groups = static_cast<long long>(num_seqs) * H.v;
   if (variant < 0) variant = recurrent_default_variant(groups);
   if (variant >= kNumRecVariants)
     return fail(GDN_ERR_INVALID, "%s: recurrent tiling %d out of range", what, variant);
@@ -245,7 +248,7 @@ int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, co
 #define GDN_REC(W, P)                                                                          \
   if (rv.waves == W && rv.passes == P)                                                        \
     launch_rec<W, P>(groups, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T,       \
-                     fixed_len, enable, scale, out, new_state);
+                     fixed_len, enable, H, scale, out, new_state);
   GDN_REC(1, 1)
   GDN_REC(2, 1)
   GDN_REC(4, 1)
@@ -262,50 +265,77 @@ int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, co
 
 }  // namespace gdn
 
+namespace gdn {
+
+// T >= 1 tokens per row for `batch` rows with head layout (hqk, hv).
+static int multi_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                        const float *state, const float *A_log, const gdn_bf16 *a,
+                        const float *dt_bias, const gdn_bf16 *b, float scale, gdn_bf16 *output,
+                        float *new_state, int batch, int tokens, int hqk, int hv, void *stream,
+                        int variant, const char *what) {
+  clear_error();
+  Heads H;
+  if (int rc = make_heads(hqk, hv, what, H)) return rc;
+  if (batch < 0 || tokens < 1)
+    return fail(GDN_ERR_INVALID, "%s: batch=%d, tokens=%d", what, batch, tokens);
+  if (!q || !k || !v || !A_log || !a || !dt_bias || !b || !output || !new_state)
+    return fail(GDN_ERR_INVALID, "%s: null pointer argument", what);
+  if (!(scale > 0.0f) || scale == __builtin_inff())
+    return fail(GDN_ERR_INVALID, "%s: scale must be finite and > 0", what);
+  if (!aligned(new_state, 16) || (state && !aligned(state, 16)))
+    return fail(GDN_ERR_INVALID, "%s: state/new_state must be 16-byte aligned", what);
+  if (!aligned(q, 8) || !aligned(k, 8))
+    return fail(GDN_ERR_INVALID, "%s: q/k must be 8-byte aligned", what);
+  if (variant < -1 || variant >= recurrent_num_variants())
+    return fail(GDN_ERR_INVALID, "%s: unknown variant %d", what, variant);
+  const long long total = static_cast<long long>(batch) * tokens;
+  if (total > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "%s: batch*tokens too large", what);
+  if (batch == 0) return GDN_OK;
+  const size_t nb = static_cast<size_t>(batch), nt = static_cast<size_t>(total);
+  const size_t nV = static_cast<size_t>(H.v), nQK = static_cast<size_t>(H.qk);
+  const size_t state_bytes = nb * nV * kDV * kDK * sizeof(float);
+  const size_t out_bytes = nt * nV * kDV * sizeof(uint16_t);
+  if (state != new_state && overlaps(state, state_bytes, new_state, state_bytes))
+    return fail(GDN_ERR_INVALID, "%s: new_state partially overlaps state", what);
+  const void *ins[] = {q, k, v, a, b, A_log, dt_bias, state};
+  const size_t in_bytes[] = {nt * nQK * kDK * 2, nt * nQK * kDK * 2, nt * nV * kDV * 2,
+                             nt * nV * 2,        nt * nV * 2,        nV * 4,
+                             nV * 4,             state ? state_bytes : 0};
+  for (int i = 0; i < 8; ++i) {
+    if (overlaps(output, out_bytes, ins[i], in_bytes[i]))
+      return fail(GDN_ERR_INVALID, "%s: output overlaps an input", what);
+    if (i < 7 && overlaps(new_state, state_bytes, ins[i], in_bytes[i]))
+      return fail(GDN_ERR_INVALID, "%s: new_state overlaps an input", what);
+  }
+  if (overlaps(output, out_bytes, new_state, state_bytes))
+    return fail(GDN_ERR_INVALID, "%s: output overlaps new_state", what);
+  // One token per row is the plain decode step, whose kernel is tuned for it.
+  if (tokens == 1 && variant == -1)
+    return decode_launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
+                         stream, -1, H, what);
+  return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, nullptr, 0, batch,
+                          static_cast<int>(total), tokens, nullptr, H, scale, output, new_state,
+                          static_cast<hipStream_t>(stream), variant, what);
+}
+
+}  // namespace gdn
+
 extern "C" int gdn_decode_multi_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                                     const float *state, const float *A_log, const gdn_bf16 *a,
                                     const float *dt_bias, const gdn_bf16 *b, float scale,
                                     gdn_bf16 *output, float *new_state, int batch, int tokens,
                                     void *stream, int variant) {
-  using namespace gdn;
-  clear_error();
-  if (batch < 0 || tokens < 1)
-    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: batch=%d, tokens=%d", batch, tokens);
-  if (!q || !k || !v || !A_log || !a || !dt_bias || !b || !output || !new_state)
-    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: null pointer argument");
-  if (!(scale > 0.0f) || scale == __builtin_inff())
-    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: scale must be finite and > 0");
-  if (!aligned(new_state, 16) || (state && !aligned(state, 16)))
-    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: state/new_state must be 16-byte aligned");
-  if (!aligned(q, 8) || !aligned(k, 8))
-    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: q/k must be 8-byte aligned");
-  if (variant < -1 || variant >= recurrent_num_variants())
-    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: unknown variant %d", variant);
-  const long long total = static_cast<long long>(batch) * tokens;
-  if (total > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: batch*tokens too large");
-  if (batch == 0) return GDN_OK;
-  const size_t nb = static_cast<size_t>(batch), nt = static_cast<size_t>(total);
-  const size_t state_bytes = nb * kHV * kDV * kDK * sizeof(float);
-  const size_t out_bytes = nt * kHV * kDV * sizeof(uint16_t);
-  if (state != new_state && overlaps(state, state_bytes, new_state, state_bytes))
-    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: new_state partially overlaps state");
-  const void *ins[] = {q, k, v, a, b, A_log, dt_bias, state};
-  const size_t in_bytes[] = {nt * kHQK * kDK * 2, nt * kHQK * kDK * 2, nt * kHV * kDV * 2,
-                             nt * kHV * 2,        nt * kHV * 2,        kHV * 4,
-                             kHV * 4,             state ? state_bytes : 0};
-  for (int i = 0; i < 8; ++i) {
-    if (overlaps(output, out_bytes, ins[i], in_bytes[i]))
-      return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: output overlaps an input");
-    if (i < 7 && overlaps(new_state, state_bytes, ins[i], in_bytes[i]))
-      return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: new_state overlaps an input");
-  }
-  if (overlaps(output, out_bytes, new_state, state_bytes))
-    return fail(GDN_ERR_INVALID, "gdn_decode_multi_fwd: output overlaps new_state");
-  // One token per row is the plain decode step, whose kernel is tuned for it.
-  if (tokens == 1 && variant == -1)
-    return gdn_decode_fwd(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
-                          stream);
-  return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, nullptr, 0, batch,
-                          static_cast<int>(total), tokens, nullptr, scale, output, new_state,
-                          static_cast<hipStream_t>(stream), variant, "gdn_decode_multi_fwd");
+  return gdn::multi_launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
+                           tokens, gdn::kHQK, gdn::kHV, stream, variant, "gdn_decode_multi_fwd");
+}
+
+extern "C" int gdn_decode_fwd_heads(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                                    const float *state, const float *A_log, const gdn_bf16 *a,
+                                    const float *dt_bias, const gdn_bf16 *b, float scale,
+                                    gdn_bf16 *output, float *new_state, int batch, int tokens,
+                                    int num_qk_heads, int num_v_heads, void *stream,
+                                    int variant) {
+  return gdn::multi_launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
+                           tokens, num_qk_heads, num_v_heads, stream, variant,
+                           "gdn_decode_fwd_heads");
 }

@@ -18,7 +18,7 @@ GDN_OK = 0
 GDN_ERR_INVALID = -1
 GDN_ERR_LAUNCH = -2
 GDN_ERR_WORKSPACE = -3
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -32,13 +32,18 @@ SIGNATURES = {
     "gdn_decode_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P]),
     "gdn_decode_fwd_variant": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _P, _I]),
     "gdn_decode_multi_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _P, _I]),
+    "gdn_decode_fwd_heads": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _I,
+                                  _P, _I]),
     "gdn_prefill_workspace_bytes": (_SZ, [_I, _I]),
+    "gdn_prefill_workspace_bytes_heads": (_SZ, [_I, _I, _I, _I]),
     "gdn_prefill_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P, _P,
                              _SZ, _P]),
     "gdn_prefill_fwd_variant": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P,
                                      _P, _SZ, _P, _I]),
     "gdn_prefill_fwd_tuned": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P,
                                    _P, _SZ, _P, _I, _I, _I]),
+    "gdn_prefill_fwd_heads": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
+                                   _P, _P, _P, _SZ, _P, _I, _I, _I]),
 }
 
 

@@ -7,9 +7,11 @@ reference/gdn_decode_ref.py:12-83 (state may be None; scale None/0.0 means
 1/sqrt(128)).  The work is one launch of the HIP kernel behind
 ``gdn_decode_fwd`` (include/gdn_amd.h) on torch's current stream.
 
-Beyond the reference (whose decode asserts T == 1): tensors with T > 1 tokens
-per row ([B, T, ...], multi-token / speculative decode) run the tokens in
-order through ``gdn_decode_multi_fwd``, the state written once at the end.
+Beyond the reference (whose decode asserts T == 1 and 4/8 heads): tensors
+with T > 1 tokens per row ([B, T, ...], multi-token / speculative decode) run
+the tokens in order through ``gdn_decode_multi_fwd``, the state written once
+at the end; other head layouts (q/k heads from ``q``, v-heads from ``v``, the
+latter a multiple of the former) run through ``gdn_decode_fwd_heads``.
 """
 
 from __future__ import annotations
@@ -25,6 +27,13 @@ _F32 = torch.float32
 _DTYPES = (_BF, _BF, _BF, _F32, _BF, _F32, _BF, _BF, _F32)
 
 
+def _heads(q, v):
+    """(q/k heads, v-heads) of a call: 4 and 8 for the reference definition."""
+    hqk = q.shape[2] if isinstance(q, torch.Tensor) and q.dim() == 4 else H_QK
+    hv = v.shape[2] if isinstance(v, torch.Tensor) and v.dim() == 4 else HV
+    return hqk, hv
+
+
 def _validate(q, k, v, state, A_log, a, dt_bias, b, output, new_state):
     if not isinstance(q, torch.Tensor) or q.dim() != 4 or q.shape[1] < 1:
         raise ValueError("q must be a [B, T, 4, 128] tensor with T >= 1")
@@ -32,6 +41,9 @@ def _validate(q, k, v, state, A_log, a, dt_bias, b, output, new_state):
     dev = q.device
     if dev.type != "cuda":
         raise ValueError(f"q is on {dev}; the HIP kernels need device tensors")
+    H_QK, HV = _heads(q, v)
+    if H_QK < 1 or HV < 1 or HV % H_QK:
+        raise ValueError(f"v-heads ({HV}) must be a multiple of q/k heads ({H_QK})")
     bf, f32 = torch.bfloat16, torch.float32
     check_tensor("q", q, (B, T, H_QK, DK), bf, dev)
     check_tensor("k", k, (B, T, H_QK, DK), bf, dev)
@@ -64,6 +76,7 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, *, va
     four = isinstance(q, torch.Tensor) and q.dim() == 4
     B = q.shape[0] if four else -1
     T = q.shape[1] if four else -1
+    H_QK, HV = _heads(q, v)
     ts = (q, k, v, A_log, a, dt_bias, b, output, new_state)
     shapes = ((B, T, H_QK, DK), (B, T, H_QK, DK), (B, T, HV, DV), (HV,), (B, T, HV), (HV,),
               (B, T, HV), (B, T, HV, DV), (B, HV, DV, DK))
@@ -80,6 +93,10 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, *, va
             None if state is None else state.data_ptr(), A_log.data_ptr(), a.data_ptr(),
             dt_bias.data_ptr(), b.data_ptr(), scale, output.data_ptr(), new_state.data_ptr(),
             B)
+    if (H_QK, HV) != (4, 8):
+        rc = lib.gdn_decode_fwd_heads(*args, T, H_QK, HV, stream_of(dev), int(variant))
+        _lib.check(rc, "gdn_decode_fwd_heads")
+        return
     if T > 1:
         rc = lib.gdn_decode_multi_fwd(*args, T, stream_of(dev), int(variant))
         _lib.check(rc, "gdn_decode_multi_fwd")
@@ -96,6 +113,7 @@ def run(q, k, v, state, A_log, a, dt_bias, b, scale):
     """Non-DPS form with the reference's return convention
     (reference/gdn_decode_ref.py:12, returns (output, new_state))."""
     B, T = q.shape[0], q.shape[1]
+    HV = v.shape[2]
     output = torch.empty((B, T, HV, DV), dtype=torch.bfloat16, device=q.device)
     new_state = torch.empty((B, HV, DV, DK), dtype=torch.float32, device=q.device)
     kernel(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state)

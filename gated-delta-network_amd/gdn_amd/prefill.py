@@ -31,16 +31,21 @@ _ws_lock = threading.Lock()
 _workspaces: dict = {}
 
 
-def workspace_bytes(total_tokens: int, num_seqs: int) -> int:
-    return int(_lib.load().gdn_prefill_workspace_bytes(int(total_tokens), int(num_seqs)))
+def workspace_bytes(total_tokens: int, num_seqs: int, heads=(H_QK, HV)) -> int:
+    """Workspace bytes for T tokens in N sequences with (q/k heads, v-heads)."""
+    lib = _lib.load()
+    if tuple(heads) == (H_QK, HV):
+        return int(lib.gdn_prefill_workspace_bytes(int(total_tokens), int(num_seqs)))
+    return int(lib.gdn_prefill_workspace_bytes_heads(int(total_tokens), int(num_seqs),
+                                                     int(heads[0]), int(heads[1])))
 
 
-def alloc_workspace(total_tokens: int, num_seqs: int, device=None) -> torch.Tensor:
+def alloc_workspace(total_tokens: int, num_seqs: int, device=None, heads=(H_QK, HV)) -> torch.Tensor:
     """A caller-owned workspace for ``kernel(..., workspace=...)``: uint8 bytes
     sized for any batch of ``total_tokens`` tokens in ``num_seqs`` sequences."""
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
-    return torch.empty(max(workspace_bytes(total_tokens, num_seqs), 256), dtype=torch.uint8,
-                       device=dev)
+    return torch.empty(max(workspace_bytes(total_tokens, num_seqs, heads), 256),
+                       dtype=torch.uint8, device=dev)
 
 
 def _check_workspace(ws, dev: torch.device, nbytes: int) -> None:
@@ -70,7 +75,12 @@ def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
 def _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state):
     if not isinstance(q, torch.Tensor) or q.dim() != 3:
         raise ValueError("q must be a [T, 4, 128] tensor")
+    if not isinstance(v, torch.Tensor) or v.dim() != 3:
+        raise ValueError("v must be a [T, 8, 128] tensor")
     T = q.shape[0]
+    H_QK, HV = q.shape[1], v.shape[1]
+    if H_QK < 1 or HV < 1 or HV % H_QK:
+        raise ValueError(f"v-heads ({HV}) must be a multiple of q/k heads ({H_QK})")
     dev = q.device
     if dev.type != "cuda":
         raise ValueError(f"q is on {dev}; the HIP kernels need device tensors")
@@ -95,7 +105,7 @@ def _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_stat
     check_tensor("new_state", new_state, (N, HV, DV, DK), f32, dev)
     check_output("output", output)
     check_output("new_state", new_state)
-    return T, N, dev
+    return T, N, dev, (H_QK, HV)
 
 
 def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state, *,
@@ -116,14 +126,15 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
     ``recurrent_variant``: that kernel's row tiling (gdn_prefill_fwd_tuned).
     """
     lib = _lib.load()
-    T, N, dev = _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state)
+    T, N, dev, heads = _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output,
+                                 new_state)
     scale = resolve_scale(scale)
     if state is not None and state.data_ptr() != new_state.data_ptr():
         state = dense(state)
     q, k, v, a, b, A_log, dt_bias, cu_seqlens = (
         dense(t) for t in (q, k, v, a, b, A_log, dt_bias, cu_seqlens))
     stream = stream_of(dev)
-    nbytes = int(lib.gdn_prefill_workspace_bytes(T, N))
+    nbytes = workspace_bytes(T, N, heads)
     if workspace is None:
         ws = _workspace(dev, stream, nbytes)
     else:
@@ -133,7 +144,10 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
             A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), b.data_ptr(),
             cu_seqlens.data_ptr(), 1 if cu_seqlens.dtype == torch.int64 else 0, N, T, scale,
             output.data_ptr(), new_state.data_ptr(), ws.data_ptr(), ws.numel(), stream)
-    if recurrent_max_len != -1 or recurrent_variant != -1:
+    if heads != (H_QK, HV):
+        rc = lib.gdn_prefill_fwd_heads(*args[:12], heads[0], heads[1], *args[12:], int(variant),
+                                       int(recurrent_max_len), int(recurrent_variant))
+    elif recurrent_max_len != -1 or recurrent_variant != -1:
         rc = lib.gdn_prefill_fwd_tuned(*args, int(variant), int(recurrent_max_len),
                                        int(recurrent_variant))
     elif variant == -1:
@@ -147,6 +161,7 @@ def run(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale):
     """Non-DPS form with the reference's return convention
     (reference/gdn_prefill_ref.py:12, returns (output, new_state))."""
     T, N = q.shape[0], cu_seqlens.numel() - 1
+    HV = v.shape[1]
     output = torch.empty((T, HV, DV), dtype=torch.bfloat16, device=q.device)
     new_state = torch.empty((N, HV, DV, DK), dtype=torch.float32, device=q.device)
     kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_state)

@@ -101,6 +101,23 @@ int gdn_decode_multi_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v
                          int variant);
 
 /*
+ * Decode for any head layout: num_qk_heads q/k heads and num_v_heads v-heads
+ * (a multiple of num_qk_heads; v-head h reads q/k head h / (num_v_heads /
+ * num_qk_heads)), head size 128, `tokens` >= 1 per row.  No counterpart in the
+ * reference, whose definitions fix 4/8 heads (reference/gdn_decode_ref.py:32-36);
+ * the contest behind it names other layouts such as 16/32 (FAQ.md:109-111).
+ * Tensors are those of gdn_decode_multi_fwd with 4 -> num_qk_heads and
+ * 8 -> num_v_heads.  variant: with tokens == 1 and -1 the decode kernel's
+ * built-in tiling; otherwise the token-sequential kernel's tiling (as for
+ * gdn_decode_multi_fwd).
+ */
+int gdn_decode_fwd_heads(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                         const float *state, const float *A_log, const gdn_bf16 *a,
+                         const float *dt_bias, const gdn_bf16 *b, float scale,
+                         gdn_bf16 *output, float *new_state, int batch, int tokens,
+                         int num_qk_heads, int num_v_heads, void *stream, int variant);
+
+/*
  * Bytes of device workspace gdn_prefill_fwd needs for a packed batch of
  * total_tokens tokens in num_seqs sequences.  The bound does not depend on the
  * individual lengths (they stay on the device), so a caller can size it once.
@@ -178,6 +195,25 @@ int gdn_prefill_fwd_tuned(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
                           gdn_bf16 *output, float *new_state, void *workspace,
                           size_t workspace_bytes, void *stream, int state_tiling,
                           int recurrent_max_len, int recurrent_tiling);
+
+/*
+ * Prefill for any head layout (see gdn_decode_fwd_heads): the workspace size
+ * and gdn_prefill_fwd_tuned with num_qk_heads / num_v_heads in place of 4 / 8
+ * (q, k [T, num_qk_heads, 128]; v, output [T, num_v_heads, 128]; a, b
+ * [T, num_v_heads]; A_log, dt_bias [num_v_heads]; state, new_state
+ * [N, num_v_heads, 128, 128]).  No counterpart in the reference (4/8 heads
+ * only, reference/gdn_prefill_ref.py:33-36).  The workspace size is 0 for an
+ * invalid layout.
+ */
+size_t gdn_prefill_workspace_bytes_heads(int total_tokens, int num_seqs, int num_qk_heads,
+                                         int num_v_heads);
+int gdn_prefill_fwd_heads(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                          const float *state, const float *A_log, const gdn_bf16 *a,
+                          const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
+                          int cu_seqlens_is_int64, int num_seqs, int total_tokens,
+                          int num_qk_heads, int num_v_heads, float scale, gdn_bf16 *output,
+                          float *new_state, void *workspace, size_t workspace_bytes, void *stream,
+                          int state_tiling, int recurrent_max_len, int recurrent_tiling);
 
 #ifdef __cplusplus
 }

@@ -120,9 +120,19 @@ def gating(A_log, a, dt_bias, b, dtype=np.float32):
 # decode
 # --------------------------------------------------------------------------
 
-def _expand_heads(x):
-    """GVA: v-head h reads q/k head h // 2 (repeat_interleave, gdn_decode_ref.py:57-58)."""
-    return np.repeat(x, GVA, axis=-2)
+def _expand_heads(x, hv):
+    """GVA: v-head h reads q/k head h // (HV / HQK) (repeat_interleave,
+    gdn_decode_ref.py:57-58); ``hv`` = number of v-heads."""
+    hqk = x.shape[-2]
+    assert hv % hqk == 0, "v-heads must be a multiple of q/k heads"
+    return np.repeat(x, hv // hqk, axis=-2)
+
+
+def _heads(q, v):
+    """(q/k heads, v-heads) from the tensors: 4 and 8 for the reference
+    definitions (gdn_decode_ref.py:32-36); other counts for the generalised
+    head configurations, with the same per-head size 128."""
+    return q.shape[-2], v.shape[-2]
 
 
 def decode(q, k, v, state, A_log, a, dt_bias, b, scale, dtype=np.float32):
@@ -130,17 +140,19 @@ def decode(q, k, v, state, A_log, a, dt_bias, b, scale, dtype=np.float32):
 
     q, k: [B,1,4,128]; v: [B,1,8,128]; state: [B,8,128,128] (k-last, [V,K]) or
     None; A_log, dt_bias: [8]; a, b: [B,1,8]. Returns (o [B,1,8,128] as
-    bf16-rounded float32, new_state [B,8,128,128] in ``dtype``).
+    bf16-rounded float32, new_state [B,8,128,128] in ``dtype``).  Other head
+    counts (HQK q/k heads, HV v-heads, HV a multiple of HQK) follow the shapes.
     """
     B = q.shape[0]
-    assert q.shape[1:] == (1, H_QK, DK) and k.shape[1:] == (1, H_QK, DK)
+    hqk, HV = _heads(q, v)
+    assert q.shape[1:] == (1, hqk, DK) and k.shape[1:] == (1, hqk, DK)
     assert v.shape[1:] == (1, HV, DV)
     scale = resolve_scale(scale)
     g, beta = gating(A_log, a, dt_bias, b, dtype)
     g = g[:, 0]  # [B,HV]
     beta = beta[:, 0]
-    qe = _expand_heads(np.asarray(q[:, 0], dtype=dtype))  # [B,HV,K]
-    ke = _expand_heads(np.asarray(k[:, 0], dtype=dtype))
+    qe = _expand_heads(np.asarray(q[:, 0], dtype=dtype), HV)  # [B,HV,K]
+    ke = _expand_heads(np.asarray(k[:, 0], dtype=dtype), HV)
     vf = np.asarray(v[:, 0], dtype=dtype)  # [B,HV,V]
     if state is None:
         S = np.zeros((B, HV, DK, DV), dtype=dtype)  # [K,V] view
@@ -163,10 +175,11 @@ def decode_loop(q, k, v, state, A_log, a, dt_bias, b, scale):
     Used as the timed CPU baseline; numerically the same op order as decode().
     """
     B = q.shape[0]
+    _, HV = _heads(q, v)
     scale = np.float32(resolve_scale(scale))
     g, beta = gating(A_log, a, dt_bias, b)
-    qe = _expand_heads(np.asarray(q[:, 0], dtype=np.float32))
-    ke = _expand_heads(np.asarray(k[:, 0], dtype=np.float32))
+    qe = _expand_heads(np.asarray(q[:, 0], dtype=np.float32), HV)
+    ke = _expand_heads(np.asarray(k[:, 0], dtype=np.float32), HV)
     vf = np.asarray(v[:, 0], dtype=np.float32)
     st = (np.zeros((B, HV, DV, DK), np.float32) if state is None
           else np.asarray(state, dtype=np.float32))
@@ -192,9 +205,10 @@ def decode_loop(q, k, v, state, A_log, a, dt_bias, b, scale):
 
 def _check_prefill_shapes(q, k, v, a, b, cu_seqlens):
     T = q.shape[0]
-    assert q.shape == (T, H_QK, DK) and k.shape == (T, H_QK, DK)
-    assert v.shape == (T, HV, DV)
-    assert a.shape == (T, HV) and b.shape == (T, HV)
+    hqk, hv = _heads(q, v)
+    assert q.shape == (T, hqk, DK) and k.shape == (T, hqk, DK)
+    assert v.shape == (T, hv, DV) and hv % hqk == 0
+    assert a.shape == (T, hv) and b.shape == (T, hv)
     cu = np.asarray(cu_seqlens, dtype=np.int64)
     assert cu.ndim == 1 and cu.size >= 1
     return T, cu
@@ -211,10 +225,11 @@ def prefill_seq(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale,
     """
     T, cu = _check_prefill_shapes(q, k, v, a, b, cu_seqlens)
     N = cu.size - 1
+    _, HV = _heads(q, v)
     scale = dtype(resolve_scale(scale))
     g, beta = gating(A_log, a, dt_bias, b, dtype)  # [T,HV]
-    qe = _expand_heads(np.asarray(q, dtype=dtype))
-    ke = _expand_heads(np.asarray(k, dtype=dtype))
+    qe = _expand_heads(np.asarray(q, dtype=dtype), HV)
+    ke = _expand_heads(np.asarray(k, dtype=dtype), HV)
     vf = np.asarray(v, dtype=dtype)
     out = np.zeros((T, HV, DV), np.float32)
     new_state = np.zeros((N, HV, DV, DK), dtype)
@@ -302,12 +317,13 @@ def prefill_chunked(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale,
     """
     T, cu = _check_prefill_shapes(q, k, v, a, b, cu_seqlens)
     N = cu.size - 1
+    _, HV = _heads(q, v)
     f = np.float64
     scale = resolve_scale(scale)
     glog = log_decay(A_log, a, dt_bias, f)  # [T,HV]
     beta = 1.0 / (1.0 + np.exp(-np.asarray(b, f)))
-    qe = _expand_heads(np.asarray(q, f))
-    ke = _expand_heads(np.asarray(k, f))
+    qe = _expand_heads(np.asarray(q, f), HV)
+    ke = _expand_heads(np.asarray(k, f), HV)
     vf = np.asarray(v, f)
     out = np.zeros((T, HV, DV), f)
     new_state = np.zeros((N, HV, DV, DK), f)
@@ -378,10 +394,12 @@ def _l2norm_bf16(x):
     return bf16_round(x.astype(np.float32))
 
 
-def make_decode_inputs(B: int, seed: int = 0, with_state: bool = True):
+def make_decode_inputs(B: int, seed: int = 0, with_state: bool = True, heads=(H_QK, HV)):
     """Decode inputs of configs[0]/[1]: numpy default_rng(seed), draw order
     q, k, v, state, A_log, a, dt_bias, b; q/k L2-normalised per head then
-    rounded to bf16; state ~ N(0, 0.05^2) (0.05 read as the std. deviation)."""
+    rounded to bf16; state ~ N(0, 0.05^2) (0.05 read as the std. deviation).
+    ``heads`` = (q/k heads, v-heads), (4, 8) for the reference definitions."""
+    H_QK, HV = heads
     rng = np.random.default_rng(seed)
     q = _l2norm_bf16(rng.standard_normal((B, 1, H_QK, DK)))
     k = _l2norm_bf16(rng.standard_normal((B, 1, H_QK, DK)))
@@ -396,12 +414,13 @@ def make_decode_inputs(B: int, seed: int = 0, with_state: bool = True):
 
 
 def make_prefill_inputs(lens, seed: int = 0, with_state: bool = True,
-                        slow_decay_heads=()):
+                        slow_decay_heads=(), heads=(H_QK, HV)):
     """Prefill inputs of configs[2]-[4] (same recipe as make_decode_inputs).
 
     ``slow_decay_heads`` get A_log = -10 (decay ~ 1 - 5e-5 per token), the
     skew configs[4] asks for.  Returns the tensors plus cu_seqlens (int64).
     """
+    H_QK, HV = heads
     lens = [int(x) for x in lens]
     T = sum(lens)
     N = len(lens)
@@ -482,7 +501,8 @@ def _clib():
         lib = ctypes.CDLL(path)
         P = ctypes.c_void_p
         lib.gdn_oracle_prefill_seq.argtypes = [P, P, P, P, P, P, P, ctypes.c_int,
-                                               ctypes.c_float, P, P, ctypes.c_int]
+                                               ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                               P, P, ctypes.c_int]
         lib.gdn_oracle_prefill_seq.restype = ctypes.c_int
         _CLIB = lib
     return _CLIB
@@ -495,6 +515,7 @@ def prefill_seq_c(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale,
     numpy float32 gating() above.  Returns (o bf16-rounded float32, new_state)."""
     T, cu = _check_prefill_shapes(q, k, v, a, b, cu_seqlens)
     N = cu.size - 1
+    hqk, HV = _heads(q, v)
     g, beta = gating(A_log, a, dt_bias, b, np.float32)
     arrs = [np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v, g, beta)]
     st = None if state is None else np.ascontiguousarray(state, dtype=np.float32)
@@ -502,7 +523,7 @@ def prefill_seq_c(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale,
     o = np.zeros((T, HV, DV), np.float32)
     ns = np.zeros((N, HV, DV, DK), np.float32)
     ptr = lambda x: None if x is None else x.ctypes.data
-    rc = _clib().gdn_oracle_prefill_seq(*[ptr(x) for x in arrs], ptr(st), ptr(cu), N,
+    rc = _clib().gdn_oracle_prefill_seq(*[ptr(x) for x in arrs], ptr(st), ptr(cu), N, hqk, HV,
                                         float(resolve_scale(scale)), ptr(o), ptr(ns),
                                         1 if use_f64 else 0)
     if rc != 0:

@@ -9,14 +9,16 @@
  * holds only the recurrence.  Every (sequence, v-head) pair is independent and
  * runs on its own OpenMP thread.
  *
- * Inputs are float32 arrays (bf16 tensors arrive as their exact float values):
- *   q, k      [T, 4, 128]        v        [T, 8, 128]
- *   g, beta   [T, 8]             (multiplicative decay and sigmoid(b))
- *   state     [N, 8, 128, 128]   k-last ([V, K]); may be NULL (zeros)
+ * Inputs are float32 arrays (bf16 tensors arrive as their exact float values);
+ * HQK q/k heads and HV v-heads (4 and 8 for the reference definitions; v-head
+ * h reads q/k head h / (HV / HQK)):
+ *   q, k      [T, HQK, 128]      v        [T, HV, 128]
+ *   g, beta   [T, HV]            (multiplicative decay and sigmoid(b))
+ *   state     [N, HV, 128, 128]  k-last ([V, K]); may be NULL (zeros)
  *   cu        [N + 1] int64
  * Outputs:
- *   o         [T, 8, 128] float32, NOT rounded to bf16 (the caller rounds)
- *   new_state [N, 8, 128, 128] float32 (zeros for a zero-length sequence,
+ *   o         [T, HV, 128] float32, NOT rounded to bf16 (the caller rounds)
+ *   new_state [N, HV, 128, 128] float32 (zeros for a zero-length sequence,
  *             reference/gdn_prefill_ref.py:61-62)
  * use_f64 != 0 evaluates the recurrence in double precision instead.
  */
@@ -24,14 +26,12 @@
 #include <stdlib.h>
 #include <string.h>
 
-#define HQK 4
-#define NHV 8
 #define DK 128
 #define DV 128
 
 static void run_head_f32(const float *q, const float *k, const float *v, const float *g,
                          const float *beta, const float *s0, int64_t bos, int64_t eos,
-                         int h, float scale, float *o, float *s_out) {
+                         int h, int HQK, int NHV, float scale, float *o, float *s_out) {
   /* S is held as [K][V] (the reference's transposed view, gdn_prefill_ref.py:65). */
   float *S = (float *)malloc(sizeof(float) * DK * DV);
   float old_v[DV], new_v[DV];
@@ -64,7 +64,7 @@ static void run_head_f32(const float *q, const float *k, const float *v, const f
 
 static void run_head_f64(const float *q, const float *k, const float *v, const float *g,
                          const float *beta, const float *s0, int64_t bos, int64_t eos,
-                         int h, float scale, float *o, float *s_out) {
+                         int h, int HQK, int NHV, float scale, float *o, float *s_out) {
   double *S = (double *)malloc(sizeof(double) * DK * DV);
   double old_v[DV], new_v[DV], acc[DV];
   const int hq = h / (NHV / HQK);
@@ -96,8 +96,9 @@ static void run_head_f64(const float *q, const float *k, const float *v, const f
 
 int gdn_oracle_prefill_seq(const float *q, const float *k, const float *v, const float *g,
                            const float *beta, const float *state, const int64_t *cu, int N,
-                           float scale, float *o, float *new_state, int use_f64) {
-  if (N < 0) return -1;
+                           int HQK, int NHV, float scale, float *o, float *new_state,
+                           int use_f64) {
+  if (N < 0 || HQK < 1 || NHV < 1 || NHV % HQK != 0) return -1;
   for (int s = 0; s < N; ++s)
     if (cu[s + 1] < cu[s]) return -1;
   memset(new_state, 0, sizeof(float) * (size_t)N * NHV * DV * DK);
@@ -109,9 +110,9 @@ int gdn_oracle_prefill_seq(const float *q, const float *k, const float *v, const
       const float *s0 = state ? state + ((size_t)s * NHV + h) * DV * DK : NULL;
       float *so = new_state + ((size_t)s * NHV + h) * DV * DK;
       if (use_f64)
-        run_head_f64(q, k, v, g, beta, s0, bos, eos, h, scale, o, so);
+        run_head_f64(q, k, v, g, beta, s0, bos, eos, h, HQK, NHV, scale, o, so);
       else
-        run_head_f32(q, k, v, g, beta, s0, bos, eos, h, scale, o, so);
+        run_head_f32(q, k, v, g, beta, s0, bos, eos, h, HQK, NHV, scale, o, so);
     }
   }
   return 0;

@@ -172,3 +172,41 @@ def test_prefill_tuned_rejects_bad_tuning(tuning, needle):
     rc = lib.gdn_prefill_fwd_tuned(*_prefill_args(), *tuning)
     assert rc == _lib.GDN_ERR_INVALID
     assert needle in _lib.last_error()
+
+
+def _heads_args(hqk, hv):
+    return _multi_args()[:-2] + [hqk, hv, None, -1]
+
+
+@pytest.mark.parametrize("hqk, hv", [(3, 8), (0, 8), (4, 0), (2048, 2048), (8, 4)])
+def test_decode_heads_rejects_bad_heads(hqk, hv):
+    lib = _lib.load()
+    rc = lib.gdn_decode_fwd_heads(*_heads_args(hqk, hv))
+    assert rc == _lib.GDN_ERR_INVALID
+    assert "heads" in _lib.last_error()
+
+
+def test_decode_heads_zero_batch_is_a_no_op():
+    lib = _lib.load()
+    args = _multi_args(batch=0)[:-2] + [16, 32, None, -1]
+    assert lib.gdn_decode_fwd_heads(*args) == _lib.GDN_OK
+
+
+def test_prefill_workspace_bytes_heads():
+    lib = _lib.load()
+    for T, N in ((0, 0), (64, 1), (8192, 1), (8192, 4), (300, 7)):
+        assert lib.gdn_prefill_workspace_bytes_heads(T, N, 4, 8) == \
+            lib.gdn_prefill_workspace_bytes(T, N)
+    assert lib.gdn_prefill_workspace_bytes_heads(8192, 1, 16, 32) > \
+        lib.gdn_prefill_workspace_bytes(8192, 1)
+    for hqk, hv in ((3, 8), (0, 8), (4, 0), (2048, 2048)):
+        assert lib.gdn_prefill_workspace_bytes_heads(64, 1, hqk, hv) == 0
+
+
+@pytest.mark.parametrize("hqk, hv", [(3, 8), (0, 8), (8, 4)])
+def test_prefill_heads_rejects_bad_heads(hqk, hv):
+    lib = _lib.load()
+    a = _prefill_args()
+    rc = lib.gdn_prefill_fwd_heads(*a[:12], hqk, hv, *a[12:], -1, -1, -1)
+    assert rc == _lib.GDN_ERR_INVALID
+    assert "heads" in _lib.last_error()

@@ -361,3 +361,57 @@ def test_work_formulas():
     assert O.decode_bytes(1) == 1_054_816
     assert O.prefill_bytes(8192, 1) == 51_642_448
     assert O.prefill_flops(128) == 128 * 8 * 11_534_336
+
+
+# ---------------------------------------------------------------------------
+# generalised head configurations (q/k heads HQK, v-heads HV = multiple of HQK)
+# ---------------------------------------------------------------------------
+
+HEAD_CONFIGS = [(16, 32), (2, 8), (1, 1)]
+
+
+@pytest.mark.parametrize("heads", HEAD_CONFIGS)
+def test_decode_general_heads_equals_per_head_problems(heads):
+    # Each v-head h is an independent single-head problem on q/k head
+    # h // (HV / HQK): a wrong head map (h % HQK, h // 2, ...) fails here.
+    hqk, hv = heads
+    inp = O.make_decode_inputs(3, seed=5, heads=heads)
+    o, s = O.decode(**inp)
+    ratio = hv // hqk
+    for h in range(hv):
+        one = dict(inp)
+        for n in ("q", "k"):
+            one[n] = inp[n][:, :, h // ratio:h // ratio + 1]
+        one["v"] = inp["v"][:, :, h:h + 1]
+        one["a"] = inp["a"][:, :, h:h + 1]
+        one["b"] = inp["b"][:, :, h:h + 1]
+        one["A_log"] = inp["A_log"][h:h + 1]
+        one["dt_bias"] = inp["dt_bias"][h:h + 1]
+        one["state"] = inp["state"][:, h:h + 1]
+        o1, s1 = O.decode(**one)
+        np.testing.assert_array_equal(o[:, :, h:h + 1], o1)
+        np.testing.assert_array_equal(s[:, h:h + 1], s1)
+
+
+@pytest.mark.parametrize("heads", [(16, 32), (2, 8)])
+def test_prefill_general_heads_chained_decode_and_c(heads):
+    # prefill(L) == L decode steps, the C recurrence == numpy, and the chunked
+    # float64 form == the sequential one, at a non-reference head layout.
+    lens = [5, 0, 70]
+    inp = O.make_prefill_inputs(lens, seed=9, heads=heads)
+    o_seq, s_seq = O.prefill_seq(**inp, dtype=np.float64)
+    o_c, s_c = O.prefill_seq_c(**inp, use_f64=True)  # gating in float32 there
+    assert np.abs(s_c - s_seq).max() <= 1e-6 * np.abs(s_seq).max()
+    o_ch, s_ch = O.prefill_chunked(**inp)
+    assert np.abs(s_ch - s_seq).max() <= 1e-9 * np.abs(s_seq).max()
+    assert np.abs(o_ch - o_seq).max() <= 1e-2 * np.abs(o_seq).max()
+    cu = inp["cu_seqlens"]
+    for s_i, L in enumerate(lens):
+        st = inp["state"][s_i:s_i + 1].astype(np.float64)
+        for t in range(cu[s_i], cu[s_i + 1]):
+            step = {n: inp[n][t:t + 1][:, None] for n in ("q", "k", "v", "a", "b")}
+            o1, st = O.decode(state=st, A_log=inp["A_log"], dt_bias=inp["dt_bias"],
+                              scale=inp["scale"], dtype=np.float64, **step)
+            np.testing.assert_allclose(o1[0, 0], o_seq[t], rtol=1e-2, atol=1e-2)
+        want = st[0] if L > 0 else np.zeros_like(st[0])
+        assert np.abs(s_seq[s_i] - want).max() <= 1e-9 * max(np.abs(want).max(), 1.0)
