@@ -491,6 +491,29 @@ struct ChunkFrag {
   float eg;            // exp(G_last)
 };
 
+// Buffer descriptor (gfx9 word 3 = 0x00020000: raw 32-bit records) over
+// `bytes` bytes at a wave-uniform base.  Loads through it take the base in
+// SGPRs and a 32-bit per-lane byte offset that never changes across chunks,
+// so a prefetch loop needs no address registers: with 64-bit VGPR addresses
+// the compiler recomputed them every chunk and, reusing registers of loads
+// still in flight, had to wait for the newest prefetch set at the loop head.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+// One float at a wave-uniform address, as a vector load issued in program
+// order with the fragments it belongs to.
+__device__ __forceinline__ float buf_load_f32(const float *p) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(p, 4), 0u, 0, 0));
+}
+
+constexpr uint32_t kWBytes = kChunk * kDK * 4;    // w of one (chunk, head): hi + lo bf16
+constexpr uint32_t kKtBytes = kDK * kChunk * 2;   // K^T of one (chunk, q/k head)
+constexpr uint32_t kUBytes = kChunk * kDV * 4;    // u of one (chunk, head), f32
+
 __device__ __forceinline__ void load_chunk_frag(ChunkFrag &f, int c, int h, const Heads &H,
                                                 int vw, int wave, int lane, const float *ws_dcy,
                                                 const float *ws_eg, const uint16_t *ws_w,
@@ -498,25 +521,26 @@ __device__ __forceinline__ void load_chunk_frag(ChunkFrag &f, int c, int h, cons
   const int q4 = 4 * (lane >> 4);
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
   // w: [mb][kk][lane][hi 8 | lo 8] fragments of this wave's 16 rows
-  const uint16_t *wf = ws_w + ch_head * (kChunk * kDK * 2) + (wave * 4) * (64 * 16);
+  const auto rw = buf_rsrc(ws_w + ch_head * (kWBytes / 2), kWBytes);
+  const uint32_t wo = static_cast<uint32_t>(wave) * 8192u + static_cast<uint32_t>(lane) * 32u;
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
-    f.wh[kk] = *reinterpret_cast<const u32x4 *>(wf + (kk * 64 + lane) * 16);
-    f.wl[kk] = *reinterpret_cast<const u32x4 *>(wf + (kk * 64 + lane) * 16 + 8);
+    f.wh[kk] = buf_load16(rw, wo + kk * 2048);
+    f.wl[kk] = buf_load16(rw, wo + kk * 2048 + 16);
   }
   // K^T: [mt][kk][lane][8] fragments of this wave's two 16-row tiles
-  const uint16_t *kt = ws_kt + (static_cast<size_t>(c) * H.qk + h / H.ratio) * (kDK * kChunk);
+  const auto rk = buf_rsrc(ws_kt + (static_cast<size_t>(c) * H.qk + h / H.ratio) * (kKtBytes / 2), kKtBytes);
+  const uint32_t ko = static_cast<uint32_t>(wave) * 4096u + static_cast<uint32_t>(lane) * 16u;
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-      f.ka[mi][kk] = *reinterpret_cast<const u32x4 *>(
-          kt + ((((2 * wave + mi) * 2 + kk) * 64) + lane) * 8);
+    for (int kk = 0; kk < 2; ++kk) f.ka[mi][kk] = buf_load16(rk, ko + mi * 2048 + kk * 1024);
   // u: [row tile][col tile][lane][4] result tiles
-  const float *ut = ws_u + ch_head * (kChunk * kDV);
-  f.u = *reinterpret_cast<const f32x4 *>(ut + ((wave * 8 + (vw >> 4)) * 64 + lane) * 4);
-  f.dcy = *reinterpret_cast<const f32x4 *>(ws_dcy + ch_head * kChunk + 16 * wave + q4);
-  f.eg = ws_eg[ch_head];
+  const auto ru = buf_rsrc(ws_u + ch_head * (kUBytes / 4), kUBytes);
+  f.u = __builtin_bit_cast(f32x4, buf_load16(ru, static_cast<uint32_t>((wave * 8 + (vw >> 4)) * 64 + lane) * 16u));
+  const auto rd = buf_rsrc(ws_dcy + ch_head * kChunk, kChunk * 4);
+  f.dcy = __builtin_bit_cast(f32x4, buf_load16(rd, static_cast<uint32_t>(16 * wave + q4) * 4u));
+  f.eg = buf_load_f32(ws_eg + ch_head);
 }
 
 template <int BV>
@@ -529,7 +553,10 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
   const int rest = blockIdx.x / H.v;
   const int vb = rest % NVB, s = rest / NVB;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = (tid >> 6) & 3, ct = tid >> 8;  // row group, column tile
+  // wave-uniform in SGPRs, so every workspace address is a scalar base plus a
+  // loop-invariant 32-bit lane offset
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);
+  const int ct = __builtin_amdgcn_readfirstlane(tid >> 8);  // row group, column tile
   const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
   const int lc = 16 * ct;                          // column tile offset in the block
   const int vw = vb * BV + lc;                     // first state column of this wave
@@ -633,14 +660,14 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
   };
 
   // Ring of three fragment sets: chunk i uses set i % 3 while the sets of
-  // chunks i + 1 and i + 2 are in flight (the loop header sits where all three
-  // sets are pending, on entry and on the back edge alike).  (A fourth set
-  // measured slower: the extra registers push accumulators into AGPRs.)  Prefetches past the last chunk
-  // re-read the last chunk, so every iteration issues the same loads and the
-  // compiler can wait for exactly the set in use (a conditional load would
-  // make it wait for all outstanding loads).  The workspace pointers carry no
-  // __restrict__ on purpose: that keeps the compiler from sinking these loads
-  // to their first use.
+  // chunks i + 1 and i + 2 are in flight.  The loop body is three straight
+  // steps with one exit test, at the back edge, so the loop head is reached
+  // with the same loads pending from both of its predecessors and the
+  // compiler waits for exactly the set in use (an exit after each step made it
+  // merge those paths and wait for nearly every prefetch).  The last 0-2
+  // chunks run after the loop.  Prefetches past the last chunk re-read it,
+  // so every iteration issues the same loads.  (A fourth set measured slower:
+  // the extra registers push accumulators into AGPRs.)
   if (nch > 0) {
     auto chunk_at = [&](int i) { return c0 + (i < nch ? i : nch - 1); };
     ChunkFrag fa, fb, fc;
@@ -649,17 +676,17 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
     GDN_LOAD(fa, 0);
     GDN_LOAD(fb, 1);
     GDN_LOAD(fc, 2);
-    for (int ci = 0;; ci += 3) {
+    int ci = 0;
+    for (; ci + 3 <= nch; ci += 3) {
       step(fa, c0 + ci);
-      if (ci + 1 >= nch) break;
       GDN_LOAD(fa, ci + 3);
       step(fb, c0 + ci + 1);
-      if (ci + 2 >= nch) break;
       GDN_LOAD(fb, ci + 4);
       step(fc, c0 + ci + 2);
-      if (ci + 3 >= nch) break;
       GDN_LOAD(fc, ci + 5);
     }
+    if (ci < nch) step(fa, c0 + ci);
+    if (ci + 1 < nch) step(fb, c0 + ci + 1);
 #undef GDN_LOAD
   }
 
