@@ -17,25 +17,37 @@
 //
 //   1. index  : one workgroup turns cu_seqlens (on the device, never copied
 //               to the host) into the chunk table and per-sequence chunk
-//               offsets.  A zero-length sequence gets no chunk (the
-//               reference's seq-id rule, fla_kernels.py:63, would misnumber
-//               every later sequence).
+//               offsets, and picks the per-chunk form below.  A zero-length
+//               sequence gets no chunk (the reference's seq-id rule,
+//               fla_kernels.py:63, would misnumber every later sequence).
 //   2. intra  : per (chunk, v-head): gating, cumsum, K K^T on MFMA, the
-//               64x64 triangular inverse in LDS (four 16x16 diagonal blocks
-//               by forward substitution, then the off-diagonal blocks by
-//               distance), u and w on MFMA.  No GVA copies: v-head h reads
-//               q/k head h/2 directly.
-//   3. state  : per (sequence, v-head, 16- or 32-column V block): the serial
+//               64x64 triangular inverse in LDS.  No GVA copies: v-head h
+//               reads q/k head h/2 directly.
+//   3. state  : per (sequence, v-head, 16 columns of V): the serial
 //               recurrence over chunks with the f32 state in MFMA
 //               accumulators; stores the chunk-start state and v_new.
 //   4. output : per (chunk, v-head): o from Q S, the masked Q K^T and v_new.
+//
+// Two forms of the state-independent per-chunk operands, chosen per batch:
+//   WY form: the intra kernel forms w and u (and K^T fragments); a state step
+//            is v_new = u - w S, then the update: two LDS exchanges.  The
+//            shortest serial chain -- best when one sequence's chain bounds
+//            the call (one sequence, or one much longer than the rest).
+//   T form:  the intra kernel stores only T = (I + A)^-1; a state step forms
+//            the right-hand side from the inputs, v_new = T (beta V - beta
+//            e^G K S): a third exchange per step, but a quarter of the
+//            intra kernel's HBM traffic and fewer bytes per step -- best
+//            when many sequences keep every CU and the memory system busy.
+// Rule (index kernel, from sweeps of both on MI355X): the T form when the
+// batch has at least 128 chunks and at least three times the chunks of its
+// longest sequence.  One sequence always takes the WY form.
 //
 // Precision.  The state recurrence must hold 1e-3 of max|S| after 128-512
 // chunks.  Rounding any operand of w S or K^T v_new (or u, w themselves) to
 // one bf16 leaves ~2-4e-3 of max|S|, so those products use split bf16: an f32
 // operand x is carried as hi + lo (both bf16, x = hi + lo to ~2^-17) and a
 // product of two such operands as hi*hi + hi*lo + lo*hi (three MFMAs), or two
-// when the other operand is exact in bf16 (K).  u, w, T and the state stay
+// when the other operand is exact in bf16 (K, V).  u, w, T and the state stay
 // f32.  The output path (Q S, Q K^T, P v_new) uses single bf16 operands: its
 // error stays ~2^-9 relative, far inside the bf16 output tolerance.
 #include "gdn_device.h"
@@ -47,9 +59,12 @@ namespace gdn {
 constexpr int kStrideK = 136;  // bf16 [64][128] tiles
 constexpr int kStrideT = 72;   // bf16 [*][64]   tiles
 
+constexpr int kTElems = kChunk * kChunk * 2;  // T of one (chunk, head): hi + lo bf16
+
 // Workspace layout; every region starts on a 256-byte boundary.
 struct PrefillLayout {
   int nt_max;  // upper bound on the chunk count from (T, N) alone
+  // The T form keeps T in the w region and (beta, beta e^G) in the u region.
   size_t chunks, offsets, G, dcy, eg, w, u, kt, ht, vnt, total;
 };
 
@@ -71,7 +86,7 @@ static PrefillLayout prefill_layout(int T, int N, const Heads &H) {
   };
   const size_t n = static_cast<size_t>(nt);
   L.chunks = take(n * sizeof(int4));
-  L.offsets = take((static_cast<size_t>(N) + 2) * sizeof(int));  // + the path flag
+  L.offsets = take((static_cast<size_t>(N) + 3) * sizeof(int));  // + path and form flags
   const size_t hv = static_cast<size_t>(H.v), hqk = static_cast<size_t>(H.qk);
   L.G = take(n * hv * kChunk * 4);
   L.dcy = take(n * hv * kChunk * 4);
@@ -92,6 +107,10 @@ static PrefillLayout prefill_layout(int T, int N, const Heads &H) {
 // clamped to [0, T] and the chunk count to nt_max, so a malformed cu_seqlens
 // cannot send any later kernel out of bounds.
 //
+// Form choice: offsets[N + 2] = form (0 WY, 1 T) -- `form` when it is 0 or 1,
+// else the rule in the file header from the chunk count and the longest
+// sequence.
+//
 // Path choice (choose != 0): the token-sequential kernel takes the whole batch
 // when choose == 1 and no sequence is longer than rec_max tokens, or when
 // choose == 2 and the cost model below favours it.  Then every sequence gets
@@ -101,13 +120,25 @@ static PrefillLayout prefill_layout(int T, int N, const Heads &H) {
 // chunked
 //   20 + 1.05 * ceil(longest / 64) + 1.05 * N  (fixed launches, serial chunks, per-sequence work)
 // ---------------------------------------------------------------------------
+// Maximum of x over the workgroup into *dst (LDS, initially <= every x): a
+// butterfly within each wave, then one LDS atomic per wave (1024 atomics on
+// one word serialize: ~2 us).
+__device__ __forceinline__ void block_max_into(int x, int *dst) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const int y = __shfl_xor(x, off);
+    x = y > x ? y : x;
+  }
+  if ((threadIdx.x & 63) == 0) atomicMax(dst, x);
+}
+
 __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int cu64, int N, int T,
                                                               int nt_max, int choose, int rec_max,
-                                                              int4 *chunks, int *offsets) {
+                                                              int form, int4 *chunks, int *offsets) {
   __shared__ int s_incl[1024];
-  __shared__ int s_longest;
+  __shared__ int s_longest, s_most_chunks;
   const int tid = threadIdx.x;
-  if (tid == 0) s_longest = 0;
+  if (tid == 0) s_longest = s_most_chunks = 0;
   __syncthreads();
   if (choose != 0) {
     int longest = 0;
@@ -115,7 +146,7 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
       const int len = load_cu(cu, cu64, s + 1, T) - load_cu(cu, cu64, s, T);
       longest = len > longest ? len : longest;
     }
-    atomicMax(&s_longest, longest);
+    block_max_into(longest, &s_longest);
   }
   __syncthreads();
   bool sequential = false;
@@ -129,6 +160,7 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
   }
   if (tid == 0) offsets[N + 1] = sequential ? 1 : 0;
   long long carry = 0;
+  int most_chunks = 0;
   for (int base = 0; base < N; base += 1024) {
     const int s = base + tid;
     int n = 0;
@@ -138,6 +170,7 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
       eos = eos < bos ? bos : eos;
       n = (eos - bos + kChunk - 1) / kChunk;
     }
+    most_chunks = n > most_chunks ? n : most_chunks;
     s_incl[tid] = n;
     __syncthreads();
     for (int off = 1; off < 1024; off <<= 1) {
@@ -172,8 +205,13 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
     carry += tile_total;
     __syncthreads();
   }
+  block_max_into(most_chunks, &s_most_chunks);
+  __syncthreads();
   const int nt = static_cast<int>(carry < nt_max ? carry : nt_max);
-  if (tid == 0) offsets[N] = nt;
+  if (tid == 0) {
+    offsets[N] = nt;
+    offsets[N + 2] = (form == 0 || form == 1) ? form : (nt >= 128 && nt >= 3 * s_most_chunks ? 1 : 0);
+  }
   for (int c = nt + tid; c < nt_max; c += 1024) chunks[c] = make_int4(-1, 0, 0, 0);
 }
 
@@ -188,6 +226,19 @@ __device__ __forceinline__ int4 chunk_info(const int4 *chunks, int c, int single
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// gfx950 ds_read_b64_tr_b16: within each group of 16 lanes, source lane s
+// reads the four 16-bit values D[s][0..3] at its own LDS address and lane t
+// receives D[4j + (t >> 2)][t & 3], j = 0..3 (pinned by an on-device probe
+// of the instruction).  So with lane s of group g addressing row
+// 8g + 4h + (s >> 2), column c0 + 4 (s & 3) of a row-major tile, lane t
+// gets the tile's column c0 + t at rows 8g + 4h .. 8g + 4h + 3: half h of
+// a transposed MFMA operand fragment.
+__device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t *p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                       (lds_s16x4 *)(const_cast<uint16_t *>(p))));
+}
 
 // v_mfma_f32_16x16x16_bf16: A lane l holds A[l & 15][4*(l >> 4) + e], B lane l
 // holds B[4*(l >> 4) + e][l & 15] (e = 0..3), D as for the 16x16x32 form.  D's
@@ -224,8 +275,7 @@ __device__ __forceinline__ int tsw(int row, int token) {
   return row * kStrideTT + ((((token >> 3) ^ (row >> 3)) & 7) << 3) + (token & 7);
 }
 
-// ---------------------------------------------------------------------------
-// 2. intra-chunk: per (chunk c = blockIdx.x, v-head h = blockIdx.y).
+// WY form of the intra kernel (per chunk c, v-head h; LDS from smem, 52 KB):
 //   * wave 0: gating, chunk-local cumsum G, decay factors.
 //   * every thread: one 8x8 block of K or V -> row-major K and transposed
 //     K^T / V^T in LDS (8x8 transposes in registers, 16-byte LDS writes).
@@ -240,18 +290,13 @@ __device__ __forceinline__ int tsw(int row, int token) {
 // Outputs go to the workspace in the exact fragment order the state kernel
 // reads: u as MFMA result tiles, w as hi/lo A-operand fragments, K^T as
 // A-operand fragments.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void prefill_intra_kernel(
-    const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
-    const float *__restrict__ A_log, const uint16_t *__restrict__ a,
-    const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
-    const int4 *__restrict__ chunks, int single_T, Heads H, float *__restrict__ ws_G,
-    float *__restrict__ ws_dcy, float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w,
-    float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
-  const int c = blockIdx.x, h = blockIdx.y;
-  const int4 ch = chunk_info(chunks, c, single_T);
-  if (ch.x < 0) return;
-  const int start = ch.y, len = ch.z;
+constexpr int kIntraWyLds = kChunk * kStrideK * 2 + kDK * kStrideTT * 2 + kChunk * 68 * 4 + 3 * kChunk * 4;
+__device__ __forceinline__ void wy_intra(
+    char *smem, int c, int h, int start, int len, const uint16_t *__restrict__ k,
+    const uint16_t *__restrict__ v, const float *__restrict__ A_log, const uint16_t *__restrict__ a,
+    const float *__restrict__ dt_bias, const uint16_t *__restrict__ b, const Heads &H,
+    float *__restrict__ ws_G, float *__restrict__ ws_dcy, float *__restrict__ ws_eg,
+    uint16_t *__restrict__ ws_w, float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4, kg = g * 8;
   const int hq = h / H.ratio;
@@ -263,10 +308,10 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
   //   sA:  strictly lower blocks of A; the unused upper blocks hold the four
   //        16x16 diagonal inverses (D_w at block kDiagBlock[w]); at the end
   //        (wave 3) w scratch.
-  __shared__ __align__(16) uint16_t sKV[kChunk * kStrideK];
-  __shared__ __align__(16) uint16_t sKt[kDK * kStrideTT];
-  __shared__ __align__(16) float sA[kChunk * kStrideA4];
-  __shared__ __align__(16) float sBeta[kChunk], sBG[kChunk], sG[kChunk];
+  uint16_t *const sKV = reinterpret_cast<uint16_t *>(smem);                  // [64][136]
+  uint16_t *const sKt = sKV + kChunk * kStrideK;                              // [128][64]
+  float *const sA = reinterpret_cast<float *>(sKt + kDK * kStrideTT);         // [64][68]
+  float *const sBeta = sA + kChunk * kStrideA4, *const sBG = sBeta + kChunk, *const sG = sBG + kChunk;
   uint16_t *const sK = sKV, *const sVt = sKV;
   static_assert(kDV * kStrideTT <= kChunk * kStrideK, "V^T must fit in the K tile");
   // D_w lives at row block w, column block dcol(w): (0,1), (1,2), (2,3), (0,2).
@@ -468,35 +513,231 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// 3. state recurrence: per (sequence s, v-head h, V block of BV columns).
-// blockIdx.x = h + 8 * (vb + NVB * s): every workgroup of one head lands on
-// the same XCD (workgroups are dealt round-robin over the 8 XCDs), so the
-// per-head w and K^T stream through one L2.
-// The state tile S[:, v0:v0+BV] ([K=128] x [BV], f32) lives in MFMA
-// accumulators.  The workgroup has 4 waves per 16-column tile: wave w owns
-// column tile w / 4 and, in it, K-rows 32*(w % 4)..+31 (two 16-row tiles) of
-// the state and v_new rows 16*(w % 4)..+15.  Teams of different column tiles
-// only share the barriers, so with BV = 32 two independent chains share each
-// SIMD and hide each other's latency.  Everything a chunk needs that does not depend on the
-// state (w, K^T, u, decay factors) is register-prefetched two chunks ahead,
-// so the serial chain per chunk is two LDS exchanges, two barriers and the
-// MFMAs.  Addresses are a per-chunk scalar base plus a 32-bit lane offset.
-// ---------------------------------------------------------------------------
-struct ChunkFrag {
-  u32x4 wh[4], wl[4];  // w rows 16*wave + (lane & 15), k-steps 0..3 (hi / lo)
-  u32x4 ka[2][2];      // K^T rows 16*(2*wave + mi) + (lane & 15), k-steps 0..1
-  f32x4 u;             // u[16*rw + 4*(lane >> 4) + r][vw + (lane & 15)]
-  f32x4 dcy;           // exp(G_last - G_i) of the lane's four v_new rows
-  float eg;            // exp(G_last)
-};
 
+// T form of the intra kernel (per chunk c, v-head h; LDS from smem, 35 KB):
+//   * wave 0: gating, chunk-local cumsum G, the per-token vectors.
+//   * A = strictly-lower(beta_i exp(G_i - G_j) K K^T) on MFMA (K exact bf16).
+//   * T = (I + A)^-1: the four 16x16 diagonal blocks D_i by forward
+//     substitution (wave i), then wave j walks block column j,
+//       T_jj = D_j,   T_ij = -D_i sum_{j<=m<i} A_im T_mj   (i > j),
+//     on split-bf16 16x16x16 MFMAs (a result tile's layout is the next
+//     product's B-operand layout, so the column stays in registers).
+// T goes to the workspace (w region) as split A-operand fragments of the
+// state kernel, which applies it to the state-dependent right-hand side
+// itself; (beta, beta e^G) go to the u region.
+constexpr int kIntraTLds = kChunk * kStrideK * 2 + kChunk * 68 * 4 + 2 * kChunk * 4;
+__device__ __forceinline__ void t_intra(
+    char *smem, int c, int h, int start, int len, const uint16_t *__restrict__ k,
+    const float *__restrict__ A_log, const uint16_t *__restrict__ a,
+    const float *__restrict__ dt_bias, const uint16_t *__restrict__ b, const Heads &H,
+    float *__restrict__ ws_G, float *__restrict__ ws_dcy, float *__restrict__ ws_eg,
+    uint16_t *__restrict__ ws_w, float *__restrict__ ws_u) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4, kg = g * 8;
+  const int hq = h / H.ratio;
+  const size_t ch_head = static_cast<size_t>(c) * H.v + h;
+
+  constexpr int kStrideA4 = 68;  // f32 stride of the 64x64 tiles (16-byte rows)
+  //   sK: K row-major until A is built, then T (f32 [64][68]) for the
+  //       fragment transposition.
+  //   sA: strictly lower blocks of A; the unused upper blocks hold the four
+  //       16x16 diagonal inverses (D_w at block (drow(w), dcol(w))).
+  uint16_t *const sK = reinterpret_cast<uint16_t *>(smem);                   // [64][136]
+  float *const sA = reinterpret_cast<float *>(sK + kChunk * kStrideK);        // [64][68]
+  float *const sBeta = sA + kChunk * kStrideA4, *const sG = sBeta + kChunk;
+  static_assert(kChunk * kStrideA4 * 4 <= kChunk * kStrideK * 2, "T must fit in the K tile");
+  float *const sT = reinterpret_cast<float *>(sK);
+  // D_w lives at row block w, column block dcol(w): (0,1), (1,2), (2,3), (0,2).
+  auto dcol = [](int w) { return w == 3 ? 2 : w + 1; };
+  auto drow = [](int w) { return w == 3 ? 0 : w; };
+
+  // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding tokens
+  // get g = 0 and beta = 0, so G stays at G_last past the end of the chunk.
+  if (wave == 0) {
+    float gl = 0.f, be = 0.f;
+    if (lane < len) {
+      const size_t t = static_cast<size_t>(start) + lane;
+      gl = gdn_log_decay(A_log[h], bf16_to_f32(a[t * H.v + h]), dt_bias[h]);
+      be = sigmoidf_(bf16_to_f32(b[t * H.v + h]));
+    }
+    float G = gl;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(G, off);
+      if (lane >= off) G += y;
+    }
+    sG[lane] = G;
+    sBeta[lane] = be;
+    const float G_last = __shfl(G, 63);
+    ws_G[ch_head * kChunk + lane] = G;
+    ws_dcy[ch_head * kChunk + lane] = expf(G_last - G);
+    float *bb = ws_u + ch_head * (kChunk * kDV);  // (beta, beta e^G) in the u region
+    bb[lane] = be;
+    bb[kChunk + lane] = be * expf(G);
+    if (lane == 0) ws_eg[ch_head] = expf(G_last);
+  }
+
+  // K row-major into LDS (rows past the chunk are zero).
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + 256 * i, row = idx >> 4, c8 = (idx & 15) * 8;
+    u32x4 kv = {0u, 0u, 0u, 0u};
+    if (row < len)
+      kv = *reinterpret_cast<const u32x4 *>(k + ((static_cast<size_t>(start) + row) * H.qk + hq) * kDK + c8);
+    *reinterpret_cast<u32x4 *>(&sK[row * kStrideK + c8]) = kv;
+  }
+  __syncthreads();
+
+  // A = strictly-lower(beta_i exp(G_i - G_j) K K^T); wave w owns rows 16w..16w+15.
+  {
+    const int mb = wave;
+    for (int nb = 0; nb <= mb; ++nb) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const u32x4 af = *reinterpret_cast<const u32x4 *>(&sK[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
+        const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[(16 * nb + r16) * kStrideK + 32 * kk + kg]);
+        acc = mfma_bf16(af, bf, acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * mb + 4 * g + r, j = 16 * nb + r16;
+        sA[i * kStrideA4 + j] = (i > j && i < len) ? sBeta[i] * expf(sG[i] - sG[j]) * acc[r] : 0.f;
+      }
+    }
+  }
+  __syncthreads();
+
+  // Diagonal blocks D_w = (I + A_ww)^-1: wave w, lane j < 16 solves column j.
+  if (lane < 16) {
+    const int base = 16 * wave;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float *arow = &sA[(base + i) * kStrideA4 + base];
+      float s0 = (i == lane) ? 1.f : 0.f, s1 = 0.f;
+#pragma unroll
+      for (int m = 0; m < i; m += 2) {
+        s0 -= arow[m] * x[m];
+        if (m + 1 < i) s1 -= arow[m + 1] * x[m + 1];
+      }
+      x[i] = s0 + s1;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      sA[(16 * drow(wave) + i) * kStrideA4 + 16 * dcol(wave) + lane] = x[i];
+  }
+  __syncthreads();
+
+  // Block column j = wave of T.  Tiles in MFMA result order: lane holds
+  // T_ij[4g + r][r16]; their hi/lo splits are the B operands of the next
+  // products.
+  f32x4 Tc[4];
+  {
+    const int j = wave;
+    u32x2 Th[4], Tl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i < j) {  // above the diagonal
+        Tc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        Th[i] = Tl[i] = u32x2{0u, 0u};
+      } else if (i == j) {  // T_jj = D_j
+        const float *d = &sA[(16 * drow(i) + 4 * g) * kStrideA4 + 16 * dcol(i) + r16];
+        Tc[i] = f32x4{d[0], d[kStrideA4], d[2 * kStrideA4], d[3 * kStrideA4]};
+        split4(Tc[i], Th[i], Tl[i]);
+      } else {
+        // Z = -sum_{j<=m<i} A_im T_mj, then T_ij = D_i Z
+        f32x4 Z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < i; ++m) {
+          if (m < j) continue;
+          const f32x4 la = *reinterpret_cast<const f32x4 *>(&sA[(16 * i + r16) * kStrideA4 + 16 * m + 4 * g]);
+          u32x2 lh, ll;
+          split4(-la, lh, ll);
+          Z = mfma16_x3(lh, ll, Th[m], Tl[m], Z);
+        }
+        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(
+            &sA[(16 * drow(i) + r16) * kStrideA4 + 16 * dcol(i) + 4 * g]);
+        u32x2 dh, dl, zh, zl;
+        split4(d4, dh, dl);
+        split4(Z, zh, zl);
+        Tc[i] = mfma16_x3(dh, dl, zh, zl, f32x4{0.f, 0.f, 0.f, 0.f});
+        split4(Tc[i], Th[i], Tl[i]);
+      }
+    }
+  }
+  // sK (K) is dead since A was built: T (f32) goes there, upper blocks zero.
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      sT[(16 * i + 4 * g + r) * kStrideA4 + 16 * wave + r16] = Tc[i][r];
+  __syncthreads();
+
+  // T as A-operand fragments of the state kernel (row 16*rt + r16, 8
+  // consecutive k), split hi/lo: [chunk][head][rt][kk][lane][hi 8 | lo 8].
+  uint16_t *tf = ws_w + ch_head * (kChunk * kDK * 2);  // T in the w region
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const f32x4 x0 = *reinterpret_cast<const f32x4 *>(&sT[(16 * wave + r16) * kStrideA4 + 32 * kk + kg]);
+    const f32x4 x1 = *reinterpret_cast<const f32x4 *>(&sT[(16 * wave + r16) * kStrideA4 + 32 * kk + kg + 4]);
+    const float x8[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+    u32x4 hi, lo;
+    split8(x8, hi, lo);
+    uint16_t *dst = tf + ((wave * 2 + kk) * 64 + lane) * 16;
+    *reinterpret_cast<u32x4 *>(dst) = hi;
+    *reinterpret_cast<u32x4 *>(dst + 8) = lo;
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// 2. intra-chunk: per (chunk c = blockIdx.x, v-head h = blockIdx.y), one
+// kernel per form, each with its own LDS size (the T form's 35 KB lets four
+// workgroups share a CU, the WY form's 52 KB three).  When the form is left
+// to the device (form_flag != nullptr) both are launched and each returns at
+// once unless *form_flag names its form.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prefill_intra_wy_kernel(
+    const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+    const float *__restrict__ A_log, const uint16_t *__restrict__ a,
+    const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
+    const int4 *__restrict__ chunks, int single_T, Heads H, const int *__restrict__ form_flag,
+    float *__restrict__ ws_G, float *__restrict__ ws_dcy, float *__restrict__ ws_eg,
+    uint16_t *__restrict__ ws_w, float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
+  __shared__ __align__(16) char smem[kIntraWyLds];
+  if (form_flag != nullptr && *form_flag != 0) return;
+  const int c = blockIdx.x, h = blockIdx.y;
+  const int4 ch = chunk_info(chunks, c, single_T);
+  if (ch.x < 0) return;
+  wy_intra(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u,
+           ws_kt);
+}
+
+__global__ __launch_bounds__(256) void prefill_intra_t_kernel(
+    const uint16_t *__restrict__ k, const float *__restrict__ A_log,
+    const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
+    const uint16_t *__restrict__ b, const int4 *__restrict__ chunks, int single_T, Heads H,
+    const int *__restrict__ form_flag, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
+    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u) {
+  __shared__ __align__(16) char smem[kIntraTLds];
+  if (form_flag != nullptr && *form_flag != 1) return;
+  const int c = blockIdx.x, h = blockIdx.y;
+  const int4 ch = chunk_info(chunks, c, single_T);
+  if (ch.x < 0) return;
+  t_intra(smem, c, h, ch.y, ch.z, k, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u);
+}
+
+// ---------------------------------------------------------------------------
+// 3. state recurrence: the two forms of a step, then the kernel.
+// ---------------------------------------------------------------------------
 // Buffer descriptor (gfx9 word 3 = 0x00020000: raw 32-bit records) over
 // `bytes` bytes at a wave-uniform base.  Loads through it take the base in
 // SGPRs and a 32-bit per-lane byte offset that never changes across chunks,
 // so a prefetch loop needs no address registers: with 64-bit VGPR addresses
 // the compiler recomputed them every chunk and, reusing registers of loads
 // still in flight, had to wait for the newest prefetch set at the loop head.
+// A load at or past `bytes` returns zero: the rows past the end of a chunk.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), bytes,
                                            0x00020000);
@@ -514,7 +755,15 @@ constexpr uint32_t kWBytes = kChunk * kDK * 4;    // w of one (chunk, head): hi 
 constexpr uint32_t kKtBytes = kDK * kChunk * 2;   // K^T of one (chunk, q/k head)
 constexpr uint32_t kUBytes = kChunk * kDV * 4;    // u of one (chunk, head), f32
 
-__device__ __forceinline__ void load_chunk_frag(ChunkFrag &f, int c, int h, const Heads &H,
+struct WyFrag {
+  u32x4 wh[4], wl[4];  // w rows 16*wave + (lane & 15), k-steps 0..3 (hi / lo)
+  u32x4 ka[2][2];      // K^T rows 16*(2*wave + mi) + (lane & 15), k-steps 0..1
+  f32x4 u;             // u[16*rw + 4*(lane >> 4) + r][vw + (lane & 15)]
+  f32x4 dcy;           // exp(G_last - G_i) of the lane's four v_new rows
+  float eg;            // exp(G_last)
+};
+
+__device__ __forceinline__ void load_wy_frag(WyFrag &f, int c, int h, const Heads &H,
                                                 int vw, int wave, int lane, const float *ws_dcy,
                                                 const float *ws_eg, const uint16_t *ws_w,
                                                 const float *ws_u, const uint16_t *ws_kt) {
@@ -543,36 +792,25 @@ __device__ __forceinline__ void load_chunk_frag(ChunkFrag &f, int c, int h, cons
   f.eg = buf_load_f32(ws_eg + ch_head);
 }
 
-template <int BV>
-__global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
-    const float *state, float *new_state, const int *offsets, const float *ws_dcy,
-    const float *ws_eg, const uint16_t *ws_w, const float *ws_u,
-    const uint16_t *ws_kt, uint16_t *ws_ht, uint16_t *ws_vnt, int N, int single_T, Heads H) {
-  constexpr int NVB = kDV / BV;
-  const int h = blockIdx.x % H.v;
-  const int rest = blockIdx.x / H.v;
-  const int vb = rest % NVB, s = rest / NVB;
-  const int tid = threadIdx.x, lane = tid & 63;
-  // wave-uniform in SGPRs, so every workspace address is a scalar base plus a
-  // loop-invariant 32-bit lane offset
-  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);
-  const int ct = __builtin_amdgcn_readfirstlane(tid >> 8);  // row group, column tile
+// WY form of a state step (see the kernel comment): wave w owns K-rows
+// 32w..32w+31 of the state tile and v_new rows (tokens) 16w..16w+15.
+// Everything a chunk needs that does not depend on the state (w, K^T, u,
+// decay factors) is prefetched into registers two chunks ahead, so the
+// serial chain per chunk is two LDS exchanges, two barriers and the MFMAs.
+constexpr int kStateWyLds = 2 * 16 * kStrideK * 2 + 2 * 16 * kStrideT * 2;
+__device__ __forceinline__ void wy_state(
+    char *smem, int c0, int nch, int h, int v0, int wave, int lane, size_t sbase,
+    const float *state, float *new_state, const float *ws_dcy, const float *ws_eg,
+    const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt, uint16_t *ws_ht,
+    uint16_t *ws_vnt, const Heads &H) {
+  const int ct = 0;  // one 16-column tile per workgroup
   const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
-  const int lc = 16 * ct;                          // column tile offset in the block
-  const int vw = vb * BV + lc;                     // first state column of this wave
-
-  __shared__ __align__(16) uint16_t sSh[BV * kStrideK];
-  __shared__ __align__(16) uint16_t sSl[BV * kStrideK];
-  __shared__ __align__(16) uint16_t sVh[BV * kStrideT];
-  __shared__ __align__(16) uint16_t sVl[BV * kStrideT];
-
-  int c0 = 0, nch = (single_T + kChunk - 1) / kChunk;  // one sequence: no table
-  if (single_T < 0) {
-    if (offsets[N + 1]) return;  // the token-sequential kernel owns the batch
-    c0 = offsets[s];
-    nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
-  }
-  const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;  // [V][K]
+  const int lc = 16 * ct;
+  const int vw = v0 + lc;
+  uint16_t *const sSh = reinterpret_cast<uint16_t *>(smem);
+  uint16_t *const sSl = sSh + 16 * kStrideK;
+  uint16_t *const sVh = sSl + 16 * kStrideK;
+  uint16_t *const sVl = sVh + 16 * kStrideT;
 
   f32x4 S[2];
 #pragma unroll
@@ -585,7 +823,7 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
   }
 
   // One chunk of the recurrence, from the prefetched fragments f.
-  auto step = [&](const ChunkFrag &f, int c) {
+  auto step = [&](const WyFrag &f, int c) {
     const size_t ch_head = static_cast<size_t>(c) * H.v + h;
     uint16_t *ht = ws_ht + ch_head * (kDV * kDK);
     uint16_t *vnt = ws_vnt + ch_head * (kDV * kChunk);
@@ -670,9 +908,9 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
   // the extra registers push accumulators into AGPRs.)
   if (nch > 0) {
     auto chunk_at = [&](int i) { return c0 + (i < nch ? i : nch - 1); };
-    ChunkFrag fa, fb, fc;
+    WyFrag fa, fb, fc;
 #define GDN_LOAD(F, I) \
-    load_chunk_frag(F, chunk_at(I), h, H, vw, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt)
+    load_wy_frag(F, chunk_at(I), h, H, vw, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt)
     GDN_LOAD(fa, 0);
     GDN_LOAD(fb, 1);
     GDN_LOAD(fc, 2);
@@ -696,6 +934,300 @@ __global__ __launch_bounds__(256 * (BV / 16)) void prefill_state_kernel(
     const int kr = 16 * (2 * wave + mi) + q4, vc = vw + r16;
     *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + kr) = S[mi];
   }
+}
+
+
+struct TFrag {
+  u32x4 kf[4];          // K rows 16*wave + (lane & 15), k-steps 0..3 (A operand of K S)
+  u32x4 th[2], tl[2];   // T rows 16*wave + (lane & 15), k-steps 0..1 (hi / lo)
+  f32x4 beta, bg, dcy;  // beta, beta e^G, exp(G_last - G) of rows 16*wave + 4*(lane >> 4) + r
+  uint32_t vv[4];       // bf16 bits of V[16*wave + 4*(lane >> 4) + r][v0 + (lane & 15)]
+                        // (widened where used: converting at the load let the
+                        // compiler hoist it, and its wait, into the step before)
+  float eg;             // exp(G_last)
+};
+
+// Per-lane byte offsets of the fragment loads: fixed for the whole kernel.
+struct FragOffsets {
+  uint32_t k, t, v, vec;
+};
+
+// Fragments of chunk c (tokens [start, start + len)) for v-head h.
+__device__ __forceinline__ void load_t_frag(TFrag &f, int c, int start, int len, int h,
+                                                const Heads &H, const FragOffsets &o,
+                                                const uint16_t *k, const uint16_t *v,
+                                                const float *ws_dcy, const float *ws_eg,
+                                                const uint16_t *ws_w, const float *ws_u) {
+  const size_t ch_head = static_cast<size_t>(c) * H.v + h;
+  const uint32_t nlen = static_cast<uint32_t>(len);
+  const auto rk = buf_rsrc(k + (static_cast<size_t>(start) * H.qk + h / H.ratio) * kDK,
+                           nlen * static_cast<uint32_t>(H.qk) * (kDK * 2));
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) f.kf[kk] = buf_load16(rk, o.k + kk * 64);
+  const auto rt = buf_rsrc(ws_w + ch_head * (kChunk * kDK * 2), kTElems * 2);  // T, w region
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    f.th[kk] = buf_load16(rt, o.t + kk * 2048);
+    f.tl[kk] = buf_load16(rt, o.t + kk * 2048 + 16);
+  }
+  const auto rv = buf_rsrc(v + (static_cast<size_t>(start) * H.v + h) * kDV,
+                           nlen * static_cast<uint32_t>(H.v) * (kDV * 2));
+  const uint32_t vrow = static_cast<uint32_t>(H.v) * (kDV * 2);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) f.vv[r] = __builtin_amdgcn_raw_buffer_load_b16(rv, o.v + r * vrow, 0, 0);
+  const auto rb = buf_rsrc(ws_u + ch_head * (kChunk * kDV), 2 * kChunk * 4);  // (beta, beta e^G)
+  f.beta = __builtin_bit_cast(f32x4, buf_load16(rb, o.vec));
+  f.bg = __builtin_bit_cast(f32x4, buf_load16(rb, o.vec + kChunk * 4));
+  const auto rd = buf_rsrc(ws_dcy + ch_head * kChunk, kChunk * 4);
+  f.dcy = __builtin_bit_cast(f32x4, buf_load16(rd, o.vec));
+  f.eg = buf_load_f32(ws_eg + ch_head);
+}
+
+// T form of a state step (see the kernel comment): wave w owns K-rows
+// 32w..32w+31 of the state tile and tokens 16w..16w+15 of the per-chunk
+// products.  Per chunk:
+//   X     = K S                              (K exact bf16, S split)
+//   Y     = beta V - beta e^G X              (the state-dependent right-hand side)
+//   v_new = T Y                              (= u - w S, without w or u)
+//   S    <- e^G_last S + K^T (D v_new)       (D = exp(G_last - G))
+// Three LDS exchanges (S, Y, D v_new) with a barrier each.  K and V come
+// straight from the input tensors; everything that does not depend on the
+// state (K, T, V, the per-token vectors) is prefetched into registers one
+// chunk ahead through buffer descriptors.  K^T, the A operand of the update,
+// is read transposed out of the LDS copy of the chunk's K rows.
+constexpr int kStateTLds = 2 * 16 * kStrideK * 2 + 4 * 16 * kStrideT * 2 + kChunk * kStrideK * 2;
+__device__ __forceinline__ void t_state(
+    char *smem, int c0, int nch, int bos, int eos, int h, int v0, int wave, int lane,
+    size_t sbase, const uint16_t *k, const uint16_t *v, const float *state, float *new_state,
+    const float *ws_dcy, const float *ws_eg, const uint16_t *ws_w, const float *ws_u,
+    uint16_t *ws_ht, uint16_t *ws_vnt, const Heads &H) {
+  const int r16 = lane & 15, g = lane >> 4, kg = 8 * g, q4 = 4 * g;
+  const int vc = v0 + r16;  // this lane's state column
+  uint16_t *const sSh = reinterpret_cast<uint16_t *>(smem);  // S^T split, [v][k]
+  uint16_t *const sSl = sSh + 16 * kStrideK;
+  uint16_t *const sYh = sSl + 16 * kStrideK;                 // Y split, [v][token]
+  uint16_t *const sYl = sYh + 16 * kStrideT;
+  uint16_t *const sVh = sYl + 16 * kStrideT;                 // D v_new split, [v][token]
+  uint16_t *const sVl = sVh + 16 * kStrideT;
+  uint16_t *const sK = sVl + 16 * kStrideT;                  // the chunk's K rows, [token][k]
+
+  f32x4 S[2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int kr = 16 * (2 * wave + mi) + q4;
+    if (state != nullptr && nch > 0)
+      S[mi] = *reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + kr);
+    else
+      S[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  FragOffsets fo;
+  fo.k = (static_cast<uint32_t>(16 * wave + r16) * H.qk * kDK + kg) * 2;
+  fo.t = static_cast<uint32_t>(wave) * 4096u + static_cast<uint32_t>(lane) * 32u;
+  fo.v = (static_cast<uint32_t>(16 * wave + q4) * H.v * kDV + vc) * 2;
+  fo.vec = static_cast<uint32_t>(16 * wave + q4) * 4u;
+
+  // One chunk of the recurrence, from the prefetched fragments f.
+  auto step = [&](const TFrag &f, int c) {
+    const size_t ch_head = static_cast<size_t>(c) * H.v + h;
+    uint16_t *ht = ws_ht + ch_head * (kDV * kDK);
+    uint16_t *vnt = ws_vnt + ch_head * (kDV * kChunk);
+    // (a) chunk-start state: split copy into LDS ([v][k]) for K S, a bf16 copy
+    //     ([v][k]) for the output kernel; the chunk's K rows into LDS.
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+      const int kr = 16 * (2 * wave + mi) + q4;
+      uint32_t h0, h1, l0, l1;
+      split2(S[mi][0], S[mi][1], h0, l0);
+      split2(S[mi][2], S[mi][3], h1, l1);
+      const u32x2 rn = {pk_bf16(S[mi][0], S[mi][1]), pk_bf16(S[mi][2], S[mi][3])};
+      *reinterpret_cast<u32x2 *>(&sSh[r16 * kStrideK + kr]) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2 *>(&sSl[r16 * kStrideK + kr]) = u32x2{l0, l1};
+      *reinterpret_cast<u32x2 *>(ht + vc * kDK + kr) = rn;
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      *reinterpret_cast<u32x4 *>(&sK[(16 * wave + r16) * kStrideK + 32 * kk + kg]) = f.kf[kk];
+    __syncthreads();
+
+    // (b) X = K S for tokens 16*wave..+15 (two chains: S hi, S lo), then
+    //     Y = beta V - beta e^G X -> LDS (split, [v][token]).  K^T fragments
+    //     for (d): 8 tokens of one K column from the LDS copy of K.
+    {
+      f32x4 X0 = {0.f, 0.f, 0.f, 0.f}, X1 = X0;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const u32x4 sh = *reinterpret_cast<const u32x4 *>(&sSh[r16 * kStrideK + 32 * kk + kg]);
+        const u32x4 sl = *reinterpret_cast<const u32x4 *>(&sSl[r16 * kStrideK + 32 * kk + kg]);
+        X0 = mfma_bf16(f.kf[kk], sh, X0);
+        X1 = mfma_bf16(f.kf[kk], sl, X1);
+      }
+      float y[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        y[r] = f.beta[r] * __uint_as_float(f.vv[r] << 16) - f.bg[r] * (X0[r] + X1[r]);
+      uint32_t h0, h1, l0, l1;
+      split2(y[0], y[1], h0, l0);
+      split2(y[2], y[3], h1, l1);
+      const int i0 = 16 * wave + q4;
+      *reinterpret_cast<u32x2 *>(&sYh[r16 * kStrideT + i0]) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2 *>(&sYl[r16 * kStrideT + i0]) = u32x2{l0, l1};
+    }
+    u32x4 ka[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const u32x2 x = ds_read_tr16(&sK[(32 * kk + kg + 4 * hh + (r16 >> 2)) * kStrideK +
+                                           32 * wave + 16 * mi + 4 * (r16 & 3)]);
+          ka[mi][kk][2 * hh] = x[0];
+          ka[mi][kk][2 * hh + 1] = x[1];
+        }
+    __syncthreads();
+
+    // (c) v_new = T Y for tokens 16*wave..+15 (T and Y split: three chains)
+    //     -> workspace (bf16, [v][token]) for the output kernel;
+    //     D v_new -> LDS (split, [v][token]) for K^T (D v_new).
+    {
+      f32x4 P0 = {0.f, 0.f, 0.f, 0.f}, P1 = P0, P2 = P0;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const u32x4 yh = *reinterpret_cast<const u32x4 *>(&sYh[r16 * kStrideT + 32 * kk + kg]);
+        const u32x4 yl = *reinterpret_cast<const u32x4 *>(&sYl[r16 * kStrideT + 32 * kk + kg]);
+        P0 = mfma_bf16(f.th[kk], yh, P0);
+        P1 = mfma_bf16(f.th[kk], yl, P1);
+        P2 = mfma_bf16(f.tl[kk], yh, P2);
+      }
+      float vn[4], vs[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        vn[r] = (P0[r] + P1[r]) + P2[r];
+        vs[r] = f.dcy[r] * vn[r];
+      }
+      const u32x2 rn = {pk_bf16(vn[0], vn[1]), pk_bf16(vn[2], vn[3])};
+      uint32_t h0, h1, l0, l1;
+      split2(vs[0], vs[1], h0, l0);
+      split2(vs[2], vs[3], h1, l1);
+      const int i0 = 16 * wave + q4;
+      *reinterpret_cast<u32x2 *>(vnt + vc * kChunk + i0) = rn;
+      *reinterpret_cast<u32x2 *>(&sVh[r16 * kStrideT + i0]) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2 *>(&sVl[r16 * kStrideT + i0]) = u32x2{l0, l1};
+    }
+    __syncthreads();
+
+    // (d) S <- exp(G_last) S + K^T (D v_new); K is exact in bf16, so two MFMAs
+    //     (hi, lo) per k-step, in two independent chains.
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+      f32x4 acc = S[mi];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] *= f.eg;
+      f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const u32x4 vh = *reinterpret_cast<const u32x4 *>(&sVh[r16 * kStrideT + 32 * kk + kg]);
+        const u32x4 vl = *reinterpret_cast<const u32x4 *>(&sVl[r16 * kStrideT + 32 * kk + kg]);
+        acc = mfma_bf16(ka[mi][kk], vh, acc);
+        acc2 = mfma_bf16(ka[mi][kk], vl, acc2);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[mi][r] = acc[r] + acc2[r];
+    }
+  };
+
+  // Two fragment sets: chunk i uses set i % 2 while the set of chunk i + 1
+  // is in flight (a third set does not fit in the registers).  The loop body
+  // is two straight steps with one exit test, at the back edge, so the loop
+  // head is reached with the same loads pending from both of its
+  // predecessors and the compiler waits for exactly the set in use (an exit
+  // after each step made it merge those paths and wait for nearly every
+  // prefetch).  A last odd chunk runs after the loop.  Prefetches past the
+  // last chunk re-read it, so every iteration issues the same loads.
+  if (nch > 0) {
+    auto load = [&](TFrag &f, int i) {
+      i = i < nch ? i : nch - 1;
+      const int start = bos + i * kChunk, rem = eos - start;
+      load_t_frag(f, c0 + i, start, rem < kChunk ? rem : kChunk, h, H, fo, k, v, ws_dcy, ws_eg,
+                  ws_w, ws_u);
+    };
+    TFrag fa, fb;
+    load(fa, 0);
+    load(fb, 1);
+    int ci = 0;
+    // (The scheduling barriers keep the compiler from moving work on the
+    // other set's registers into a step, which made it wait for that set's
+    // loads too.)
+    for (; ci + 2 <= nch; ci += 2) {
+      step(fa, c0 + ci);
+      __builtin_amdgcn_sched_barrier(0);
+      load(fa, ci + 2);
+      step(fb, c0 + ci + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      load(fb, ci + 3);
+    }
+    if (ci < nch) step(fa, c0 + ci);
+  }
+
+  // Final state (zeros for a zero-length sequence, as the reference).
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int kr = 16 * (2 * wave + mi) + q4;
+    *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + kr) = S[mi];
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// 3. state recurrence: per (sequence s, v-head h, 16 columns of V),
+// blockIdx.x = h + H.v * (vb + 8 s): with 8 v-heads every workgroup of one
+// head lands on the same XCD (workgroups are dealt round-robin over the 8
+// XCDs), so the per-head operands stream through one L2.  The state tile
+// S[:, v0:v0+16] ([K=128] x [16], f32) lives in MFMA accumulators.  The form
+// is `form` (0 WY, 1 T) or, when form < 0, the index kernel's flag.
+//
+// What bounds a step (MI355X counters): the bytes each workgroup streams in
+// per chunk (WY ~52 KB: w, K^T, u; T ~35 KB: K, T, V), from L2 at 400-750
+// cycles latency with a bounded number of misses in flight per CU, and the
+// serial chain of exchanges (two in the WY form, three in the T form).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prefill_state_kernel(
+    const uint16_t *k, const uint16_t *v, const float *state, float *new_state,
+    const int4 *chunks, const int *offsets, const float *ws_dcy, const float *ws_eg,
+    const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt, uint16_t *ws_ht,
+    uint16_t *ws_vnt, int N, int single_T, Heads H, int form) {
+  __shared__ __align__(16) char smem[kStateWyLds > kStateTLds ? kStateWyLds : kStateTLds];
+  constexpr int NVB = kDV / 16;
+  const int h = blockIdx.x % H.v;
+  const int rest = blockIdx.x / H.v;
+  const int vb = rest % NVB, s = rest / NVB;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in SGPRs
+
+  // This workgroup's chunks: c0 .. c0 + nch - 1.
+  int c0 = 0, nch = (single_T + kChunk - 1) / kChunk;
+  if (single_T < 0) {
+    if (offsets[N + 1]) return;  // the token-sequential kernel owns the batch
+    if (form < 0) form = offsets[N + 2];
+    c0 = offsets[s];
+    nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
+  }
+  const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;  // [V][K]
+  if (form == 1) {
+    // the T form reads K and V itself: the sequence's tokens [bos, eos)
+    int bos = 0, eos = single_T;
+    if (single_T < 0 && nch > 0) {
+      const int4 first = chunks[c0], last = chunks[c0 + nch - 1];
+      bos = first.y;
+      eos = last.y + last.z;
+    }
+    t_state(smem, c0, nch, bos, eos, h, vb * 16, wave, lane, sbase, k, v, state, new_state, ws_dcy,
+            ws_eg, ws_w, ws_u, ws_ht, ws_vnt, H);
+  }
+  else
+    wy_state(smem, c0, nch, h, vb * 16, wave, lane, sbase, state, new_state, ws_dcy, ws_eg, ws_w,
+             ws_u, ws_kt, ws_ht, ws_vnt, H);
 }
 
 // ---------------------------------------------------------------------------
@@ -840,7 +1372,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: state/new_state must be 16-byte aligned");
   if (!aligned(cu_seqlens, cu64 ? 8 : 4))
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: cu_seqlens misaligned");
-  if (variant < -1 || variant > 1) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown variant %d", variant);
+  if (variant < -1 || variant > 1) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown variant %d (0 WY form, 1 T form)", variant);
   if (rec_max < -2) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: recurrent_max_len %d < -2", rec_max);
   if (rec_variant < -1 || rec_variant >= recurrent_num_variants())
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown recurrent tiling %d", rec_variant);
@@ -915,9 +1447,21 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   // from T, and the kernels compute them instead of reading a table.
   const int single_T = (N == 1 && choose == 0) ? T : -1;
   int rc = GDN_OK;
+  // Form of the per-chunk operands: `variant` when 0 (WY) or 1 (T); else the
+  // index kernel's rule (T iff at least 128 chunks and three times the
+  // longest sequence's), settled here when (T, N) alone exclude the T form --
+  // one or two sequences, fewer than 128 chunks, or fewer than three times
+  // the chunks of the mean length, a lower bound on the longest -- so that
+  // only one intra kernel is launched.
+  int form = variant;
+  if (form < 0) {
+    const long long mean_chunks = ((static_cast<long long>(T) + N - 1) / N + kChunk - 1) / kChunk;
+    const bool t_possible = single_T < 0 && N > 2 && L.nt_max >= 128 && L.nt_max >= 3 * mean_chunks;
+    form = t_possible ? -1 : 0;
+  }
   if (single_T < 0) {
     hipLaunchKernelGGL(prefill_index_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, cu64, N, T,
-                       L.nt_max, choose, rec_max, chunks, offsets);
+                       L.nt_max, choose, rec_max, form, chunks, offsets);
     if ((rc = check_launch("gdn_prefill_fwd(index)"))) return rc;
   }
   if (choose != 0) {
@@ -927,19 +1471,23 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     if (rc) return rc;
   }
   if (L.nt_max > 0) {
-    hipLaunchKernelGGL(prefill_intra_kernel, dim3(L.nt_max, H.v), dim3(256), 0, stream, k, v, A_log,
-                       a, dt_bias, b, chunks, single_T, H, wsG, wsD, wsE, wsw, wsu, kt);
-    if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
+    const int *flag = form < 0 ? offsets + N + 2 : nullptr;
+    if (form != 1) {
+      hipLaunchKernelGGL(prefill_intra_wy_kernel, dim3(L.nt_max, H.v), dim3(256), 0, stream, k, v,
+                         A_log, a, dt_bias, b, chunks, single_T, H, flag, wsG, wsD, wsE, wsw, wsu, kt);
+      if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
+    }
+    if (form != 0) {
+      hipLaunchKernelGGL(prefill_intra_t_kernel, dim3(L.nt_max, H.v), dim3(256), 0, stream, k,
+                         A_log, a, dt_bias, b, chunks, single_T, H, flag, wsG, wsD, wsE, wsw, wsu);
+      if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
+    }
   }
-  const int bv = variant == 1 ? 32 : 16;  // 16 measured faster at every size
-  const long long blocks = static_cast<long long>(N) * H.v * (kDV / bv);
+  const long long blocks = static_cast<long long>(N) * H.v * (kDV / 16);
   if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
-  if (bv == 32)
-    hipLaunchKernelGGL(prefill_state_kernel<32>, dim3(static_cast<unsigned>(blocks)), dim3(512), 0,
-                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N, single_T, H);
-  else
-    hipLaunchKernelGGL(prefill_state_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       stream, state, new_state, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N, single_T, H);
+  hipLaunchKernelGGL(prefill_state_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                     k, v, state, new_state, chunks, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N,
+                     single_T, H, form);
   if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
   if (L.nt_max > 0) {
     hipLaunchKernelGGL(prefill_output_kernel, dim3(L.nt_max, H.v), dim3(256), 0, stream, q, k, chunks,

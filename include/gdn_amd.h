@@ -164,14 +164,21 @@ int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                     size_t workspace_bytes, void *stream);
 
 /*
- * gdn_prefill_fwd with an explicit tiling of the serial state recurrence:
- * variant 0 = 16-column V blocks (8 workgroups of 4 waves per sequence and
- * head), 1 = 32-column blocks (4 workgroups of 8 waves: two 16-column teams
- * sharing each SIMD), -1 = the built-in choice (what gdn_prefill_fwd uses).  The counterpart of the reference's autotuned
- * BV of chunk_gated_delta_rule_fwd_kernel_h (solutions/
+ * gdn_prefill_fwd with an explicit form of the per-chunk operands:
+ * variant 0 = WY form (the intra kernel forms w = (I+A)^-1 beta e^G K and
+ * u = (I+A)^-1 beta V; each serial state step is v_new = u - w S: the
+ * shortest chain), 1 = T form (the intra kernel stores only (I+A)^-1; each
+ * state step forms beta V - beta e^G K S from the inputs: less memory
+ * traffic, one more exchange per step), -1 = the built-in choice (what
+ * gdn_prefill_fwd uses: the T form for batches of at least 128 chunks with at
+ * least three times the chunks of their longest sequence, decided on the
+ * device; the WY form otherwise and for one sequence).  The counterpart of
+ * the reference's autotuned launch parameters of
+ * chunk_gated_delta_rule_fwd_kernel_h (solutions/
  * gdn_prefill_qk4_v8_d128_k_last/solution/triton/fla_kernels.py:407-426,
- * 1028-1035).  Results are identical for every variant (a batch that runs
- * token by token does not depend on it).
+ * 1028-1035).  Both forms compute the same function within the stated
+ * tolerances (not bit for bit); a batch that runs token by token does not
+ * depend on the variant.
  */
 int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                             const float *state, const float *A_log, const gdn_bf16 *a,
@@ -182,7 +189,8 @@ int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16
 
 /*
  * gdn_prefill_fwd with every tuning choice explicit (for sweeps and tests):
- *   state_tiling       as the variant of gdn_prefill_fwd_variant (-1 built-in)
+ *   state_tiling       the form, as the variant of gdn_prefill_fwd_variant
+ *                      (-1 built-in)
  *   recurrent_max_len  a batch whose longest sequence has at most this many
  *                      tokens runs token by token; -1 = built-in, -2 = never
  *                      (always chunked)

@@ -155,14 +155,69 @@ def test_prefill_config4_long_context(cuda_device):
     check(o, s, o_ref, s_ref)
 
 
-def test_prefill_variants_identical(cuda_device):
-    inp = O.make_prefill_inputs([100, 0, 300], seed=12)
+# Forms of the per-chunk operands (variant): 0 WY, 1 T.
+FORMS = {"wy": 0, "t": 1}
+
+
+def form_rule(lens):
+    """Restatement of the built-in form choice of gdn_prefill.hip (index
+    kernel): the T form for a batch of several sequences with at least 128
+    chunks and at least three times the chunks of the longest one."""
+    chunks = [-(-L // 64) for L in lens]
+    nt, longest = sum(chunks), max(chunks)
+    return 1 if len(lens) > 1 and nt >= 128 and nt >= 3 * longest else 0
+
+
+@pytest.mark.parametrize("form", list(FORMS))
+def test_prefill_forms_reference_and_edge_cases(cuda_device, form):
+    # Every reference case and edge length through the chunks in both forms.
+    cases = [(lens, st) for lens, st in REFERENCE_CASES] + \
+        [(lens, True) for lens in ([1], [2, 1, 3], [63], [0, 5, 0, 70], [0], [0, 0, 17],
+                                   [129, 0, 1, 64, 65], [100, 0, 300])]
+    for i, (lens, with_state) in enumerate(cases):
+        print(f"prefill form={form} lens={lens} state={with_state}", flush=True)
+        inp = O.make_prefill_inputs(lens, seed=300 + i, with_state=with_state)
+        o_ref, s_ref = O.prefill_seq_c(**inp)
+        o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, variant=FORMS[form], route="chunked")
+        for j, L in enumerate(lens):
+            if L == 0:
+                assert np.all(s[j] == 0.0), "zero-length sequence must give a zero state"
+        check(o, s, o_ref, s_ref)
+
+
+@pytest.mark.parametrize("lens", [[512] * 16, [1024] * 8, [2048] * 4, [4096] * 2, [8192, 1024, 512, 100],
+                                  [6, 49, 294, 1800, 2040, 61], [64] * 130])
+def test_prefill_built_in_form_choice(cuda_device, lens):
+    # The built-in choice is bit-identical to the form the rule names, and
+    # the flag the index kernel leaves in the workspace is that form.
+    from gdn_amd import prefill
+    print(f"prefill form choice lens={len(lens)}x{lens[0]}.. expect {form_rule(lens)}", flush=True)
+    inp = O.make_prefill_inputs(lens, seed=21)
     d = to_dev(inp, cuda_device)
-    o0, s0 = run_gpu(d, cuda_device, variant=0, route="chunked")
-    o1, s1 = run_gpu(d, cuda_device, variant=1, route="chunked")
-    assert np.array_equal(o0, o1) and np.array_equal(s0, s1)
+    o_a, s_a = run_gpu(d, cuda_device, variant=-1, route="chunked")
+    T, N = sum(lens), len(lens)
+    L = _layout(T, N)
+    ws = prefill._workspace(cuda_device, _stream(cuda_device), 0).cpu().numpy()
+    flag = np.frombuffer(ws[L["offsets"]:L["offsets"] + (N + 3) * 4].tobytes(), np.int32)[N + 2]
+    assert flag == form_rule(lens)
+    o_f, s_f = run_gpu(d, cuda_device, variant=form_rule(lens), route="chunked")
+    assert np.array_equal(o_a, o_f) and np.array_equal(s_a, s_f)
     o_ref, s_ref = O.prefill_seq_c(**inp)
-    check(o0, s0, o_ref, s_ref)
+    check(o_a, s_a, o_ref, s_ref)
+
+
+@pytest.mark.parametrize("name", ["prefill_1x8192", "prefill_varlen6", "prefill_4x8192"])
+def test_prefill_forms_full_size(cuda_device, name):
+    # The benchmark configurations at full size in the form the built-in
+    # choice does not take for them.
+    cfg = O.CONFIGS[name]
+    kw = {"slow_decay_heads": cfg["slow_decay_heads"]} if "slow_decay_heads" in cfg else {}
+    inp = O.make_prefill_inputs(cfg["lens"], seed=cfg["seed"], with_state=cfg["with_state"], **kw)
+    other = 1 - form_rule(cfg["lens"])
+    print(f"prefill {name} form={other}", flush=True)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, variant=other, route="chunked")
+    check(o, s, o_ref, s_ref)
 
 
 @pytest.mark.parametrize("route", list(ROUTES))
@@ -270,12 +325,12 @@ def _layout(T, N):
         off = (off + nbytes + 255) // 256 * 256
 
     take("chunks", nt * 16)
-    take("offsets", (N + 2) * 4)  # offsets[0..N], then the path flag
+    take("offsets", (N + 3) * 4)  # offsets[0..N], then the path and form flags
     take("G", nt * 8 * 64 * 4)
     take("dcy", nt * 8 * 64 * 4)
     take("eg", nt * 8 * 4)
-    take("w", nt * 8 * 64 * 128 * 4)
-    take("u", nt * 8 * 64 * 128 * 4)
+    take("w", nt * 8 * 64 * 128 * 4)  # WY: w; T form: (I + A)^-1
+    take("u", nt * 8 * 64 * 128 * 4)  # WY: u; T form: beta, beta exp(G)
     take("kt", nt * 4 * 128 * 64 * 2)
     take("ht", nt * 8 * 128 * 128 * 2)
     take("vnt", nt * 8 * 128 * 64 * 2)
@@ -283,7 +338,8 @@ def _layout(T, N):
     return L
 
 
-def test_prefill_stage_intermediates(cuda_device):
+@pytest.mark.parametrize("form", list(FORMS))
+def test_prefill_stage_intermediates(cuda_device, form):
     from gdn_amd import _lib, prefill
     lens = [100, 0, 64, 5]
     inp = O.make_prefill_inputs(lens, seed=18)
@@ -291,7 +347,7 @@ def test_prefill_stage_intermediates(cuda_device):
     L = _layout(T, N)
     assert prefill.workspace_bytes(T, N) == L["total"]
     d = to_dev(inp, cuda_device)
-    run_gpu(d, cuda_device, route="chunked")
+    run_gpu(d, cuda_device, variant=FORMS[form], route="chunked")
     ws = prefill._workspace(cuda_device, _stream(cuda_device), 0).cpu().numpy()
     _, _, it = O.prefill_chunked(**inp, return_intermediates=True)
     seq, local, offs = O.chunk_index(inp["cu_seqlens"])
@@ -306,23 +362,56 @@ def test_prefill_stage_intermediates(cuda_device):
     assert chunks[:nt, 0].tolist() == seq.tolist()
     assert chunks[:nt, 3].tolist() == local.tolist()
     assert (chunks[nt:, 0] == -1).all()
-    assert arr("offsets", np.int32, (N + 1,)).tolist() == offs.tolist()
+    flags = arr("offsets", np.int32, (N + 3,))
+    assert flags[:N + 1].tolist() == offs.tolist()
+    assert flags[N + 1] == 0 and flags[N + 2] == FORMS[form]  # chunk path, this form
     G = arr("G", np.float32, (L["nt"], 8, 64))[:nt]
+    dcy = arr("dcy", np.float32, (L["nt"], 8, 64))[:nt]
+    eg = arr("eg", np.float32, (L["nt"], 8))[:nt]
     for c in range(nt):
         C = min(64, lens[seq[c]] - 64 * local[c])
-        assert np.allclose(G[c, :, :C], it["g_cs"][c, :, :C], rtol=1e-5, atol=1e-5)
-    # u: MFMA result tiles [c][h][row tile i][col tile n][lane][r] holding
-    # u[16i + 4(lane >> 4) + r][16n + (lane & 15)]
-    ut = arr("u", np.float32, (L["nt"], 8, 4, 8, 4, 16, 4))[:nt]  # lane = (g, r16)
-    u = ut.transpose(0, 1, 2, 4, 6, 3, 5).reshape(nt, 8, 64, 128)
-    assert np.abs(u - it["u"]).max() <= 1e-4 * np.abs(it["u"]).max()
-    # w: A fragments [c][h][mb][kk][lane][hi 8 | lo 8] holding
-    # w[16mb + (lane & 15)][32kk + 8(lane >> 4) + e]
-    wf = arr("w", np.uint16, (L["nt"], 8, 4, 4, 4, 16, 2, 8))[:nt]  # lane = (g, r16)
-    wv = (O.bf16_from_bits(wf[..., 0, :]).astype(np.float64)
-          + O.bf16_from_bits(wf[..., 1, :]))                       # [c,h,mb,kk,g,r16,e]
-    w = wv.transpose(0, 1, 2, 5, 3, 4, 6).reshape(nt, 8, 64, 128)
-    assert np.abs(w - it["w"]).max() <= 1e-4 * np.abs(it["w"]).max()
+        Gc = it["g_cs"][c, :, :C]
+        assert np.allclose(G[c, :, :C], Gc, rtol=1e-5, atol=1e-5)
+        assert np.allclose(dcy[c, :, :C], np.exp(Gc[:, -1:] - Gc), rtol=1e-4, atol=1e-6)
+        assert np.allclose(eg[c], np.exp(Gc[:, -1]), rtol=1e-4, atol=1e-7)
+    if form == "wy":
+        # u: MFMA result tiles [c][h][row tile i][col tile n][lane][r] holding
+        # u[16i + 4(lane >> 4) + r][16n + (lane & 15)]
+        ut = arr("u", np.float32, (L["nt"], 8, 4, 8, 4, 16, 4))[:nt]  # lane = (g, r16)
+        u = ut.transpose(0, 1, 2, 4, 6, 3, 5).reshape(nt, 8, 64, 128)
+        assert np.abs(u - it["u"]).max() <= 1e-4 * np.abs(it["u"]).max()
+        # w: A fragments [c][h][mb][kk][lane][hi 8 | lo 8] holding
+        # w[16mb + (lane & 15)][32kk + 8(lane >> 4) + e]
+        wf = arr("w", np.uint16, (L["nt"], 8, 4, 4, 4, 16, 2, 8))[:nt]  # lane = (g, r16)
+        wv = (O.bf16_from_bits(wf[..., 0, :]).astype(np.float64)
+              + O.bf16_from_bits(wf[..., 1, :]))                       # [c,h,mb,kk,g,r16,e]
+        w = wv.transpose(0, 1, 2, 5, 3, 4, 6).reshape(nt, 8, 64, 128)
+        assert np.abs(w - it["w"]).max() <= 1e-4 * np.abs(it["w"]).max()
+    else:
+        # T = (I + A)^-1 in the w region: A fragments [c][h][rt][kk][lane][hi 8 | lo 8]
+        # holding T[16rt + (lane & 15)][32kk + 8(lane >> 4) + e]
+        # (w region stride per (chunk, head): 64 x 128 x 2 bf16; T fills the first half)
+        tf = arr("w", np.uint16, (L["nt"], 8, 64 * 128 * 2))[:nt, :, :64 * 64 * 2]
+        tf = tf.reshape(nt, 8, 4, 2, 4, 16, 2, 8)                       # lane = (g, r16)
+        tv = (O.bf16_from_bits(tf[..., 0, :]).astype(np.float64)
+              + O.bf16_from_bits(tf[..., 1, :]))                       # [c,h,rt,kk,g,r16,e]
+        Tm = tv.transpose(0, 1, 2, 5, 3, 4, 6).reshape(nt, 8, 64, 64)
+        # (beta, beta e^G) in the u region: [c][h][2][64] (u region stride 64 x 128 f32)
+        bb = arr("u", np.float32, (L["nt"], 8, 64 * 128))[:nt, :, :128].reshape(nt, 8, 2, 64)
+        beta = 1.0 / (1.0 + np.exp(-inp["b"].astype(np.float64)))
+        for c in range(nt):
+            C = min(64, lens[seq[c]] - 64 * local[c])
+            t0 = int(inp["cu_seqlens"][seq[c]]) + 64 * local[c]
+            Gc = it["g_cs"][c, :, :C]
+            assert np.allclose(bb[c, :, 0, :C], beta[t0:t0 + C].T, rtol=1e-6, atol=1e-7)
+            assert np.allclose(bb[c, :, 1, :C], beta[t0:t0 + C].T * np.exp(Gc), rtol=1e-4, atol=1e-6)
+            assert (bb[c, :, :, C:] == 0).all()
+            # (I + A)^-1 on the chunk's rows, identity on the padding rows
+            Ai = it["Ai"][c, :, :C, :C]
+            assert np.abs(Tm[c, :, :C, :C] - Ai).max() <= 1e-4 * max(1.0, np.abs(Ai).max())
+            pad = np.zeros((8, 64, 64))
+            pad[:, C:, C:] = np.eye(64 - C)
+            assert (Tm[c][:, C:, :] == pad[:, C:, :]).all() and (Tm[c][:, :C, C:] == 0).all()
     ht = O.bf16_from_bits(arr("ht", np.uint16, (L["nt"], 8, 128, 128))[:nt])
     assert np.abs(ht - it["h"].transpose(0, 1, 3, 2)).max() <= 1e-2 * np.abs(it["h"]).max()
     vnt = O.bf16_from_bits(arr("vnt", np.uint16, (L["nt"], 8, 128, 64))[:nt])
