@@ -9,9 +9,10 @@ twice the 256 MB Infinity Cache) so no step reads a state that is still cached.
 
 Reported beside it: decode kernel time and achieved HBM bandwidth (the
 roofline of the dominant kernel, from HIP events around each launch on the
-launch stream), the prefill at 1x8192 (ms and tokens/s), and the CPU baseline
-(the reference's loop nest restated in numpy, oracle/gdn_oracle.py:decode_loop,
-single thread, on a bounded sample).
+launch stream), the decode batch sweep of configs[1], the prefill at 1x8192
+(ms and tokens/s) and at configs[2..4], and the CPU baseline (the reference's
+loop nest restated in numpy, oracle/gdn_oracle.py:decode_loop, single thread,
+on a bounded sample).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep]
 """
@@ -62,6 +63,7 @@ ONLY_WORKLOADS = {
     "prefill_1x1024": ("prefill", [1024]),
     "prefill_64x16": ("prefill", [16] * 64),
     "prefill_configs3": ("prefill", [6, 49, 294, 1800, 2040, 61]),
+    "prefill_8x2048": ("prefill", [2048] * 8),
 }
 
 
@@ -125,7 +127,7 @@ def bench_decode(B, steps, warmup, dev, variant=-1, tokens=1):
     return ms_eager, ms_graph
 
 
-def bench_prefill(lens, steps, warmup, dev, variant=-1):
+def bench_prefill(lens, steps, warmup, dev, variant=-1, slow_decay_heads=None):
     """Times `steps` prefill calls on a packed batch with sequence lengths
     `lens` (the configs[2..4] recipe, zero initial state for one sequence)
     and returns (eager ms/call, graph ms/call)."""
@@ -134,7 +136,8 @@ def bench_prefill(lens, steps, warmup, dev, variant=-1):
     from gdn_amd import prefill
     from oracle import gdn_oracle as O  # input recipe only
 
-    inp = O.make_prefill_inputs(lens, seed=2, with_state=len(lens) > 1)
+    kw = {} if slow_decay_heads is None else {"slow_decay_heads": slow_decay_heads}
+    inp = O.make_prefill_inputs(lens, seed=2, with_state=len(lens) > 1, **kw)
     d = _dev_inputs(inp, dev)
     cu = torch.from_numpy(inp["cu_seqlens"]).to(dev)
     T, N = sum(lens), len(lens)
@@ -333,6 +336,23 @@ def main():
         short[name] = round(pg, 4)
     log(f"short-sequence prefill (ms per call): {short}")
 
+    # the decode batch sweep (one step in graph replay per B), and
+    # the prefill configurations configs[3] and configs[4] (configs[2] is
+    # the 1x1024 line above); the 4x8192 recipe skews heads 6-7 to near-unit
+    # decay.
+    sweep = {}
+    for b in (1, 2, 4, 8, 16, 32, 48, 64):
+        _, mg = bench_decode(b, 100, 10, dev)
+        sweep[f"B{b}"] = {"us": round(mg * 1e3, 3),
+                          "GBps": round(O.decode_bytes(b) / (mg * 1e-3) / 1e9, 1)}
+    log(f"decode sweep (graph us/step, GB/s): {sweep}")
+    cfg_ms = {}
+    for name, lens, kw in (("configs3_varlen6", [6, 49, 294, 1800, 2040, 61], {}),
+                           ("configs4_4x8192", [8192] * 4, {"slow_decay_heads": (6, 7)})):
+        _, pg = bench_prefill(lens, 10, 2, dev, **kw)
+        cfg_ms[name] = round(pg, 4)
+    log(f"prefill configs (graph ms per call): {cfg_ms}")
+
     cpu_s, reps = cpu_baseline_decode(B, args.cpu_seconds)
     cpu_gbs = nbytes / cpu_s / 1e9
     log(f"cpu baseline decode B={B}: {cpu_s * 1e3:.1f} ms/step over {reps} steps")
@@ -361,6 +381,8 @@ def main():
         "prefill_ms_1x8192_clone": round(pre_clone, 4),
         "prefill_ms_1x1024": round(pre1k_ms, 4),
         "prefill_ms_1x1024_clone": round(pre1k_clone, 4),
+        "decode_sweep": sweep,
+        "prefill_ms_configs": cfg_ms,
         "decode_multi_token_us": mtp,
         "prefill_ms_short_batches": short,
         "prefill_roofline": {"bound": "mfma", "achieved": round(pre_tflops, 2), "peak": 2500.0,
