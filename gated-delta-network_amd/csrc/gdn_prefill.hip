@@ -225,6 +225,26 @@ __device__ __forceinline__ int4 chunk_info(const int4 *chunks, int c, int single
   return chunks[c];
 }
 
+// Workgroup id -> (chunk c, v-head h) for the per-(chunk, head) kernels, so
+// that the `ratio` v-heads reading one q/k head of one chunk are dispatched
+// back to back on the same XCD: ids are dealt round-robin over the 8 XCDs,
+// so id = 8 s + x runs on XCD x, and consecutive s on one XCD take the
+// v-heads of one (chunk, q/k head) pair -- the second and later ones find
+// that chunk's q/k rows in the XCD's L2.  Pairs are numbered P = 8 p + x in
+// chunk-major order.  False for ids past the last pair.
+__host__ __device__ inline long long chunk_head_grid(int nt, const Heads &H) {
+  return (static_cast<long long>(nt) * H.qk + 7) / 8 * 8 * H.ratio;
+}
+__device__ __forceinline__ bool chunk_head_of(int id, int nt, const Heads &H, int &c, int &h) {
+  const int x = id & 7, sl = id >> 3;
+  const int p = sl / H.ratio, r = sl - p * H.ratio;
+  const long long P = 8LL * p + x;
+  if (P >= static_cast<long long>(nt) * H.qk) return false;
+  c = static_cast<int>(P / H.qk);
+  h = static_cast<int>(P - static_cast<long long>(c) * H.qk) * H.ratio + r;
+  return true;
+}
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
@@ -692,7 +712,7 @@ __device__ __forceinline__ void t_intra(
 
 
 // ---------------------------------------------------------------------------
-// 2. intra-chunk: per (chunk c = blockIdx.x, v-head h = blockIdx.y), one
+// 2. intra-chunk: per (chunk c, v-head h) = chunk_head_of(blockIdx.x), one
 // kernel per form, each with its own LDS size (the T form's 35 KB lets four
 // workgroups share a CU, the WY form's 52 KB three).  When the form is left
 // to the device (form_flag != nullptr) both are launched and each returns at
@@ -702,12 +722,14 @@ __global__ __launch_bounds__(256) void prefill_intra_wy_kernel(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
-    const int4 *__restrict__ chunks, int single_T, Heads H, const int *__restrict__ form_flag,
-    float *__restrict__ ws_G, float *__restrict__ ws_dcy, float *__restrict__ ws_eg,
-    uint16_t *__restrict__ ws_w, float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
+    const int4 *__restrict__ chunks, int single_T, int nt_max, Heads H,
+    const int *__restrict__ form_flag, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
+    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u,
+    uint16_t *__restrict__ ws_kt) {
   __shared__ __align__(16) char smem[kIntraWyLds];
   if (form_flag != nullptr && *form_flag != 0) return;
-  const int c = blockIdx.x, h = blockIdx.y;
+  int c, h;
+  if (!chunk_head_of(blockIdx.x, nt_max, H, c, h)) return;
   const int4 ch = chunk_info(chunks, c, single_T);
   if (ch.x < 0) return;
   wy_intra(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u,
@@ -717,12 +739,14 @@ __global__ __launch_bounds__(256) void prefill_intra_wy_kernel(
 __global__ __launch_bounds__(256) void prefill_intra_t_kernel(
     const uint16_t *__restrict__ k, const float *__restrict__ A_log,
     const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
-    const uint16_t *__restrict__ b, const int4 *__restrict__ chunks, int single_T, Heads H,
-    const int *__restrict__ form_flag, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
-    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u) {
+    const uint16_t *__restrict__ b, const int4 *__restrict__ chunks, int single_T, int nt_max,
+    Heads H, const int *__restrict__ form_flag, float *__restrict__ ws_G,
+    float *__restrict__ ws_dcy, float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w,
+    float *__restrict__ ws_u) {
   __shared__ __align__(16) char smem[kIntraTLds];
   if (form_flag != nullptr && *form_flag != 1) return;
-  const int c = blockIdx.x, h = blockIdx.y;
+  int c, h;
+  if (!chunk_head_of(blockIdx.x, nt_max, H, c, h)) return;
   const int4 ch = chunk_info(chunks, c, single_T);
   if (ch.x < 0) return;
   t_intra(smem, c, h, ch.y, ch.z, k, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u);
@@ -1231,16 +1255,17 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// 4. chunk output: per (chunk c = blockIdx.x, v-head h = blockIdx.y).
+// 4. chunk output: per (chunk c, v-head h) = chunk_head_of(blockIdx.x).
 //   P  = mask_{j<=i} exp(G_i - G_j) Q K^T      (waves split the rows)
 //   O  = exp(G_i) Q S_c + P v_new              (waves split the columns)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prefill_output_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
-    const int4 *__restrict__ chunks, int single_T, Heads H, const float *__restrict__ ws_G,
-    const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
+    const int4 *__restrict__ chunks, int single_T, int nt_max, Heads H,
+    const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
     uint16_t *__restrict__ out) {
-  const int c = blockIdx.x, h = blockIdx.y;
+  int c, h;
+  if (!chunk_head_of(blockIdx.x, nt_max, H, c, h)) return;
   const int4 ch = chunk_info(chunks, c, single_T);
   if (ch.x < 0) return;
   const int start = ch.y, len = ch.z;
@@ -1470,16 +1495,19 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
                           "gdn_prefill_fwd");
     if (rc) return rc;
   }
+  const long long grid_ll = chunk_head_grid(L.nt_max, H);
+  if (grid_ll > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many tokens");
+  const unsigned grid = static_cast<unsigned>(grid_ll);
   if (L.nt_max > 0) {
     const int *flag = form < 0 ? offsets + N + 2 : nullptr;
     if (form != 1) {
-      hipLaunchKernelGGL(prefill_intra_wy_kernel, dim3(L.nt_max, H.v), dim3(256), 0, stream, k, v,
-                         A_log, a, dt_bias, b, chunks, single_T, H, flag, wsG, wsD, wsE, wsw, wsu, kt);
+      hipLaunchKernelGGL(prefill_intra_wy_kernel, dim3(grid), dim3(256), 0, stream, k, v, A_log, a,
+                         dt_bias, b, chunks, single_T, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu, kt);
       if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
     }
     if (form != 0) {
-      hipLaunchKernelGGL(prefill_intra_t_kernel, dim3(L.nt_max, H.v), dim3(256), 0, stream, k,
-                         A_log, a, dt_bias, b, chunks, single_T, H, flag, wsG, wsD, wsE, wsw, wsu);
+      hipLaunchKernelGGL(prefill_intra_t_kernel, dim3(grid), dim3(256), 0, stream, k, A_log, a,
+                         dt_bias, b, chunks, single_T, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu);
       if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
     }
   }
@@ -1490,8 +1518,8 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
                      single_T, H, form);
   if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
   if (L.nt_max > 0) {
-    hipLaunchKernelGGL(prefill_output_kernel, dim3(L.nt_max, H.v), dim3(256), 0, stream, q, k, chunks,
-                       single_T, H, wsG, ht, vnt, scale, output);
+    hipLaunchKernelGGL(prefill_output_kernel, dim3(grid), dim3(256), 0, stream, q, k, chunks,
+                       single_T, L.nt_max, H, wsG, ht, vnt, scale, output);
     if ((rc = check_launch("gdn_prefill_fwd(output)"))) return rc;
   }
   return GDN_OK;
