@@ -1259,7 +1259,8 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
 //   P  = mask_{j<=i} exp(G_i - G_j) Q K^T      (waves split the rows)
 //   O  = exp(G_i) Q S_c + P v_new              (waves split the columns)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void prefill_output_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+void prefill_output_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
     const int4 *__restrict__ chunks, int single_T, int nt_max, Heads H,
     const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
@@ -1269,40 +1270,51 @@ __global__ __launch_bounds__(256) void prefill_output_kernel(
   const int4 ch = chunk_info(chunks, c, single_T);
   if (ch.x < 0) return;
   const int start = ch.y, len = ch.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
   const int hq = h / H.ratio;
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
 
+  // 27 KB of LDS and at most 128 VGPRs: four workgroups per CU.
   __shared__ __align__(16) uint16_t sQ[kChunk * kStrideK];
-  __shared__ __align__(16) uint16_t sK[kChunk * kStrideK];
   __shared__ __align__(16) uint16_t sP[kChunk * kStrideT];
   __shared__ float sG[kChunk];
+
+  // K rows as B operands of Q K^T straight from the input (16 contiguous
+  // bytes per lane; rows past the chunk read zero through the descriptor's
+  // range): wave w needs the rows of key blocks 0..w.
+  const auto rk = buf_rsrc(k + (static_cast<size_t>(start) * H.qk + hq) * kDK,
+                           static_cast<uint32_t>(len) * static_cast<uint32_t>(H.qk) * (kDK * 2));
+  u32x4 kb[4][4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      kb[nb][kk] = nb <= wave ? buf_load16(rk, (static_cast<uint32_t>(16 * nb + r16) * H.qk * kDK +
+                                                32 * kk + kg) * 2)
+                              : u32x4{0u, 0u, 0u, 0u};
 
   if (tid < kChunk) sG[tid] = ws_G[ch_head * kChunk + tid];
   for (int idx = tid; idx < kChunk * 16; idx += 256) {
     const int row = idx >> 4, c8 = (idx & 15) * 8;
-    u32x4 qv = {0u, 0u, 0u, 0u}, kv = {0u, 0u, 0u, 0u};
-    if (row < len) {
-      const size_t t = static_cast<size_t>(start) + row;
-      qv = *reinterpret_cast<const u32x4 *>(q + (t * H.qk + hq) * kDK + c8);
-      kv = *reinterpret_cast<const u32x4 *>(k + (t * H.qk + hq) * kDK + c8);
-    }
+    u32x4 qv = {0u, 0u, 0u, 0u};
+    if (row < len)
+      qv = *reinterpret_cast<const u32x4 *>(q + ((static_cast<size_t>(start) + row) * H.qk + hq) * kDK + c8);
     *reinterpret_cast<u32x4 *>(&sQ[row * kStrideK + c8]) = qv;
-    *reinterpret_cast<u32x4 *>(&sK[row * kStrideK + c8]) = kv;
   }
   __syncthreads();
 
   {
     const int mb = wave;
+#pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
       if (nb <= mb) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
           const u32x4 af = *reinterpret_cast<const u32x4 *>(&sQ[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
-          const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[(16 * nb + r16) * kStrideK + 32 * kk + kg]);
-          acc = mfma_bf16(af, bf, acc);
+          acc = mfma_bf16(af, kb[nb][kk], acc);
         }
       }
 #pragma unroll
