@@ -206,6 +206,38 @@ def test_prefill_built_in_form_choice(cuda_device, lens):
     check(o_a, s_a, o_ref, s_ref)
 
 
+@pytest.mark.parametrize("form", list(FORMS))
+def test_prefill_forms_extreme_gates(cuda_device, form):
+    # Per-head gates around softplus' threshold (x > 20), beta saturated at 0
+    # and 1, decays ~1 and so fast that exp(G) underflows inside a chunk.
+    lens = [200, 64, 130]
+    inp = O.make_prefill_inputs(lens, seed=31)
+    rng = np.random.default_rng(31)
+    T = sum(lens)
+    a_h = np.array([30.0, -30.0, 20.0, 0.0, 19.5, -5.0, 5.0, 1.0], np.float32)
+    b_h = np.array([-40.0, 40.0, 0.0, 8.0, -8.0, 1.0, -1.0, 0.0], np.float32)
+    inp["a"][:] = O.bf16_round(a_h[None, :] + rng.normal(0, 0.5, (T, 8)).astype(np.float32))
+    inp["b"][:] = O.bf16_round(b_h[None, :] + rng.normal(0, 0.5, (T, 8)).astype(np.float32))
+    inp["A_log"][:] = np.array([-10.0, 2.7, 0.0, -20.0, 1.0, 0.5, 0.1, 2.0], np.float32)
+    print(f"prefill extreme gates form={form}", flush=True)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, variant=FORMS[form], route="chunked")
+    assert np.isfinite(o).all() and np.isfinite(s).all()
+    check(o, s, o_ref, s_ref)
+
+
+def test_prefill_forms_long_sequence(cuda_device):
+    # One 32768-token sequence (512 chunks, initial state, two near-unit-decay
+    # heads) through both forms against one oracle run.
+    inp = O.make_prefill_inputs([32768], seed=32, slow_decay_heads=(6, 7))
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    d = to_dev(inp, cuda_device)
+    for form, var in FORMS.items():
+        print(f"prefill 1x32768 form={form}", flush=True)
+        o, s = run_gpu(d, cuda_device, variant=var, route="chunked")
+        check(o, s, o_ref, s_ref)
+
+
 @pytest.mark.parametrize("name", ["prefill_1x8192", "prefill_varlen6", "prefill_4x8192"])
 def test_prefill_forms_full_size(cuda_device, name):
     # The benchmark configurations at full size in the form the built-in
