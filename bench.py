@@ -259,8 +259,8 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the operators "
-              "are per-GPU shards with no cross-GPU exchange; see DESIGN.md for how they "
-              "would shard).", file=sys.stderr)
+              "are per-GPU shards: decode splits over batch rows or heads and prefill over "
+              "sequences or heads, with no cross-GPU exchange).", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -65,8 +65,15 @@ constexpr int kTElems = kChunk * kChunk * 2;  // T of one (chunk, head): hi + lo
 struct PrefillLayout {
   int nt_max;  // upper bound on the chunk count from (T, N) alone
   // The T form keeps T in the w region and (beta, beta e^G) in the u region.
-  size_t chunks, offsets, G, dcy, eg, w, u, kt, ht, vnt, total;
+  size_t chunks, offsets, G, dcy, eg, w, u, kt, ht, vnt;
+  // Two-segment scan of one sequence (N == 1 only, else empty): the map's
+  // linear part per chunk of the second segment, the first segment's final
+  // state and the second segment's map (offset, linear part).
+  size_t htm, send, cend, mend, total;
 };
+
+// First chunk of the second segment of a two-segment scan over nt chunks.
+__host__ __device__ inline int split_first(int nt) { return (nt + 1) / 2; }
 
 static long long max_chunks(long long T, long long N) {
   if (T <= 0 || N <= 0) return 0;
@@ -96,6 +103,12 @@ static PrefillLayout prefill_layout(int T, int N, const Heads &H) {
   L.kt = take(n * hqk * kDK * kChunk * 2);
   L.ht = take(n * hv * kDV * kDK * 2);
   L.vnt = take(n * hv * kDV * kChunk * 2);
+  const size_t n1 = N == 1 ? static_cast<size_t>(nt - split_first(static_cast<int>(nt))) : 0;
+  const size_t one = N == 1 ? 1 : 0;
+  L.htm = take(n1 * hv * kDV * kDK * 2);
+  L.send = take(one * hv * kDV * kDK * 4);
+  L.cend = take(one * hv * kDV * kDK * 4);
+  L.mend = take(one * hv * kDV * kDK * 4);
   L.total = off;
   return L;
 }
@@ -787,6 +800,7 @@ struct WyFrag {
   float eg;            // exp(G_last)
 };
 
+template <bool LOAD_U>
 __device__ __forceinline__ void load_wy_frag(WyFrag &f, int c, int h, const Heads &H,
                                                 int vw, int wave, int lane, const float *ws_dcy,
                                                 const float *ws_eg, const uint16_t *ws_w,
@@ -809,8 +823,12 @@ __device__ __forceinline__ void load_wy_frag(WyFrag &f, int c, int h, const Head
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) f.ka[mi][kk] = buf_load16(rk, ko + mi * 2048 + kk * 1024);
   // u: [row tile][col tile][lane][4] result tiles
-  const auto ru = buf_rsrc(ws_u + ch_head * (kUBytes / 4), kUBytes);
-  f.u = __builtin_bit_cast(f32x4, buf_load16(ru, static_cast<uint32_t>((wave * 8 + (vw >> 4)) * 64 + lane) * 16u));
+  if constexpr (LOAD_U) {
+    const auto ru = buf_rsrc(ws_u + ch_head * (kUBytes / 4), kUBytes);
+    f.u = __builtin_bit_cast(f32x4, buf_load16(ru, static_cast<uint32_t>((wave * 8 + (vw >> 4)) * 64 + lane) * 16u));
+  } else {
+    f.u = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   const auto rd = buf_rsrc(ws_dcy + ch_head * kChunk, kChunk * 4);
   f.dcy = __builtin_bit_cast(f32x4, buf_load16(rd, static_cast<uint32_t>(16 * wave + q4) * 4u));
   f.eg = buf_load_f32(ws_eg + ch_head);
@@ -821,12 +839,18 @@ __device__ __forceinline__ void load_wy_frag(WyFrag &f, int c, int h, const Head
 // Everything a chunk needs that does not depend on the state (w, K^T, u,
 // decay factors) is prefetched into registers two chunks ahead, so the
 // serial chain per chunk is two LDS exchanges, two barriers and the MFMAs.
+//
+// MAP: the linear part of the map over the chunks instead of the state --
+// rows v0..v0+15 of the identity as the start, u = 0 (no u loads), no v_new
+// stores; ht then receives M over the chunks before c (rows j = v0..v0+15 of
+// [j][k]) at chunk index c - ht_c0.
 constexpr int kStateWyLds = 2 * 16 * kStrideK * 2 + 2 * 16 * kStrideT * 2;
+template <bool MAP>
 __device__ __forceinline__ void wy_state(
     char *smem, int c0, int nch, int h, int v0, int wave, int lane, size_t sbase,
     const float *state, float *new_state, const float *ws_dcy, const float *ws_eg,
     const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt, uint16_t *ws_ht,
-    uint16_t *ws_vnt, const Heads &H) {
+    uint16_t *ws_vnt, const Heads &H, int ht_c0) {
   const int ct = 0;  // one 16-column tile per workgroup
   const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
   const int lc = 16 * ct;
@@ -840,16 +864,20 @@ __device__ __forceinline__ void wy_state(
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
     const int kr = 16 * (2 * wave + mi) + q4, vc = vw + r16;
-    if (state != nullptr && nch > 0)
+    if constexpr (MAP) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[mi][r] = vc == kr + r ? 1.f : 0.f;
+    } else if (state != nullptr && nch > 0) {
       S[mi] = *reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + kr);
-    else
+    } else {
       S[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   }
 
   // One chunk of the recurrence, from the prefetched fragments f.
   auto step = [&](const WyFrag &f, int c) {
     const size_t ch_head = static_cast<size_t>(c) * H.v + h;
-    uint16_t *ht = ws_ht + ch_head * (kDV * kDK);
+    uint16_t *ht = ws_ht + (static_cast<size_t>(c - ht_c0) * H.v + h) * (kDV * kDK);
     uint16_t *vnt = ws_vnt + ch_head * (kDV * kChunk);
     // (a) chunk-start state: split copy into LDS ([v][k]) for w S, and a bf16
     //     copy ([v][k]) for the output kernel.
@@ -895,7 +923,7 @@ __device__ __forceinline__ void wy_state(
       split2(vs[2], vs[3], h1, l1);
       const u32x2 hi = {h0, h1}, lo = {l0, l1};
       const int i0 = 16 * wave + q4;
-      *reinterpret_cast<u32x2 *>(vnt + (vw + r16) * kChunk + i0) = rn;
+      if constexpr (!MAP) *reinterpret_cast<u32x2 *>(vnt + (vw + r16) * kChunk + i0) = rn;
       *reinterpret_cast<u32x2 *>(&sVh[vl * kStrideT + i0]) = hi;
       *reinterpret_cast<u32x2 *>(&sVl[vl * kStrideT + i0]) = lo;
     }
@@ -934,7 +962,7 @@ __device__ __forceinline__ void wy_state(
     auto chunk_at = [&](int i) { return c0 + (i < nch ? i : nch - 1); };
     WyFrag fa, fb, fc;
 #define GDN_LOAD(F, I) \
-    load_wy_frag(F, chunk_at(I), h, H, vw, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt)
+    load_wy_frag<!MAP>(F, chunk_at(I), h, H, vw, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt)
     GDN_LOAD(fa, 0);
     GDN_LOAD(fb, 1);
     GDN_LOAD(fc, 2);
@@ -1215,12 +1243,27 @@ __device__ __forceinline__ void t_state(
 // per chunk (WY ~52 KB: w, K^T, u; T ~35 KB: K, T, V), from L2 at 400-750
 // cycles latency with a bounded number of misses in flight per CU, and the
 // serial chain of exchanges (two in the WY form, three in the T form).
+//
+// Two-segment scan (one sequence, WY form, sp.nt0 > 0).  Each chunk maps the
+// state affinely, S -> S M_c + C_c, so the chunks [nt0, nt) need not wait for
+// the state at nt0: beside the chain over [0, nt0) (from the initial state,
+// ending in sp.send), the chunks [nt0, nt) run from a zero state (their ht
+// and v_new are then the offsets; the end is sp.cend) and from the identity
+// (MAP: the linear parts M into sp.htm; the end is sp.mend).  The three
+// groups of 8 workgroups per head run side by side, s = 0, 1, 2 below, so the
+// serial chain is half as long; prefill_split_fix_kernel then combines them.
 // ---------------------------------------------------------------------------
+struct SplitScan {
+  int nt0;        // first chunk of the second segment; 0 = one chain
+  uint16_t *htm;  // [nt - nt0][H.v][128 j][128 k] bf16
+  float *send, *cend, *mend;  // [H.v][128][128] f32 each
+};
+
 __global__ __launch_bounds__(256) void prefill_state_kernel(
     const uint16_t *k, const uint16_t *v, const float *state, float *new_state,
     const int4 *chunks, const int *offsets, const float *ws_dcy, const float *ws_eg,
     const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt, uint16_t *ws_ht,
-    uint16_t *ws_vnt, int N, int single_T, Heads H, int form) {
+    uint16_t *ws_vnt, int N, int single_T, Heads H, int form, SplitScan sp) {
   __shared__ __align__(16) char smem[kStateWyLds > kStateTLds ? kStateWyLds : kStateTLds];
   constexpr int NVB = kDV / 16;
   const int h = blockIdx.x % H.v;
@@ -1231,13 +1274,29 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
 
   // This workgroup's chunks: c0 .. c0 + nch - 1.
   int c0 = 0, nch = (single_T + kChunk - 1) / kChunk;
-  if (single_T < 0) {
+  size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;  // [V][K]
+  if (sp.nt0 > 0) {  // two-segment scan of one sequence (single_T >= 0, WY form)
+    sbase = static_cast<size_t>(h) * kDV * kDK;
+    if (s == 2) {
+      wy_state<true>(smem, sp.nt0, nch - sp.nt0, h, vb * 16, wave, lane, sbase, nullptr, sp.mend,
+                     ws_dcy, ws_eg, ws_w, ws_u, ws_kt, sp.htm, ws_vnt, H, sp.nt0);
+      return;
+    }
+    if (s == 0) {
+      nch = sp.nt0;
+      new_state = sp.send;
+    } else {
+      c0 = sp.nt0;
+      nch -= sp.nt0;
+      state = nullptr;
+      new_state = sp.cend;
+    }
+  } else if (single_T < 0) {
     if (offsets[N + 1]) return;  // the token-sequential kernel owns the batch
     if (form < 0) form = offsets[N + 2];
     c0 = offsets[s];
     nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
   }
-  const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;  // [V][K]
   if (form == 1) {
     // the T form reads K and V itself: the sequence's tokens [bos, eos)
     int bos = 0, eos = single_T;
@@ -1250,8 +1309,191 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
             ws_eg, ws_w, ws_u, ws_ht, ws_vnt, H);
   }
   else
-    wy_state(smem, c0, nch, h, vb * 16, wave, lane, sbase, state, new_state, ws_dcy, ws_eg, ws_w,
-             ws_u, ws_kt, ws_ht, ws_vnt, H);
+    wy_state<false>(smem, c0, nch, h, vb * 16, wave, lane, sbase, state, new_state, ws_dcy, ws_eg,
+                    ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0);
+}
+
+// ---------------------------------------------------------------------------
+// 3b. two-segment scan, combination (after the state kernel).  With S0 =
+// sp.send (the state at chunk nt0) and, for a chunk c >= nt0, M_c = sp.htm
+// (the linear part of the map over chunks nt0..c-1, bf16 [j][k]) and C_c = ht
+// (its offset, bf16 [v][k]), the chunk-start state is S_c = S0 M_c + C_c.
+// Workgroups [0, (nt - nt0) H.v): chunk c = nt0 + id / H.v, head h = id % H.v
+// (a head's workgroups share an XCD and read S0 from its L2):
+//   S_c   = S0 M_c + C_c   (S0 split into bf16 hi + lo, M_c bf16) -> ht
+//   v_new = u - w S_c      (w and S_c split: three products)      -> vnt
+// so the output kernel reads what one chain would have left, to the bf16
+// rounding of M_c and C_c (a relative 2^-9 of S0 M_c and C_c, the same order
+// as the bf16 ht itself).  The 16 H.v workgroups after them: 8 rows each of
+// new_state = S0 M + C in f32 FMAs (M = sp.mend, C = sp.cend).
+// ---------------------------------------------------------------------------
+constexpr int kFixRows = 8;  // new_state rows per combination workgroup
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_split_fix_kernel(int nt, Heads H, SplitScan sp, const uint16_t *__restrict__ ws_w,
+                              const float *__restrict__ ws_u, uint16_t *ws_ht,
+                              uint16_t *__restrict__ ws_vnt, float *__restrict__ new_state) {
+  // Phase 1: M_c in [0, kDV * kStrideK); phase 2: S_c hi there, lo after it.
+  __shared__ __align__(16) uint16_t smem[2 * kDV * kStrideK];
+  constexpr size_t kElems = static_cast<size_t>(kDV) * kDK;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ncorr = (nt - sp.nt0) * H.v;
+  const int id = blockIdx.x;
+
+  if (id >= ncorr) {
+    // new_state rows v0..v0+7 of head h: the rows of S0 in LDS, M streamed;
+    // thread t owns column k = t & 127 of rows v0 + 4 (t >> 7) .. +3.
+    const int f = id - ncorr;
+    const int h = f % H.v, vb = f / H.v;
+    if (vb >= kDV / kFixRows) return;
+    const int v0 = kFixRows * vb;
+    float *sS0 = reinterpret_cast<float *>(smem);  // [kFixRows][kDK]
+    const float *S0 = sp.send + h * kElems + static_cast<size_t>(v0) * kDK;
+    for (int i = tid; i < kFixRows * kDK / 4; i += 256)
+      reinterpret_cast<f32x4 *>(sS0)[i] = reinterpret_cast<const f32x4 *>(S0)[i];
+    __syncthreads();
+    const int k = tid & 127, i0 = 4 * (tid >> 7);
+    const float *M = sp.mend + h * kElems + k;
+    const float *C = sp.cend + h * kElems + static_cast<size_t>(v0 + i0) * kDK + k;
+    float acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = C[i * kDK];
+#pragma unroll 4
+    for (int j = 0; j < kDK; j += 4) {
+      float m[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) m[jj] = M[(j + jj) * kDK];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 sv = *reinterpret_cast<const f32x4 *>(&sS0[(i0 + i) * kDK + j]);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) acc[i] = fmaf(sv[jj], m[jj], acc[i]);
+      }
+    }
+    float *dst = new_state + h * kElems + static_cast<size_t>(v0 + i0) * kDK + k;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i * kDK] = acc[i];
+    return;
+  }
+
+  const int c = sp.nt0 + id / H.v, h = id % H.v;
+  const size_t ch_head = static_cast<size_t>(c) * H.v + h;
+  const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
+  uint16_t *const sM = smem;
+  uint16_t *const sSh = smem;
+  uint16_t *const sSl = smem + kDV * kStrideK;
+  uint16_t *const ht = ws_ht + ch_head * kElems;
+  const uint16_t *const Mc = sp.htm + (static_cast<size_t>(c - sp.nt0) * H.v + h) * kElems;
+  const float *const S0 = sp.send + static_cast<size_t>(h) * kElems;
+
+  // Phase 1 has wave w produce the columns v = 32 w + 16 vi + (lane & 15),
+  // vi = 0, 1, of S_c^T[k][v] = sum_j M_c[j][k] S0[v][j] for all 128 k
+  // (tiles mi): A = M_c^T rows k (transposed LDS reads), B = S0 rows split.
+  // Loads that do not wait for M_c come first: C_c at this lane's result
+  // positions (k = 16 mi + q4 .. +3), this wave's S0 rows, the w fragments.
+  u32x2 cc[8][2];
+#pragma unroll
+  for (int mi = 0; mi < 8; ++mi)
+#pragma unroll
+    for (int vi = 0; vi < 2; ++vi)
+      cc[mi][vi] = *reinterpret_cast<const u32x2 *>(ht + (32 * wave + 16 * vi + r16) * kDK + 16 * mi + q4);
+  u32x4 bh[2][4], bl[2][4];
+#pragma unroll
+  for (int vi = 0; vi < 2; ++vi)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const float *p = S0 + (32 * wave + 16 * vi + r16) * kDK + 32 * kk + kg;
+      const f32x4 x0 = *reinterpret_cast<const f32x4 *>(p);
+      const f32x4 x1 = *reinterpret_cast<const f32x4 *>(p + 4);
+      const float xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      split8(xs, bh[vi][kk], bl[vi][kk]);
+    }
+  const auto rw = buf_rsrc(ws_w + ch_head * (kWBytes / 2), kWBytes);
+  const uint32_t wo = static_cast<uint32_t>(wave) * 8192u + static_cast<uint32_t>(lane) * 32u;
+  u32x4 wh[4], wl[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    wh[kk] = buf_load16(rw, wo + kk * 2048);
+    wl[kk] = buf_load16(rw, wo + kk * 2048 + 16);
+  }
+
+  for (int idx = tid; idx < kDV * 16; idx += 256) {
+    const int row = idx >> 4, c8 = (idx & 15) * 8;
+    *reinterpret_cast<u32x4 *>(&sM[row * kStrideK + c8]) =
+        *reinterpret_cast<const u32x4 *>(Mc + row * kDK + c8);
+  }
+  __syncthreads();
+
+  f32x4 acc[8][2];
+#pragma unroll
+  for (int mi = 0; mi < 8; ++mi) {
+    u32x4 am[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const u32x2 x = ds_read_tr16(&sM[(32 * kk + kg + 4 * hh + (r16 >> 2)) * kStrideK +
+                                         16 * mi + 4 * (r16 & 3)]);
+        am[kk][2 * hh] = x[0];
+        am[kk][2 * hh + 1] = x[1];
+      }
+#pragma unroll
+    for (int vi = 0; vi < 2; ++vi) {
+      f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        a = mfma_bf16(am[kk], bh[vi][kk], a);
+        a = mfma_bf16(am[kk], bl[vi][kk], a);
+      }
+      acc[mi][vi] = a;
+    }
+  }
+  __syncthreads();  // every wave is done with M_c: S_c takes its place
+
+  // S_c = product + C_c -> ht (bf16) and LDS (split, [v][k]).
+#pragma unroll
+  for (int mi = 0; mi < 8; ++mi)
+#pragma unroll
+    for (int vi = 0; vi < 2; ++vi) {
+      const int k0 = 16 * mi + q4, v = 32 * wave + 16 * vi + r16;
+      f32x4 sc;
+      sc[0] = acc[mi][vi][0] + __uint_as_float(cc[mi][vi][0] << 16);
+      sc[1] = acc[mi][vi][1] + __uint_as_float(cc[mi][vi][0] & 0xffff0000u);
+      sc[2] = acc[mi][vi][2] + __uint_as_float(cc[mi][vi][1] << 16);
+      sc[3] = acc[mi][vi][3] + __uint_as_float(cc[mi][vi][1] & 0xffff0000u);
+      *reinterpret_cast<u32x2 *>(ht + v * kDK + k0) =
+          u32x2{pk_bf16(sc[0], sc[1]), pk_bf16(sc[2], sc[3])};
+      u32x2 hi, lo;
+      split4(sc, hi, lo);
+      *reinterpret_cast<u32x2 *>(&sSh[v * kStrideK + k0]) = hi;
+      *reinterpret_cast<u32x2 *>(&sSl[v * kStrideK + k0]) = lo;
+    }
+  __syncthreads();
+
+  // Phase 2: v_new = u - w S_c for tokens 16 wave..+15, all 128 columns.
+  const auto ru = buf_rsrc(ws_u + ch_head * (kUBytes / 4), kUBytes);
+  f32x4 uf[8];
+#pragma unroll
+  for (int vt = 0; vt < 8; ++vt)
+    uf[vt] = __builtin_bit_cast(f32x4, buf_load16(ru, static_cast<uint32_t>((wave * 8 + vt) * 64 + lane) * 16u));
+  uint16_t *const vnt = ws_vnt + ch_head * (kDV * kChunk);
+#pragma unroll
+  for (int vt = 0; vt < 8; ++vt) {
+    f32x4 P0 = {0.f, 0.f, 0.f, 0.f}, P1 = P0, P2 = P0;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 sh = *reinterpret_cast<const u32x4 *>(&sSh[(16 * vt + r16) * kStrideK + 32 * kk + kg]);
+      const u32x4 sl = *reinterpret_cast<const u32x4 *>(&sSl[(16 * vt + r16) * kStrideK + 32 * kk + kg]);
+      P0 = mfma_bf16(wh[kk], sh, P0);
+      P1 = mfma_bf16(wh[kk], sl, P1);
+      P2 = mfma_bf16(wl[kk], sh, P2);
+    }
+    float vn[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vn[r] = uf[vt][r] - ((P0[r] + P1[r]) + P2[r]);
+    *reinterpret_cast<u32x2 *>(vnt + (16 * vt + r16) * kChunk + 16 * wave + q4) =
+        u32x2{pk_bf16(vn[0], vn[1]), pk_bf16(vn[2], vn[3])};
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1386,6 +1628,12 @@ void prefill_output_kernel(
 constexpr int kRecurrentMaxLen = 96;
 constexpr int kCandidateMeanLen = 32;
 
+// Two-segment scan of one sequence (state kernel, SplitScan): three groups of
+// 8 workgroups per v-head, one per CU, so it needs 24 H.v <= 256; the built-in
+// choice takes it from kSplitMinChunks chunks on.  Variants: 0 / -1 built in,
+// 2 never (one chain), 3 always (one sequence of at least two chunks).
+constexpr int kSplitMinChunks = 16;
+
 static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                           const float *state, const float *A_log, const gdn_bf16 *a,
                           const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
@@ -1409,7 +1657,9 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: state/new_state must be 16-byte aligned");
   if (!aligned(cu_seqlens, cu64 ? 8 : 4))
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: cu_seqlens misaligned");
-  if (variant < -1 || variant > 1) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown variant %d (0 WY form, 1 T form)", variant);
+  if (variant < -1 || variant > 3)
+    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown variant %d (0 WY form, 1 T form, 2 WY one "
+                "chain, 3 WY two segments)", variant);
   if (rec_max < -2) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: recurrent_max_len %d < -2", rec_max);
   if (rec_variant < -1 || rec_variant >= recurrent_num_variants())
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown recurrent tiling %d", rec_variant);
@@ -1490,7 +1740,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   // one or two sequences, fewer than 128 chunks, or fewer than three times
   // the chunks of the mean length, a lower bound on the longest -- so that
   // only one intra kernel is launched.
-  int form = variant;
+  int form = variant >= 2 ? 0 : variant;
   if (form < 0) {
     const long long mean_chunks = ((static_cast<long long>(T) + N - 1) / N + kChunk - 1) / kChunk;
     const bool t_possible = single_T < 0 && N > 2 && L.nt_max >= 128 && L.nt_max >= 3 * mean_chunks;
@@ -1523,12 +1773,27 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
       if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
     }
   }
-  const long long blocks = static_cast<long long>(N) * H.v * (kDV / 16);
+  SplitScan sp{0, nullptr, nullptr, nullptr, nullptr};
+  if (single_T >= 0 && form == 0 && variant != 2 && L.nt_max >= 2 && 24 * H.v <= 256 &&
+      (variant == 3 || L.nt_max >= kSplitMinChunks)) {
+    sp.nt0 = split_first(L.nt_max);
+    sp.htm = reinterpret_cast<uint16_t *>(ws + L.htm);
+    sp.send = reinterpret_cast<float *>(ws + L.send);
+    sp.cend = reinterpret_cast<float *>(ws + L.cend);
+    sp.mend = reinterpret_cast<float *>(ws + L.mend);
+  }
+  const long long blocks = static_cast<long long>(sp.nt0 > 0 ? 3 : N) * H.v * (kDV / 16);
   if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
   hipLaunchKernelGGL(prefill_state_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                      k, v, state, new_state, chunks, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N,
-                     single_T, H, form);
+                     single_T, H, form, sp);
   if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
+  if (sp.nt0 > 0) {
+    const unsigned fix_grid = static_cast<unsigned>((L.nt_max - sp.nt0) * H.v + (kDV / kFixRows) * H.v);
+    hipLaunchKernelGGL(prefill_split_fix_kernel, dim3(fix_grid), dim3(256), 0, stream, L.nt_max, H,
+                       sp, wsw, wsu, ht, vnt, new_state);
+    if ((rc = check_launch("gdn_prefill_fwd(split)"))) return rc;
+  }
   if (L.nt_max > 0) {
     hipLaunchKernelGGL(prefill_output_kernel, dim3(grid), dim3(256), 0, stream, q, k, chunks,
                        single_T, L.nt_max, H, wsG, ht, vnt, scale, output);

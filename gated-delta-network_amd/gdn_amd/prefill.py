@@ -118,7 +118,9 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
     on the device (0 = cu[0] <= ... <= cu[N] = T); scale float, 0-d tensor or
     None; output [T,8,128] bf16; new_state [N,8,128,128] f32 (may be state).
     ``variant`` picks the form of the per-chunk operands
-    (gdn_prefill_fwd_variant): 0 WY, 1 T, -1 the built-in choice.  ``workspace``: a caller-owned uint8
+    (gdn_prefill_fwd_variant): 0 WY, 1 T, -1 the built-in choice; 2 WY with
+    one serial chain per sequence, 3 WY with the two-segment scan of a single
+    sequence (0 and -1 take it from 16 chunks on).  ``workspace``: a caller-owned uint8
     buffer (``alloc_workspace``) used instead of the per-stream cache.
     ``recurrent_max_len``: a batch whose longest sequence has at most this
     many tokens runs token by token instead of through the chunks (-1

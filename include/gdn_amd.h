@@ -172,7 +172,13 @@ int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
  * traffic, one more exchange per step), -1 = the built-in choice (what
  * gdn_prefill_fwd uses: the T form for batches of at least 128 chunks with at
  * least three times the chunks of their longest sequence, decided on the
- * device; the WY form otherwise and for one sequence).  The counterpart of
+ * device; the WY form otherwise and for one sequence), 2 = WY form with one
+ * serial chain of state steps per sequence, 3 = WY form with the two-segment
+ * scan for a single sequence of at least two chunks (the second half of the
+ * chunks runs beside the first from a zero state and from the identity, and
+ * one more launch applies the first half's final state: half the serial
+ * chain; 0 and -1 take it from 16 chunks on when 24 x num_v_heads <= 256).
+ * The counterpart of
  * the reference's autotuned launch parameters of
  * chunk_gated_delta_rule_fwd_kernel_h (solutions/
  * gdn_prefill_qk4_v8_d128_k_last/solution/triton/fla_kernels.py:407-426,

@@ -4,7 +4,7 @@
  * Restates the per-token loop of reference/gdn_prefill_ref.py:71-89 (same op
  * order: old = g*S; old_v = k @ old; new_v = beta*v + (1-beta)*old_v;
  * S = old - k (x) old_v + k (x) new_v; o = scale * q @ S) so that the oracle
- * reaches the full BASELINE sizes (up to 4 x 8192 tokens) in seconds.  The
+ * reaches the full benchmark sizes (up to 4 x 8192 tokens) in seconds.  The
  * gating (g, beta) is computed by the numpy oracle and passed in, so this file
  * holds only the recurrence.  Every (sequence, v-head) pair is independent and
  * runs on its own OpenMP thread.

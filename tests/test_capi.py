@@ -102,9 +102,10 @@ def test_prefill_workspace_bytes():
     small = lib.gdn_prefill_workspace_bytes(64, 1)
     big = lib.gdn_prefill_workspace_bytes(8192, 1)
     assert 0 < small < big
-    # bounded by the chunk count alone: 1x8192 -> 128 chunks
-    assert big < 128 * 2 ** 20
-    assert lib.gdn_prefill_workspace_bytes(8192, 4) > big
+    # bounded by the chunk count alone: 1x8192 -> 128 chunks (~120 MiB of
+    # per-chunk operands, plus 17.5 MiB for the two-segment scan of one sequence)
+    assert big < 144 * 2 ** 20
+    assert lib.gdn_prefill_workspace_bytes(8192, 4) > lib.gdn_prefill_workspace_bytes(8192, 2)
 
 
 @pytest.mark.parametrize("over, needle, code", [
@@ -165,7 +166,8 @@ def test_decode_multi_zero_batch_is_a_no_op():
 @pytest.mark.parametrize("tuning, needle", [
     ((-1, -3, -1), "recurrent_max_len"),
     ((-1, -1, 10), "recurrent tiling"),
-    ((2, -1, -1), "variant"),
+    ((4, -1, -1), "variant"),
+    ((-2, -1, -1), "variant"),
 ])
 def test_prefill_tuned_rejects_bad_tuning(tuning, needle):
     lib = _lib.load()

@@ -366,6 +366,12 @@ def _layout(T, N):
     take("kt", nt * 4 * 128 * 64 * 2)
     take("ht", nt * 8 * 128 * 128 * 2)
     take("vnt", nt * 8 * 128 * 64 * 2)
+    n1 = nt - (nt + 1) // 2 if N == 1 else 0   # chunks of the second segment
+    one = 1 if N == 1 else 0
+    take("htm", n1 * 8 * 128 * 128 * 2)
+    take("send", one * 8 * 128 * 128 * 4)
+    take("cend", one * 8 * 128 * 128 * 4)
+    take("mend", one * 8 * 128 * 128 * 4)
     L["total"] = off
     return L
 
@@ -454,3 +460,104 @@ def test_prefill_stage_intermediates(cuda_device, form):
 def _stream(dev):
     from gdn_amd._common import stream_of
     return stream_of(dev)
+
+
+# Two-segment scan of one sequence (gdn_prefill.hip, SplitScan): the second
+# half of the chunks runs beside the first from a zero state and from the
+# identity, and a combination kernel applies the first half's final state.
+# variant 3 forces it (one sequence of >= 2 chunks), 2 forbids it; the built-in
+# choice takes it from 16 chunks on.
+SPLIT, CHAIN = 3, 2
+
+
+@pytest.mark.parametrize("L, with_state, slow", [
+    (65, True, ()), (128, False, ()), (129, True, (6, 7)), (1000, True, (6, 7)),
+    (4095, False, (0, 7)), (8192, True, (6, 7))])
+def test_prefill_two_segment_scan(cuda_device, L, with_state, slow):
+    print(f"prefill two-segment scan L={L} state={with_state} slow={slow}", flush=True)
+    inp = O.make_prefill_inputs([L], seed=400 + L % 97, with_state=with_state,
+                                slow_decay_heads=slow)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    d = to_dev(inp, cuda_device)
+    res = {}
+    for var in (SPLIT, CHAIN):
+        res[var] = run_gpu(d, cuda_device, variant=var, route="chunked")
+        check(*res[var], o_ref, s_ref)
+    if with_state:  # in place last: it overwrites d["state"]
+        oi, si = run_gpu(d, cuda_device, in_place=True, variant=SPLIT, route="chunked")
+        assert np.array_equal(oi, res[SPLIT][0]) and np.array_equal(si, res[SPLIT][1])
+
+
+@pytest.mark.parametrize("L, expect", [(512, CHAIN), (1024, SPLIT), (8192, SPLIT)])
+def test_prefill_two_segment_built_in_choice(cuda_device, L, expect):
+    print(f"prefill two-segment choice L={L} expect variant {expect}", flush=True)
+    inp = O.make_prefill_inputs([L], seed=41, with_state=True)
+    d = to_dev(inp, cuda_device)
+    o_a, s_a = run_gpu(d, cuda_device, variant=-1, route="chunked")
+    o_e, s_e = run_gpu(d, cuda_device, variant=expect, route="chunked")
+    assert np.array_equal(o_a, o_e) and np.array_equal(s_a, s_e)
+
+
+def test_prefill_two_segment_extreme_gates(cuda_device):
+    # The gates of test_prefill_forms_extreme_gates on one 1000-token sequence.
+    T = 1000
+    inp = O.make_prefill_inputs([T], seed=42)
+    rng = np.random.default_rng(42)
+    a_h = np.array([30.0, -30.0, 20.0, 0.0, 19.5, -5.0, 5.0, 1.0], np.float32)
+    b_h = np.array([-40.0, 40.0, 0.0, 8.0, -8.0, 1.0, -1.0, 0.0], np.float32)
+    inp["a"][:] = O.bf16_round(a_h[None, :] + rng.normal(0, 0.5, (T, 8)).astype(np.float32))
+    inp["b"][:] = O.bf16_round(b_h[None, :] + rng.normal(0, 0.5, (T, 8)).astype(np.float32))
+    inp["A_log"][:] = np.array([-10.0, 2.7, 0.0, -20.0, 1.0, 0.5, 0.1, 2.0], np.float32)
+    print("prefill two-segment scan, extreme gates", flush=True)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, variant=SPLIT, route="chunked")
+    assert np.isfinite(o).all() and np.isfinite(s).all()
+    check(o, s, o_ref, s_ref)
+
+
+@pytest.mark.parametrize("heads", [(1, 1), (2, 8), (8, 8)])
+def test_prefill_two_segment_heads(cuda_device, heads):
+    from gdn_amd import prefill
+    hqk, hv = heads
+    L = 1500
+    print(f"prefill two-segment scan heads={heads} L={L}", flush=True)
+    inp = O.make_prefill_inputs([L], seed=43, heads=heads)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    d = to_dev(inp, cuda_device)
+    for var in (SPLIT, CHAIN):
+        out = torch.empty((L, hv, 128), dtype=torch.bfloat16, device=cuda_device)
+        ns = torch.empty((1, hv, 128, 128), dtype=torch.float32, device=cuda_device)
+        prefill.kernel(d["q"], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"],
+                       d["b"], d["cu_seqlens"], d["scale"], out, ns, variant=var,
+                       recurrent_max_len=-2)
+        torch.cuda.synchronize()
+        check(out.float().cpu().numpy(), ns.cpu().numpy(), o_ref, s_ref)
+
+
+def test_prefill_two_segment_stage_intermediates(cuda_device):
+    # After the combination kernel the workspace holds what one chain leaves:
+    # every chunk's start state (ht) and v_new (vnt), and the first
+    # segment's final state (send) is the state at chunk nt0.
+    from gdn_amd import prefill
+    L = 300  # 5 chunks: nt0 = 3, the last one partial
+    inp = O.make_prefill_inputs([L], seed=44)
+    lay = _layout(L, 1)
+    assert prefill.workspace_bytes(L, 1) == lay["total"]
+    run_gpu(to_dev(inp, cuda_device), cuda_device, variant=SPLIT, route="chunked")
+    ws = prefill._workspace(cuda_device, _stream(cuda_device), 0).cpu().numpy()
+    _, _, it = O.prefill_chunked(**inp, return_intermediates=True)
+    nt, nt0 = 5, 3
+
+    def arr(name, dtype, shape):
+        n = int(np.prod(shape))
+        return np.frombuffer(ws[lay[name]:lay[name] + n * np.dtype(dtype).itemsize].tobytes(),
+                             dtype=dtype).reshape(shape)
+
+    ht = O.bf16_from_bits(arr("ht", np.uint16, (nt, 8, 128, 128)))
+    h_ref = it["h"].transpose(0, 1, 3, 2)
+    assert np.abs(ht - h_ref).max() <= 1e-2 * np.abs(h_ref).max()
+    vnt = O.bf16_from_bits(arr("vnt", np.uint16, (nt, 8, 128, 64)))
+    vn_ref = it["v_new"].transpose(0, 1, 3, 2)
+    assert np.abs(vnt - vn_ref).max() <= 1e-2 * np.abs(vn_ref).max()
+    send = arr("send", np.float32, (8, 128, 128))
+    assert np.abs(send - h_ref[nt0]).max() <= 1e-4 * np.abs(h_ref[nt0]).max()
