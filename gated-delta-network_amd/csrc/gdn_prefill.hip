@@ -235,8 +235,51 @@ __device__ __forceinline__ int4 chunk_info(const int4 *chunks, int c, int single
     const int start = c * kChunk, rest = single_T - start;
     return rest > 0 ? make_int4(0, start, rest < kChunk ? rest : kChunk, c) : make_int4(-1, 0, 0, 0);
   }
-  return chunks[c];
+  // the same entry in every lane: keep it in SGPRs (buffer descriptors built
+  // from it are then uniform, with no per-lane loop around each load)
+  const int4 e = chunks[c];
+  return make_int4(__builtin_amdgcn_readfirstlane(e.x), __builtin_amdgcn_readfirstlane(e.y),
+                   __builtin_amdgcn_readfirstlane(e.z), __builtin_amdgcn_readfirstlane(e.w));
 }
+
+// Buffer descriptor (gfx9 word 3 = 0x00020000: raw 32-bit records) over
+// `bytes` bytes at a wave-uniform base.  Loads through it take the base in
+// SGPRs and a 32-bit per-lane byte offset that never changes across chunks,
+// so a prefetch loop needs no address registers: with 64-bit VGPR addresses
+// the compiler recomputed them every chunk and, reusing registers of loads
+// still in flight, had to wait for the newest prefetch set at the loop head.
+// A load at or past `bytes` returns zero: the rows past the end of a chunk.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+// One float at a wave-uniform address, as a vector load issued in program
+// order with the fragments it belongs to.
+__device__ __forceinline__ float buf_load_f32(const float *p) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(p, 4), 0u, 0, 0));
+}
+
+// Gating of token `lane` of a chunk of `len` tokens from `start` (v-head h):
+// g = log decay, beta = sigmoid(b); both loads go through descriptors bounded
+// at the chunk's end and are issued before any arithmetic; padding tokens
+// (lane >= len) get g = beta = 0.
+__device__ __forceinline__ void chunk_gates(int lane, int start, int len, int h, const Heads &H,
+                                            const float *A_log, const uint16_t *a,
+                                            const float *dt_bias, const uint16_t *b, float &gl,
+                                            float &be) {
+  const size_t base = static_cast<size_t>(start) * H.v + h;
+  const uint32_t bytes = static_cast<uint32_t>(len) * static_cast<uint32_t>(H.v) * 2u;
+  const uint32_t off = static_cast<uint32_t>(lane) * static_cast<uint32_t>(H.v) * 2u;
+  const uint16_t ar = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(a + base, bytes), off, 0, 0);
+  const uint16_t br = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(b + base, bytes), off, 0, 0);
+  const float al = A_log[h], db = dt_bias[h];
+  gl = lane < len ? gdn_log_decay(al, bf16_to_f32(ar), db) : 0.f;
+  be = lane < len ? sigmoidf_(bf16_to_f32(br)) : 0.f;
+}
+
 
 // Workgroup id -> (chunk c, v-head h) for the per-(chunk, head) kernels, so
 // that the `ratio` v-heads reading one q/k head of one chunk are dispatched
@@ -354,12 +397,8 @@ __device__ __forceinline__ void wy_intra(
   // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding tokens
   // get g = 0 and beta = 0, so G stays at G_last past the end of the chunk.
   if (wave == 0) {
-    float gl = 0.f, be = 0.f;
-    if (lane < len) {
-      const size_t t = static_cast<size_t>(start) + lane;
-      gl = gdn_log_decay(A_log[h], bf16_to_f32(a[t * H.v + h]), dt_bias[h]);
-      be = sigmoidf_(bf16_to_f32(b[t * H.v + h]));
-    }
+    float gl, be;
+    chunk_gates(lane, start, len, h, H, A_log, a, dt_bias, b, gl, be);
     float G = gl;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -378,18 +417,19 @@ __device__ __forceinline__ void wy_intra(
   // One 8x8 block of K (threads 0..127) or V (128..255) per thread, loaded
   // now; K goes to LDS (row-major and transposed) at once, V's transpose waits
   // in registers until A is built (it reuses the K tile's space).
-  const bool isK = tid < 128;
+  const bool isK = __builtin_amdgcn_readfirstlane(wave) < 2;  // wave-uniform (SGPR)
   const int blk = tid & 127, rb = blk >> 4, cb = blk & 15;
+  // (rows past the chunk read zero through the descriptor's range)
   u32x4 rows[8];
+  {
+    const int nh = isK ? H.qk : H.v;
+    const uint16_t *src = isK ? k + (static_cast<size_t>(start) * H.qk + hq) * kDK
+                              : v + (static_cast<size_t>(start) * H.v + h) * kDV;
+    const uint32_t rstride = static_cast<uint32_t>(nh) * (kDK * 2);
+    const auto rs = buf_rsrc(src, static_cast<uint32_t>(len) * rstride);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = rb * 8 + i;
-    rows[i] = u32x4{0u, 0u, 0u, 0u};
-    if (row < len) {
-      const size_t t = static_cast<size_t>(start) + row;
-      rows[i] = isK ? *reinterpret_cast<const u32x4 *>(k + (t * H.qk + hq) * kDK + cb * 8)
-                    : *reinterpret_cast<const u32x4 *>(v + (t * H.v + h) * kDV + cb * 8);
-    }
+    for (int i = 0; i < 8; ++i)
+      rows[i] = buf_load16(rs, static_cast<uint32_t>(rb * 8 + i) * rstride + cb * 16);
   }
   // Column j of the block = 8 tokens of feature cb*8 + j, into transposed LDS.
   auto transpose_into = [&](uint16_t *dstT, bool kt_frags) {
@@ -587,12 +627,8 @@ __device__ __forceinline__ void t_intra(
   // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding tokens
   // get g = 0 and beta = 0, so G stays at G_last past the end of the chunk.
   if (wave == 0) {
-    float gl = 0.f, be = 0.f;
-    if (lane < len) {
-      const size_t t = static_cast<size_t>(start) + lane;
-      gl = gdn_log_decay(A_log[h], bf16_to_f32(a[t * H.v + h]), dt_bias[h]);
-      be = sigmoidf_(bf16_to_f32(b[t * H.v + h]));
-    }
+    float gl, be;
+    chunk_gates(lane, start, len, h, H, A_log, a, dt_bias, b, gl, be);
     float G = gl;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -610,14 +646,23 @@ __device__ __forceinline__ void t_intra(
     if (lane == 0) ws_eg[ch_head] = expf(G_last);
   }
 
-  // K row-major into LDS (rows past the chunk are zero).
+  // K row-major into LDS (rows past the chunk read zero through the
+  // descriptor's range); every load issued before the LDS stores.
+  {
+    const uint32_t rstride = static_cast<uint32_t>(H.qk) * (kDK * 2);
+    const auto rs = buf_rsrc(k + (static_cast<size_t>(start) * H.qk + hq) * kDK,
+                             static_cast<uint32_t>(len) * rstride);
+    u32x4 kv[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = tid + 256 * i, row = idx >> 4, c8 = (idx & 15) * 8;
-    u32x4 kv = {0u, 0u, 0u, 0u};
-    if (row < len)
-      kv = *reinterpret_cast<const u32x4 *>(k + ((static_cast<size_t>(start) + row) * H.qk + hq) * kDK + c8);
-    *reinterpret_cast<u32x4 *>(&sK[row * kStrideK + c8]) = kv;
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      kv[i] = buf_load16(rs, static_cast<uint32_t>(idx >> 4) * rstride + (idx & 15) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      *reinterpret_cast<u32x4 *>(&sK[(idx >> 4) * kStrideK + (idx & 15) * 8]) = kv[i];
+    }
   }
   __syncthreads();
 
@@ -768,26 +813,6 @@ __global__ __launch_bounds__(256) void prefill_intra_t_kernel(
 // ---------------------------------------------------------------------------
 // 3. state recurrence: the two forms of a step, then the kernel.
 // ---------------------------------------------------------------------------
-// Buffer descriptor (gfx9 word 3 = 0x00020000: raw 32-bit records) over
-// `bytes` bytes at a wave-uniform base.  Loads through it take the base in
-// SGPRs and a 32-bit per-lane byte offset that never changes across chunks,
-// so a prefetch loop needs no address registers: with 64-bit VGPR addresses
-// the compiler recomputed them every chunk and, reusing registers of loads
-// still in flight, had to wait for the newest prefetch set at the loop head.
-// A load at or past `bytes` returns zero: the rows past the end of a chunk.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), bytes,
-                                           0x00020000);
-}
-__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
-}
-// One float at a wave-uniform address, as a vector load issued in program
-// order with the fragments it belongs to.
-__device__ __forceinline__ float buf_load_f32(const float *p) {
-  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(p, 4), 0u, 0, 0));
-}
-
 constexpr uint32_t kWBytes = kChunk * kDK * 4;    // w of one (chunk, head): hi + lo bf16
 constexpr uint32_t kKtBytes = kDK * kChunk * 2;   // K^T of one (chunk, q/k head)
 constexpr uint32_t kUBytes = kChunk * kDV * 4;    // u of one (chunk, head), f32
@@ -1318,14 +1343,16 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
 // sp.send (the state at chunk nt0) and, for a chunk c >= nt0, M_c = sp.htm
 // (the linear part of the map over chunks nt0..c-1, bf16 [j][k]) and C_c = ht
 // (its offset, bf16 [v][k]), the chunk-start state is S_c = S0 M_c + C_c.
-// Workgroups [0, (nt - nt0) H.v): chunk c = nt0 + id / H.v, head h = id % H.v
-// (a head's workgroups share an XCD and read S0 from its L2):
+// Workgroups id = [0, (nt - nt0) H.v) after those of new_state: chunk c =
+// nt0 + id / H.v, head h = id % H.v (a head's workgroups share an XCD and
+// read S0 from its L2):
 //   S_c   = S0 M_c + C_c   (S0 split into bf16 hi + lo, M_c bf16) -> ht
 //   v_new = u - w S_c      (w and S_c split: three products)      -> vnt
 // so the output kernel reads what one chain would have left, to the bf16
 // rounding of M_c and C_c (a relative 2^-9 of S0 M_c and C_c, the same order
-// as the bf16 ht itself).  The 16 H.v workgroups after them: 8 rows each of
-// new_state = S0 M + C in f32 FMAs (M = sp.mend, C = sp.cend).
+// as the bf16 ht itself).  The first 16 H.v workgroups of the grid compute
+// new_state = S0 M + C instead, 8 rows each, in f32 FMAs (M = sp.mend, C =
+// sp.cend).
 // ---------------------------------------------------------------------------
 constexpr int kFixRows = 8;  // new_state rows per combination workgroup
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
@@ -1337,32 +1364,37 @@ void prefill_split_fix_kernel(int nt, Heads H, SplitScan sp, const uint16_t *__r
   constexpr size_t kElems = static_cast<size_t>(kDV) * kDK;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ncorr = (nt - sp.nt0) * H.v;
-  const int id = blockIdx.x;
+  constexpr int kFixGroups = kDV / kFixRows;
+  const int nfix = kFixGroups * H.v;
 
-  if (id >= ncorr) {
-    // new_state rows v0..v0+7 of head h: the rows of S0 in LDS, M streamed;
+  if (blockIdx.x < nfix) {
+    // new_state rows v0..v0+7 of head h (first in the grid, so that they run
+    // beside the chunk workgroups): M and the rows of S0 staged in LDS;
     // thread t owns column k = t & 127 of rows v0 + 4 (t >> 7) .. +3.
-    const int f = id - ncorr;
-    const int h = f % H.v, vb = f / H.v;
-    if (vb >= kDV / kFixRows) return;
-    const int v0 = kFixRows * vb;
-    float *sS0 = reinterpret_cast<float *>(smem);  // [kFixRows][kDK]
-    const float *S0 = sp.send + h * kElems + static_cast<size_t>(v0) * kDK;
-    for (int i = tid; i < kFixRows * kDK / 4; i += 256)
-      reinterpret_cast<f32x4 *>(sS0)[i] = reinterpret_cast<const f32x4 *>(S0)[i];
-    __syncthreads();
+    const int h = blockIdx.x % H.v, v0 = kFixRows * (blockIdx.x / H.v);
+    float *sMf = reinterpret_cast<float *>(smem);  // [kDK][kDK]
+    float *sS0 = sMf + kDK * kDK;                  // [kFixRows][kDK]
+    const f32x4 *M4 = reinterpret_cast<const f32x4 *>(sp.mend + h * kElems);
+    const f32x4 *S04 = reinterpret_cast<const f32x4 *>(sp.send + h * kElems + static_cast<size_t>(v0) * kDK);
+    // every load issued before any LDS store (one memory latency, not 16)
+    f32x4 mv[kDK * kDK / 4 / 256];
+#pragma unroll
+    for (int i = 0; i < kDK * kDK / 4 / 256; ++i) mv[i] = M4[tid + 256 * i];
+    const f32x4 sv0 = S04[tid % (kFixRows * kDK / 4)];
+#pragma unroll
+    for (int i = 0; i < kDK * kDK / 4 / 256; ++i) reinterpret_cast<f32x4 *>(sMf)[tid + 256 * i] = mv[i];
+    if (tid < kFixRows * kDK / 4) reinterpret_cast<f32x4 *>(sS0)[tid] = sv0;
     const int k = tid & 127, i0 = 4 * (tid >> 7);
-    const float *M = sp.mend + h * kElems + k;
     const float *C = sp.cend + h * kElems + static_cast<size_t>(v0 + i0) * kDK + k;
     float acc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = C[i * kDK];
+    __syncthreads();
 #pragma unroll 4
     for (int j = 0; j < kDK; j += 4) {
       float m[4];
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) m[jj] = M[(j + jj) * kDK];
+      for (int jj = 0; jj < 4; ++jj) m[jj] = sMf[(j + jj) * kDK + k];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const f32x4 sv = *reinterpret_cast<const f32x4 *>(&sS0[(i0 + i) * kDK + j]);
@@ -1376,6 +1408,7 @@ void prefill_split_fix_kernel(int nt, Heads H, SplitScan sp, const uint16_t *__r
     return;
   }
 
+  const int id = blockIdx.x - nfix;
   const int c = sp.nt0 + id / H.v, h = id % H.v;
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
   const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
@@ -1385,6 +1418,12 @@ void prefill_split_fix_kernel(int nt, Heads H, SplitScan sp, const uint16_t *__r
   uint16_t *const ht = ws_ht + ch_head * kElems;
   const uint16_t *const Mc = sp.htm + (static_cast<size_t>(c - sp.nt0) * H.v + h) * kElems;
   const float *const S0 = sp.send + static_cast<size_t>(h) * kElems;
+
+  // M_c rows, loaded first (row tid / 16 + 16 i, columns 8 (tid % 16) ..+7).
+  u32x4 mrow[kDV * 16 / 256];
+#pragma unroll
+  for (int i = 0; i < kDV * 16 / 256; ++i)
+    mrow[i] = *reinterpret_cast<const u32x4 *>(Mc + (tid / 16 + 16 * i) * kDK + 8 * (tid % 16));
 
   // Phase 1 has wave w produce the columns v = 32 w + 16 vi + (lane & 15),
   // vi = 0, 1, of S_c^T[k][v] = sum_j M_c[j][k] S0[v][j] for all 128 k
@@ -1417,11 +1456,9 @@ void prefill_split_fix_kernel(int nt, Heads H, SplitScan sp, const uint16_t *__r
     wl[kk] = buf_load16(rw, wo + kk * 2048 + 16);
   }
 
-  for (int idx = tid; idx < kDV * 16; idx += 256) {
-    const int row = idx >> 4, c8 = (idx & 15) * 8;
-    *reinterpret_cast<u32x4 *>(&sM[row * kStrideK + c8]) =
-        *reinterpret_cast<const u32x4 *>(Mc + row * kDK + c8);
-  }
+#pragma unroll
+  for (int i = 0; i < kDV * 16 / 256; ++i)
+    *reinterpret_cast<u32x4 *>(&sM[(tid / 16 + 16 * i) * kStrideK + 8 * (tid % 16)]) = mrow[i];
   __syncthreads();
 
   f32x4 acc[8][2];
@@ -1538,12 +1575,23 @@ void prefill_output_kernel(
                               : u32x4{0u, 0u, 0u, 0u};
 
   if (tid < kChunk) sG[tid] = ws_G[ch_head * kChunk + tid];
-  for (int idx = tid; idx < kChunk * 16; idx += 256) {
-    const int row = idx >> 4, c8 = (idx & 15) * 8;
-    u32x4 qv = {0u, 0u, 0u, 0u};
-    if (row < len)
-      qv = *reinterpret_cast<const u32x4 *>(q + ((static_cast<size_t>(start) + row) * H.qk + hq) * kDK + c8);
-    *reinterpret_cast<u32x4 *>(&sQ[row * kStrideK + c8]) = qv;
+  {
+    // Q rows (zero past the chunk through the descriptor's range), every load
+    // issued before the LDS stores.
+    const uint32_t rstride = static_cast<uint32_t>(H.qk) * (kDK * 2);
+    const auto rq = buf_rsrc(q + (static_cast<size_t>(start) * H.qk + hq) * kDK,
+                             static_cast<uint32_t>(len) * rstride);
+    u32x4 qv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      qv[i] = buf_load16(rq, static_cast<uint32_t>(idx >> 4) * rstride + (idx & 15) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      *reinterpret_cast<u32x4 *>(&sQ[(idx >> 4) * kStrideK + (idx & 15) * 8]) = qv[i];
+    }
   }
   __syncthreads();
 
