@@ -1615,21 +1615,32 @@ void prefill_output_kernel(
       }
     }
   }
+  // The chunk-start state and v_new fragments of this wave's columns, loaded
+  // before the barrier (the K fragments are dead): their latency overlaps it.
+  u32x4 hbf[2][4], vbf[2][2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int n = 16 * (2 * wave + nt) + r16;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      hbf[nt][kk] = *reinterpret_cast<const u32x4 *>(ws_ht + (ch_head * kDV + n) * kDK + 32 * kk + kg);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+      vbf[nt][kk] = *reinterpret_cast<const u32x4 *>(ws_vnt + (ch_head * kDV + n) * kChunk + 32 * kk + kg);
+  }
   __syncthreads();
 
   f32x4 O[4][2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    const int n = 16 * (2 * wave + nt) + r16;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) O[mb][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const u32x4 hb = *reinterpret_cast<const u32x4 *>(ws_ht + (ch_head * kDV + n) * kDK + 32 * kk + kg);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const u32x4 qa = *reinterpret_cast<const u32x4 *>(&sQ[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
-        O[mb][nt] = mfma_bf16(qa, hb, O[mb][nt]);
+        O[mb][nt] = mfma_bf16(qa, hbf[nt][kk], O[mb][nt]);
       }
     }
 #pragma unroll
@@ -1638,11 +1649,10 @@ void prefill_output_kernel(
       for (int r = 0; r < 4; ++r) O[mb][nt][r] *= expf(sG[16 * mb + q4 + r]);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const u32x4 vb = *reinterpret_cast<const u32x4 *>(ws_vnt + (ch_head * kDV + n) * kChunk + 32 * kk + kg);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const u32x4 pa = *reinterpret_cast<const u32x4 *>(&sP[(16 * mb + r16) * kStrideT + 32 * kk + kg]);
-        O[mb][nt] = mfma_bf16(pa, vb, O[mb][nt]);
+        O[mb][nt] = mfma_bf16(pa, vbf[nt][kk], O[mb][nt]);
       }
     }
   }
