@@ -1339,198 +1339,302 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// 3b. two-segment scan, combination (after the state kernel).  With S0 =
-// sp.send (the state at chunk nt0) and, for a chunk c >= nt0, M_c = sp.htm
-// (the linear part of the map over chunks nt0..c-1, bf16 [j][k]) and C_c = ht
-// (its offset, bf16 [v][k]), the chunk-start state is S_c = S0 M_c + C_c.
-// Workgroups id = [0, (nt - nt0) H.v) after those of new_state: chunk c =
-// nt0 + id / H.v, head h = id % H.v (a head's workgroups share an XCD and
-// read S0 from its L2):
-//   S_c   = S0 M_c + C_c   (S0 split into bf16 hi + lo, M_c bf16) -> ht
-//   v_new = u - w S_c      (w and S_c split: three products)      -> vnt
-// so the output kernel reads what one chain would have left, to the bf16
-// rounding of M_c and C_c (a relative 2^-9 of S0 M_c and C_c, the same order
-// as the bf16 ht itself).  The first 16 H.v workgroups of the grid compute
-// new_state = S0 M + C instead, 8 rows each, in f32 FMAs (M = sp.mend, C =
-// sp.cend).
+// 3b. two-segment scan: the combination, and the output of the second
+// segment's chunks (one launch after the state kernel).  With S0 = sp.send
+// (the state at chunk nt0) and, for a chunk c >= nt0, M_c = sp.htm (the
+// linear part of the map over chunks nt0..c-1, bf16 [j][k]) and C_c = ht (its
+// offset, bf16 [v][k]), the chunk-start state is S_c = S0 M_c + C_c.
+//
+// Each workgroup produces the output of one chunk c >= nt0 and v-head h
+// (c = nt0 + id / H.v, h = id % H.v, so a head's workgroups share an XCD and
+// read S0 from its L2); wave w owns the columns v = 32 w .. 32 w + 31:
+//   S_c   = S0 M_c + C_c      S0 split into bf16 hi + lo, M_c bf16, in f32
+//   v_new = u - w S_c         w and S_c split: three products
+//   P     = mask_{j<=i}(exp(G_i - G_j) q_i . k_j)
+//   o     = scale (exp(G_i) q_i S_c + P v_new)
+// The state and v_new never leave the registers: a 16x16 result tile of
+// S_c^T (4 consecutive k per lane) and of v_new (4 consecutive tokens) is
+// the B operand of a 16x16x16 MFMA as it stands.  Up to the bf16 rounding of
+// M_c and C_c (a relative 2^-9 of S0 M_c and C_c, the order of the bf16 state
+// the output kernel uses) this is what the output kernel computes from the
+// single chain's ht and v_new.  new_state = S0 M + C (M = sp.mend, C =
+// sp.cend) is computed by extra workgroups of the output kernel's launch
+// (split_state_tile), which runs beside this one's in the same round.
 // ---------------------------------------------------------------------------
-constexpr int kFixRows = 8;  // new_state rows per combination workgroup
+constexpr int kSplitOutLds = 2 * kChunk * kStrideK * 2 + kDV * kStrideK * 2 + kChunk * kStrideT * 2 + kChunk * 4;
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-void prefill_split_fix_kernel(int nt, Heads H, SplitScan sp, const uint16_t *__restrict__ ws_w,
-                              const float *__restrict__ ws_u, uint16_t *ws_ht,
-                              uint16_t *__restrict__ ws_vnt, float *__restrict__ new_state) {
-  // Phase 1: M_c in [0, kDV * kStrideK); phase 2: S_c hi there, lo after it.
-  __shared__ __align__(16) uint16_t smem[2 * kDV * kStrideK];
+void prefill_split_out_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
+                              int T, int nt, Heads H, SplitScan sp,
+                              const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_w,
+                              const float *__restrict__ ws_u, const uint16_t *__restrict__ ws_ht,
+                              float scale, uint16_t *__restrict__ out) {
+  __shared__ __align__(16) uint16_t smem[kSplitOutLds / 2];
   constexpr size_t kElems = static_cast<size_t>(kDV) * kDK;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  constexpr int kFixGroups = kDV / kFixRows;
-  const int nfix = kFixGroups * H.v;
-
-  if (blockIdx.x < nfix) {
-    // new_state rows v0..v0+7 of head h (first in the grid, so that they run
-    // beside the chunk workgroups): M and the rows of S0 staged in LDS;
-    // thread t owns column k = t & 127 of rows v0 + 4 (t >> 7) .. +3.
-    const int h = blockIdx.x % H.v, v0 = kFixRows * (blockIdx.x / H.v);
-    float *sMf = reinterpret_cast<float *>(smem);  // [kDK][kDK]
-    float *sS0 = sMf + kDK * kDK;                  // [kFixRows][kDK]
-    const f32x4 *M4 = reinterpret_cast<const f32x4 *>(sp.mend + h * kElems);
-    const f32x4 *S04 = reinterpret_cast<const f32x4 *>(sp.send + h * kElems + static_cast<size_t>(v0) * kDK);
-    // every load issued before any LDS store (one memory latency, not 16)
-    f32x4 mv[kDK * kDK / 4 / 256];
-#pragma unroll
-    for (int i = 0; i < kDK * kDK / 4 / 256; ++i) mv[i] = M4[tid + 256 * i];
-    const f32x4 sv0 = S04[tid % (kFixRows * kDK / 4)];
-#pragma unroll
-    for (int i = 0; i < kDK * kDK / 4 / 256; ++i) reinterpret_cast<f32x4 *>(sMf)[tid + 256 * i] = mv[i];
-    if (tid < kFixRows * kDK / 4) reinterpret_cast<f32x4 *>(sS0)[tid] = sv0;
-    const int k = tid & 127, i0 = 4 * (tid >> 7);
-    const float *C = sp.cend + h * kElems + static_cast<size_t>(v0 + i0) * kDK + k;
-    float acc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = C[i * kDK];
-    __syncthreads();
-#pragma unroll 4
-    for (int j = 0; j < kDK; j += 4) {
-      float m[4];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) m[jj] = sMf[(j + jj) * kDK + k];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4 sv = *reinterpret_cast<const f32x4 *>(&sS0[(i0 + i) * kDK + j]);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) acc[i] = fmaf(sv[jj], m[jj], acc[i]);
-      }
-    }
-    float *dst = new_state + h * kElems + static_cast<size_t>(v0 + i0) * kDK + k;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i * kDK] = acc[i];
-    return;
-  }
-
-  const int id = blockIdx.x - nfix;
+  const int id = blockIdx.x;
   const int c = sp.nt0 + id / H.v, h = id % H.v;
+  const int start = c * kChunk, len = T - start < kChunk ? T - start : kChunk;
+  const int hq = h / H.ratio;
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
-  const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
-  uint16_t *const sM = smem;
-  uint16_t *const sSh = smem;
-  uint16_t *const sSl = smem + kDV * kStrideK;
-  uint16_t *const ht = ws_ht + ch_head * kElems;
-  const uint16_t *const Mc = sp.htm + (static_cast<size_t>(c - sp.nt0) * H.v + h) * kElems;
+  const int r16 = lane & 15, g = lane >> 4, kg = 8 * g, q4 = 4 * g;
+  uint16_t *const sQ = smem;                      // [64][kStrideK]; at the end o
+  uint16_t *const sK = sQ + kChunk * kStrideK;    // [64][kStrideK]
+  uint16_t *const sM = sK + kChunk * kStrideK;    // [128][kStrideK] M_c; then w's fragments
+  uint16_t *const sP = sM + kDV * kStrideK;       // [64][kStrideT]
+  float *const sG = reinterpret_cast<float *>(sP + kChunk * kStrideT);
   const float *const S0 = sp.send + static_cast<size_t>(h) * kElems;
+  const uint16_t *const Mc = sp.htm + (static_cast<size_t>(c - sp.nt0) * H.v + h) * kElems;
+  const uint16_t *const Cc = ws_ht + ch_head * kElems;
 
-  // M_c rows, loaded first (row tid / 16 + 16 i, columns 8 (tid % 16) ..+7).
-  u32x4 mrow[kDV * 16 / 256];
+  // --- loads: q, K rows (zero past the chunk through the descriptors'
+  // range), M_c rows, G -> LDS; C_c at this lane's result positions of S_c^T
+  // (k = 16 mi + q4 .. +3, v = 32 wave + 16 vi + r16) and this wave's S0 rows.
+  {
+    const uint32_t rstride = static_cast<uint32_t>(H.qk) * (kDK * 2);
+    const size_t qk0 = (static_cast<size_t>(start) * H.qk + hq) * kDK;
+    const auto rq = buf_rsrc(q + qk0, static_cast<uint32_t>(len) * rstride);
+    const auto rk = buf_rsrc(k + qk0, static_cast<uint32_t>(len) * rstride);
+    u32x4 qv[4], kv[4], mrow[8];
 #pragma unroll
-  for (int i = 0; i < kDV * 16 / 256; ++i)
-    mrow[i] = *reinterpret_cast<const u32x4 *>(Mc + (tid / 16 + 16 * i) * kDK + 8 * (tid % 16));
-
-  // Phase 1 has wave w produce the columns v = 32 w + 16 vi + (lane & 15),
-  // vi = 0, 1, of S_c^T[k][v] = sum_j M_c[j][k] S0[v][j] for all 128 k
-  // (tiles mi): A = M_c^T rows k (transposed LDS reads), B = S0 rows split.
-  // Loads that do not wait for M_c come first: C_c at this lane's result
-  // positions (k = 16 mi + q4 .. +3), this wave's S0 rows, the w fragments.
-  u32x2 cc[8][2];
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      const uint32_t off = static_cast<uint32_t>(idx >> 4) * rstride + (idx & 15) * 16;
+      qv[i] = buf_load16(rq, off);
+      kv[i] = buf_load16(rk, off);
+    }
 #pragma unroll
-  for (int mi = 0; mi < 8; ++mi)
+    for (int i = 0; i < 8; ++i)
+      mrow[i] = *reinterpret_cast<const u32x4 *>(Mc + (tid / 16 + 16 * i) * kDK + 8 * (tid % 16));
+    if (tid < kChunk) sG[tid] = ws_G[ch_head * kChunk + tid];
 #pragma unroll
-    for (int vi = 0; vi < 2; ++vi)
-      cc[mi][vi] = *reinterpret_cast<const u32x2 *>(ht + (32 * wave + 16 * vi + r16) * kDK + 16 * mi + q4);
-  u32x4 bh[2][4], bl[2][4];
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      *reinterpret_cast<u32x4 *>(&sQ[(idx >> 4) * kStrideK + (idx & 15) * 8]) = qv[i];
+      *reinterpret_cast<u32x4 *>(&sK[(idx >> 4) * kStrideK + (idx & 15) * 8]) = kv[i];
+    }
 #pragma unroll
-  for (int vi = 0; vi < 2; ++vi)
+    for (int i = 0; i < 8; ++i)
+      *reinterpret_cast<u32x4 *>(&sM[(tid / 16 + 16 * i) * kStrideK + 8 * (tid % 16)]) = mrow[i];
+  }
+  u32x2 cc[2][8];
+  f32x4 s0r[2][4][2];
+#pragma unroll
+  for (int vi = 0; vi < 2; ++vi) {
+    const int v = 32 * wave + 16 * vi + r16;
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi)
+      cc[vi][mi] = *reinterpret_cast<const u32x2 *>(Cc + v * kDK + 16 * mi + q4);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const float *p = S0 + (32 * wave + 16 * vi + r16) * kDK + 32 * kk + kg;
-      const f32x4 x0 = *reinterpret_cast<const f32x4 *>(p);
-      const f32x4 x1 = *reinterpret_cast<const f32x4 *>(p + 4);
-      const float xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-      split8(xs, bh[vi][kk], bl[vi][kk]);
+      s0r[vi][kk][0] = *reinterpret_cast<const f32x4 *>(S0 + v * kDK + 32 * kk + kg);
+      s0r[vi][kk][1] = *reinterpret_cast<const f32x4 *>(S0 + v * kDK + 32 * kk + kg + 4);
     }
-  const auto rw = buf_rsrc(ws_w + ch_head * (kWBytes / 2), kWBytes);
-  const uint32_t wo = static_cast<uint32_t>(wave) * 8192u + static_cast<uint32_t>(lane) * 32u;
-  u32x4 wh[4], wl[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    wh[kk] = buf_load16(rw, wo + kk * 2048);
-    wl[kk] = buf_load16(rw, wo + kk * 2048 + 16);
   }
-
-#pragma unroll
-  for (int i = 0; i < kDV * 16 / 256; ++i)
-    *reinterpret_cast<u32x4 *>(&sM[(tid / 16 + 16 * i) * kStrideK + 8 * (tid % 16)]) = mrow[i];
   __syncthreads();
 
-  f32x4 acc[8][2];
+  // --- P rows 16 wave .. +15 (as the output kernel).
+  {
+    const int mb = wave;
 #pragma unroll
-  for (int mi = 0; mi < 8; ++mi) {
-    u32x4 am[4];
+    for (int nb = 0; nb < 4; ++nb) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (nb <= mb) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const u32x2 x = ds_read_tr16(&sM[(32 * kk + kg + 4 * hh + (r16 >> 2)) * kStrideK +
-                                         16 * mi + 4 * (r16 & 3)]);
-        am[kk][2 * hh] = x[0];
-        am[kk][2 * hh + 1] = x[1];
+        for (int kk = 0; kk < 4; ++kk) {
+          const u32x4 af = *reinterpret_cast<const u32x4 *>(&sQ[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
+          const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[(16 * nb + r16) * kStrideK + 32 * kk + kg]);
+          acc = mfma_bf16(af, bf, acc);
+        }
       }
 #pragma unroll
-    for (int vi = 0; vi < 2; ++vi) {
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * mb + q4 + r, j = 16 * nb + r16;
+        const float p = (j <= i && i < len) ? expf(sG[i] - sG[j]) * acc[r] : 0.f;
+        sP[i * kStrideT + j] = f32_to_bf16(p);
+      }
+    }
+  }
+
+  // --- S_c^T[k][v] = sum_j M_c[j][k] S0[v][j] + C_c: A = M_c^T rows k
+  // (transposed LDS reads), B = S0 rows split; kept as split K=16 B operands.
+  u32x2 Sh[8][2], Sl[8][2];
+#pragma unroll
+  for (int vi = 0; vi < 2; ++vi) {
+    u32x4 bh[4], bl[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const f32x4 x0 = s0r[vi][kk][0], x1 = s0r[vi][kk][1];
+      const float xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      split8(xs, bh[kk], bl[kk]);
+    }
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi) {
+      u32x4 am[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const u32x2 x = ds_read_tr16(&sM[(32 * kk + kg + 4 * hh + (r16 >> 2)) * kStrideK +
+                                           16 * mi + 4 * (r16 & 3)]);
+          am[kk][2 * hh] = x[0];
+          am[kk][2 * hh + 1] = x[1];
+        }
       f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        a = mfma_bf16(am[kk], bh[vi][kk], a);
-        a = mfma_bf16(am[kk], bl[vi][kk], a);
+        a = mfma_bf16(am[kk], bh[kk], a);
+        a = mfma_bf16(am[kk], bl[kk], a);
       }
-      acc[mi][vi] = a;
+      const f32x4 sc = {a[0] + __uint_as_float(cc[vi][mi][0] << 16),
+                        a[1] + __uint_as_float(cc[vi][mi][0] & 0xffff0000u),
+                        a[2] + __uint_as_float(cc[vi][mi][1] << 16),
+                        a[3] + __uint_as_float(cc[vi][mi][1] & 0xffff0000u)};
+      split4(sc, Sh[mi][vi], Sl[mi][vi]);
     }
   }
-  __syncthreads();  // every wave is done with M_c: S_c takes its place
-
-  // S_c = product + C_c -> ht (bf16) and LDS (split, [v][k]).
+  // w's fragments (32 KB, the state kernel's A-operand order) into M_c's space.
+  u32x4 wraw[8];
+  {
+    const uint16_t *wsrc = ws_w + ch_head * (kWBytes / 2);
 #pragma unroll
-  for (int mi = 0; mi < 8; ++mi)
+    for (int i = 0; i < 8; ++i) wraw[i] = *reinterpret_cast<const u32x4 *>(wsrc + (tid + 256 * i) * 8);
+  }
+  __syncthreads();  // every wave is done with M_c and P is complete
 #pragma unroll
-    for (int vi = 0; vi < 2; ++vi) {
-      const int k0 = 16 * mi + q4, v = 32 * wave + 16 * vi + r16;
-      f32x4 sc;
-      sc[0] = acc[mi][vi][0] + __uint_as_float(cc[mi][vi][0] << 16);
-      sc[1] = acc[mi][vi][1] + __uint_as_float(cc[mi][vi][0] & 0xffff0000u);
-      sc[2] = acc[mi][vi][2] + __uint_as_float(cc[mi][vi][1] << 16);
-      sc[3] = acc[mi][vi][3] + __uint_as_float(cc[mi][vi][1] & 0xffff0000u);
-      *reinterpret_cast<u32x2 *>(ht + v * kDK + k0) =
-          u32x2{pk_bf16(sc[0], sc[1]), pk_bf16(sc[2], sc[3])};
-      u32x2 hi, lo;
-      split4(sc, hi, lo);
-      *reinterpret_cast<u32x2 *>(&sSh[v * kStrideK + k0]) = hi;
-      *reinterpret_cast<u32x2 *>(&sSl[v * kStrideK + k0]) = lo;
-    }
+  for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4 *>(&sM[(tid + 256 * i) * 8]) = wraw[i];
+  f32x4 uf[4][2];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int vi = 0; vi < 2; ++vi)
+      uf[tb][vi] = *reinterpret_cast<const f32x4 *>(
+          ws_u + ch_head * (kChunk * kDV) + ((tb * 8 + 2 * wave + vi) * 64 + lane) * 4);
   __syncthreads();
 
-  // Phase 2: v_new = u - w S_c for tokens 16 wave..+15, all 128 columns.
-  const auto ru = buf_rsrc(ws_u + ch_head * (kUBytes / 4), kUBytes);
-  f32x4 uf[8];
+  // --- v_new[t][v] = u - sum_k w[t][k] S_c[v][k] for all 64 tokens t (tiles
+  // tb) and this wave's columns; K=16 A fragments of w (4 consecutive k) are
+  // halves of the stored K=32 fragments: (tb, mi, lane) reads record
+  // (tb, mi / 2, lane 16 (2 (mi & 1) + (g >> 1)) + r16), elements 4 (g & 1)..+3.
+  u32x2 vb[4][2];  // v_new as bf16 B operands of P v_new
 #pragma unroll
-  for (int vt = 0; vt < 8; ++vt)
-    uf[vt] = __builtin_bit_cast(f32x4, buf_load16(ru, static_cast<uint32_t>((wave * 8 + vt) * 64 + lane) * 16u));
-  uint16_t *const vnt = ws_vnt + ch_head * (kDV * kChunk);
+  for (int tb = 0; tb < 4; ++tb) {
+    f32x4 P0[2], P1[2], P2[2];
 #pragma unroll
-  for (int vt = 0; vt < 8; ++vt) {
-    f32x4 P0 = {0.f, 0.f, 0.f, 0.f}, P1 = P0, P2 = P0;
+    for (int vi = 0; vi < 2; ++vi) P0[vi] = P1[vi] = P2[vi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const u32x4 sh = *reinterpret_cast<const u32x4 *>(&sSh[(16 * vt + r16) * kStrideK + 32 * kk + kg]);
-      const u32x4 sl = *reinterpret_cast<const u32x4 *>(&sSl[(16 * vt + r16) * kStrideK + 32 * kk + kg]);
-      P0 = mfma_bf16(wh[kk], sh, P0);
-      P1 = mfma_bf16(wh[kk], sl, P1);
-      P2 = mfma_bf16(wl[kk], sh, P2);
+    for (int mi = 0; mi < 8; ++mi) {
+      const int rec = (tb * 4 + (mi >> 1)) * 64 + 16 * (2 * (mi & 1) + (g >> 1)) + r16;
+      const u32x2 wh = *reinterpret_cast<const u32x2 *>(&sM[rec * 16 + 4 * (g & 1)]);
+      const u32x2 wl = *reinterpret_cast<const u32x2 *>(&sM[rec * 16 + 8 + 4 * (g & 1)]);
+#pragma unroll
+      for (int vi = 0; vi < 2; ++vi) {
+        P0[vi] = mfma16_bf16(wh, Sh[mi][vi], P0[vi]);
+        P1[vi] = mfma16_bf16(wh, Sl[mi][vi], P1[vi]);
+        P2[vi] = mfma16_bf16(wl, Sh[mi][vi], P2[vi]);
+      }
     }
-    float vn[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) vn[r] = uf[vt][r] - ((P0[r] + P1[r]) + P2[r]);
-    *reinterpret_cast<u32x2 *>(vnt + (16 * vt + r16) * kChunk + 16 * wave + q4) =
-        u32x2{pk_bf16(vn[0], vn[1]), pk_bf16(vn[2], vn[3])};
+    for (int vi = 0; vi < 2; ++vi) {
+      float vn[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vn[r] = uf[tb][vi][r] - ((P0[vi][r] + P1[vi][r]) + P2[vi][r]);
+      vb[tb][vi] = u32x2{pk_bf16(vn[0], vn[1]), pk_bf16(vn[2], vn[3])};
+    }
   }
+
+  // --- O = exp(G_t) q S_c^T + P v_new for all 64 tokens, this wave's columns.
+  f32x4 O[4][2];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+#pragma unroll
+    for (int vi = 0; vi < 2; ++vi) O[tb][vi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi) {
+      const u32x2 qa = *reinterpret_cast<const u32x2 *>(&sQ[(16 * tb + r16) * kStrideK + 16 * mi + q4]);
+#pragma unroll
+      for (int vi = 0; vi < 2; ++vi) {
+        O[tb][vi] = mfma16_bf16(qa, Sh[mi][vi], O[tb][vi]);
+        O[tb][vi] = mfma16_bf16(qa, Sl[mi][vi], O[tb][vi]);
+      }
+    }
+    float eg[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) eg[r] = expf(sG[16 * tb + q4 + r]);
+#pragma unroll
+    for (int vi = 0; vi < 2; ++vi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) O[tb][vi][r] *= eg[r];
+#pragma unroll
+    for (int jt = 0; jt <= tb; ++jt) {
+      const u32x2 pa = *reinterpret_cast<const u32x2 *>(&sP[(16 * tb + r16) * kStrideT + 16 * jt + q4]);
+#pragma unroll
+      for (int vi = 0; vi < 2; ++vi) O[tb][vi] = mfma16_bf16(pa, vb[jt][vi], O[tb][vi]);
+    }
+  }
+  __syncthreads();  // every wave is done with the Q tile: o takes its place
+
+  uint16_t *sO = sQ;  // [64][kStrideK]
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int vi = 0; vi < 2; ++vi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sO[(16 * tb + q4 + r) * kStrideK + 32 * wave + 16 * vi + r16] = f32_to_bf16(scale * O[tb][vi][r]);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + 256 * i, row = idx >> 4, c8 = (idx & 15) * 8;
+    if (row < len)
+      *reinterpret_cast<u32x4 *>(out + ((static_cast<size_t>(start) + row) * H.v + h) * kDV + c8) =
+          *reinterpret_cast<const u32x4 *>(&sO[row * kStrideK + c8]);
+  }
+}
+
+// new_state tile of a two-segment scan: rows 16 rb .. +15, columns 32 cb ..
+// +31 of head h, new_state = S0 M + C in f32 FMAs, with S0's rows and M's
+// columns staged in LDS (24 KB of the output kernel's 27 KB).  Thread t owns
+// column 32 cb + (t & 31) of rows 16 rb + (t >> 5) and 16 rb + (t >> 5) + 8.
+constexpr int kStateTiles = (kDV / 16) * (kDK / 32);  // per head
+__device__ __forceinline__ void split_state_tile(char *smem, int f, const Heads &H,
+                                                 const SplitScan &sp, float *new_state) {
+  constexpr size_t kElems = static_cast<size_t>(kDV) * kDK;
+  const int tid = threadIdx.x;
+  const int h = f % H.v, t = f / H.v, rb = t / (kDK / 32), cb = t % (kDK / 32);
+  float *sS0 = reinterpret_cast<float *>(smem);  // [16][128]
+  float *sMc = sS0 + 16 * kDK;                   // [128][32]
+  const float *S0 = sp.send + h * kElems + static_cast<size_t>(16 * rb) * kDK;
+  const float *M = sp.mend + h * kElems + 32 * cb;
+  f32x4 sv[2], mv[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) sv[i] = reinterpret_cast<const f32x4 *>(S0)[tid + 256 * i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + 256 * i;
+    mv[i] = *reinterpret_cast<const f32x4 *>(M + (idx >> 3) * kDK + 4 * (idx & 7));
+  }
+  const int col = tid & 31, r0 = tid >> 5;
+  const size_t o0 = h * kElems + static_cast<size_t>(16 * rb + r0) * kDK + 32 * cb + col;
+  float acc0 = sp.cend[o0], acc1 = sp.cend[o0 + 8 * kDK];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) reinterpret_cast<f32x4 *>(sS0)[tid + 256 * i] = sv[i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) reinterpret_cast<f32x4 *>(sMc)[tid + 256 * i] = mv[i];
+  __syncthreads();
+#pragma unroll 4
+  for (int j = 0; j < kDK; j += 4) {
+    const f32x4 a = *reinterpret_cast<const f32x4 *>(&sS0[r0 * kDK + j]);
+    const f32x4 b = *reinterpret_cast<const f32x4 *>(&sS0[(r0 + 8) * kDK + j]);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const float m = sMc[(j + jj) * 32 + col];
+      acc0 = fmaf(a[jj], m, acc0);
+      acc1 = fmaf(b[jj], m, acc1);
+    }
+  }
+  new_state[o0] = acc0;
+  new_state[o0 + 8 * kDK] = acc1;
 }
 
 // ---------------------------------------------------------------------------
@@ -1543,9 +1647,22 @@ void prefill_output_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
     const int4 *__restrict__ chunks, int single_T, int nt_max, Heads H,
     const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
-    uint16_t *__restrict__ out) {
+    uint16_t *__restrict__ out, SplitScan sp, float *__restrict__ new_state) {
+  // 27 KB of LDS and at most 128 VGPRs: four workgroups per CU.
+  __shared__ __align__(16) char osmem[kChunk * kStrideK * 2 + kChunk * kStrideT * 2 + kChunk * 4];
+  uint16_t *const sQ = reinterpret_cast<uint16_t *>(osmem);  // [64][kStrideK]
+  uint16_t *const sP = sQ + kChunk * kStrideK;                // [64][kStrideT]
+  float *const sG = reinterpret_cast<float *>(sP + kChunk * kStrideT);
+  static_assert(16 * kDK * 4 + kDK * 32 * 4 <= sizeof(osmem), "new_state tile must fit");
+  // After a two-segment scan the first kStateTiles H.v workgroups compute
+  // new_state.
+  const int nfix = sp.nt0 > 0 ? kStateTiles * H.v : 0;
+  if (static_cast<int>(blockIdx.x) < nfix) {
+    split_state_tile(osmem, blockIdx.x, H, sp, new_state);
+    return;
+  }
   int c, h;
-  if (!chunk_head_of(blockIdx.x, nt_max, H, c, h)) return;
+  if (!chunk_head_of(blockIdx.x - nfix, nt_max, H, c, h)) return;
   const int4 ch = chunk_info(chunks, c, single_T);
   if (ch.x < 0) return;
   const int start = ch.y, len = ch.z;
@@ -1554,11 +1671,6 @@ void prefill_output_kernel(
   const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
   const int hq = h / H.ratio;
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
-
-  // 27 KB of LDS and at most 128 VGPRs: four workgroups per CU.
-  __shared__ __align__(16) uint16_t sQ[kChunk * kStrideK];
-  __shared__ __align__(16) uint16_t sP[kChunk * kStrideT];
-  __shared__ float sG[kChunk];
 
   // K rows as B operands of Q K^T straight from the input (16 contiguous
   // bytes per lane; rows past the chunk read zero through the descriptor's
@@ -1688,9 +1800,11 @@ constexpr int kCandidateMeanLen = 32;
 
 // Two-segment scan of one sequence (state kernel, SplitScan): three groups of
 // 8 workgroups per v-head, one per CU, so it needs 24 H.v <= 256; the built-in
-// choice takes it from kSplitMinChunks chunks on.  Variants: 0 / -1 built in,
-// 2 never (one chain), 3 always (one sequence of at least two chunks).
-constexpr int kSplitMinChunks = 16;
+// choice takes it from kSplitMinChunks chunks on (MI355X, graph replay: one
+// chain vs two segments 41.0 vs 44.9 us at 16 chunks, 54.2 vs 51.6 at 32,
+// 173.9 vs ~130 at 128, 308 vs 275 at 256).  Variants: 0 / -1 built in, 2
+// never (one chain), 3 always (one sequence of at least two chunks).
+constexpr int kSplitMinChunks = 32;
 
 static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                           const float *state, const float *A_log, const gdn_bf16 *a,
@@ -1847,14 +1961,20 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
                      single_T, H, form, sp);
   if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
   if (sp.nt0 > 0) {
-    const unsigned fix_grid = static_cast<unsigned>((L.nt_max - sp.nt0) * H.v + (kDV / kFixRows) * H.v);
-    hipLaunchKernelGGL(prefill_split_fix_kernel, dim3(fix_grid), dim3(256), 0, stream, L.nt_max, H,
-                       sp, wsw, wsu, ht, vnt, new_state);
+    // new_state and the output of the second segment's chunks
+    const unsigned split_grid = static_cast<unsigned>((L.nt_max - sp.nt0) * H.v);
+    hipLaunchKernelGGL(prefill_split_out_kernel, dim3(split_grid), dim3(256), 0, stream, q, k, T,
+                       L.nt_max, H, sp, wsG, wsw, wsu, ht, scale, output);
     if ((rc = check_launch("gdn_prefill_fwd(split)"))) return rc;
   }
   if (L.nt_max > 0) {
-    hipLaunchKernelGGL(prefill_output_kernel, dim3(grid), dim3(256), 0, stream, q, k, chunks,
-                       single_T, L.nt_max, H, wsG, ht, vnt, scale, output);
+    // with the two-segment scan, the output kernel covers the first segment
+    // and new_state (extra workgroups first in its grid)
+    const int out_chunks = sp.nt0 > 0 ? sp.nt0 : L.nt_max;
+    const long long out_grid = chunk_head_grid(out_chunks, H) + (sp.nt0 > 0 ? kStateTiles * H.v : 0);
+    hipLaunchKernelGGL(prefill_output_kernel, dim3(static_cast<unsigned>(out_grid)), dim3(256), 0,
+                       stream, q, k, chunks, single_T, out_chunks, H, wsG, ht, vnt, scale, output,
+                       sp, new_state);
     if ((rc = check_launch("gdn_prefill_fwd(output)"))) return rc;
   }
   return GDN_OK;

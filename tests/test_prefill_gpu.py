@@ -466,7 +466,7 @@ def _stream(dev):
 # half of the chunks runs beside the first from a zero state and from the
 # identity, and a combination kernel applies the first half's final state.
 # variant 3 forces it (one sequence of >= 2 chunks), 2 forbids it; the built-in
-# choice takes it from 16 chunks on.
+# choice takes it from 32 chunks on.
 SPLIT, CHAIN = 3, 2
 
 
@@ -488,7 +488,7 @@ def test_prefill_two_segment_scan(cuda_device, L, with_state, slow):
         assert np.array_equal(oi, res[SPLIT][0]) and np.array_equal(si, res[SPLIT][1])
 
 
-@pytest.mark.parametrize("L, expect", [(512, CHAIN), (1024, SPLIT), (8192, SPLIT)])
+@pytest.mark.parametrize("L, expect", [(1024, CHAIN), (2048, SPLIT), (8192, SPLIT)])
 def test_prefill_two_segment_built_in_choice(cuda_device, L, expect):
     print(f"prefill two-segment choice L={L} expect variant {expect}", flush=True)
     inp = O.make_prefill_inputs([L], seed=41, with_state=True)
@@ -535,9 +535,11 @@ def test_prefill_two_segment_heads(cuda_device, heads):
 
 
 def test_prefill_two_segment_stage_intermediates(cuda_device):
-    # After the combination kernel the workspace holds what one chain leaves:
-    # every chunk's start state (ht) and v_new (vnt), and the first
-    # segment's final state (send) is the state at chunk nt0.
+    # The workspace after a two-segment call: the first segment's chunk-start
+    # states (ht) and v_new (vnt) are those of one chain; send is the state
+    # at chunk nt0; for the second segment, ht holds the offsets C_c and htm
+    # the linear parts M_c of the maps from chunk nt0, so that
+    # S_c = send M_c + C_c is the chain's chunk-start state.
     from gdn_amd import prefill
     L = 300  # 5 chunks: nt0 = 3, the last one partial
     inp = O.make_prefill_inputs([L], seed=44)
@@ -553,11 +555,17 @@ def test_prefill_two_segment_stage_intermediates(cuda_device):
         return np.frombuffer(ws[lay[name]:lay[name] + n * np.dtype(dtype).itemsize].tobytes(),
                              dtype=dtype).reshape(shape)
 
-    ht = O.bf16_from_bits(arr("ht", np.uint16, (nt, 8, 128, 128)))
-    h_ref = it["h"].transpose(0, 1, 3, 2)
-    assert np.abs(ht - h_ref).max() <= 1e-2 * np.abs(h_ref).max()
+    h_ref = it["h"].transpose(0, 1, 3, 2)          # [c, h, v, k]
+    vn_ref = it["v_new"].transpose(0, 1, 3, 2)     # [c, h, v, token]
+    ht = O.bf16_from_bits(arr("ht", np.uint16, (nt, 8, 128, 128))).astype(np.float64)
     vnt = O.bf16_from_bits(arr("vnt", np.uint16, (nt, 8, 128, 64)))
-    vn_ref = it["v_new"].transpose(0, 1, 3, 2)
-    assert np.abs(vnt - vn_ref).max() <= 1e-2 * np.abs(vn_ref).max()
-    send = arr("send", np.float32, (8, 128, 128))
+    assert np.abs(ht[:nt0] - h_ref[:nt0]).max() <= 1e-2 * np.abs(h_ref).max()
+    assert np.abs(vnt[:nt0] - vn_ref[:nt0]).max() <= 1e-2 * np.abs(vn_ref).max()
+    send = arr("send", np.float32, (8, 128, 128)).astype(np.float64)
     assert np.abs(send - h_ref[nt0]).max() <= 1e-4 * np.abs(h_ref[nt0]).max()
+    htm = O.bf16_from_bits(arr("htm", np.uint16, (nt - nt0, 8, 128, 128))).astype(np.float64)
+    assert np.array_equal(htm[0], np.broadcast_to(np.eye(128), (8, 128, 128)))  # M at nt0 = I
+    assert not ht[nt0].any()                                                   # C at nt0 = 0
+    for c in range(nt0, nt):
+        S_c = send @ htm[c - nt0] + ht[c]
+        assert np.abs(S_c - h_ref[c]).max() <= 1e-2 * np.abs(h_ref[c]).max(), f"chunk {c}"
