@@ -207,6 +207,50 @@ def bench_prefill_clone(lens, reps, dev):
     return statistics.median(times)
 
 
+def bench_copy(nbytes, steps, warmup, dev):
+    """The streaming ceiling of the decode step: `steps` calls of the library's
+    gdn_stream_copy (the decode kernel's access pattern, nbytes read and
+    nbytes written per call) over 8 rotating buffer pairs, captured in a HIP
+    graph as bench_decode's steps are; returns ms per call."""
+    import torch
+    from gdn_amd import _lib
+    from gdn_amd._common import stream_of
+
+    lib = _lib.load()
+    srcs = [torch.ones(nbytes // 4, dtype=torch.float32, device=dev) for _ in range(ROTATE)]
+    dsts = [torch.empty_like(srcs[0]) for _ in range(ROTATE)]
+
+    def step(i):
+        rc = lib.gdn_stream_copy(srcs[i % ROTATE].data_ptr(), dsts[i % ROTATE].data_ptr(), nbytes,
+                                 stream_of(dev))
+        _lib.check(rc, "gdn_stream_copy")
+
+    for i in range(warmup):
+        step(i)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        step(0)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            step(i)
+    graph.replay()
+    best = None
+    for _ in range(3):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record()
+        graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        best = ms if best is None else min(best, ms)
+    return best
+
+
 def measured_traffic(path=os.path.join(ROOT, "profiles", "decode_b64_hbm_traffic.md")):
     """HBM bytes per decode launch at B=64 from the committed rocprofv3 PMC
     summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of known size);
@@ -300,6 +344,12 @@ def main():
     gbs_step = nbytes / (ms_step * 1e-3) / 1e9
     log(f"decode B={B}: graph {ms_step * 1e3:.2f} us/step ({gbs_step:.1f} GB/s, "
         f"{gbs_step / HBM_PEAK_GBPS:.1%} of peak); eager {ms_eager * 1e3:.2f} us/step")
+    state_bytes = B * 8 * 128 * 128 * 4
+    copy_ms = bench_copy(state_bytes, args.steps, args.warmup, dev)
+    copy_gbs = 2 * state_bytes / (copy_ms * 1e-3) / 1e9
+    log(f"copy of the decode state (read + write {2 * state_bytes >> 20} MiB, the decode "
+        f"kernel's access pattern): {copy_ms * 1e3:.2f} us/call ({copy_gbs:.1f} GB/s); decode "
+        f"step / copy = {ms_step / copy_ms:.3f}")
 
     if args.sweep:
         for lens in ([1024], [6, 49, 294, 1800, 2040, 61], [8192], [8192] * 4, [64], [256]):
@@ -375,6 +425,9 @@ def main():
                    "batch": B, "heads_qk": 4, "heads_v": 8, "head_dim": 128},
         "decode_us_per_step": round(ms_step * 1e3, 3),
         "decode_us_per_step_eager": round(ms_eager * 1e3, 3),
+        "decode_copy_ceiling": {"us": round(copy_ms * 1e3, 3), "GBps": round(copy_gbs, 1),
+                                "bytes_moved": 2 * state_bytes,
+                                "decode_time_over_copy": round(ms_step / copy_ms, 4)},
         "prefill_ms_1x8192": round(pre_ms, 4),
         "prefill_ms_1x8192_eager": round(pre_eager, 4),
         "prefill_tokens_per_s": round(T8 / (pre_ms * 1e-3), 1),

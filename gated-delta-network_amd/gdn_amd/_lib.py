@@ -44,6 +44,7 @@ SIGNATURES = {
                                    _P, _SZ, _P, _I, _I, _I]),
     "gdn_prefill_fwd_heads": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F,
                                    _P, _P, _P, _SZ, _P, _I, _I, _I]),
+    "gdn_stream_copy": (_I, [_P, _P, _SZ, _P]),
 }
 
 

@@ -229,6 +229,17 @@ int gdn_prefill_fwd_heads(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
                           float *new_state, void *workspace, size_t workspace_bytes, void *stream,
                           int state_tiling, int recurrent_max_len, int recurrent_tiling);
 
+/*
+ * Measurement support (no counterpart in the reference): copies `bytes`
+ * bytes from src to dst in the decode kernel's access pattern (one wave per
+ * 32 KiB, every load before the first store, non-temporal), i.e. the HBM
+ * streaming ceiling of a kernel that reads and writes each byte of a state
+ * once at that size, launch ramp included.  bytes must be a multiple of
+ * 32768; src and dst 16-byte aligned and disjoint.  bench.py reports the
+ * decode step against it.
+ */
+int gdn_stream_copy(const void *src, void *dst, size_t bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -212,3 +212,16 @@ def test_prefill_heads_rejects_bad_heads(hqk, hv):
     rc = lib.gdn_prefill_fwd_heads(*a[:12], hqk, hv, *a[12:], -1, -1, -1)
     assert rc == _lib.GDN_ERR_INVALID
     assert "heads" in _lib.last_error()
+
+
+@pytest.mark.parametrize("src, dst, nbytes, needle", [
+    (None, 1 << 20, 32768, "null"),
+    (1 << 20, (1 << 21) + 8, 32768, "aligned"),
+    (1 << 20, 1 << 21, 32768 + 16, "multiple"),
+    (1 << 20, (1 << 20) + 16384, 32768, "overlap"),
+])
+def test_stream_copy_rejects_bad_arguments(src, dst, nbytes, needle):
+    # Rejected before any HIP call, so this runs without a GPU.
+    lib = _lib.load()
+    assert lib.gdn_stream_copy(src, dst, nbytes, None) == _lib.GDN_ERR_INVALID
+    assert needle in _lib.last_error()

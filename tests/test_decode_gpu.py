@@ -222,3 +222,17 @@ def test_decode_deterministic(cuda_device):
     runs = [run_gpu(d, B, cuda_device) for _ in range(3)]
     for o, s in runs[1:]:
         assert np.array_equal(o, runs[0][0]) and np.array_equal(s, runs[0][1])
+
+
+def test_stream_copy_copies(cuda_device):
+    # The measurement copy behind bench.py's decode_copy_ceiling.
+    from gdn_amd import _lib
+    from gdn_amd._common import stream_of
+    n = 3 * 32768
+    print(f"stream copy {n} bytes", flush=True)
+    src = torch.randn(n // 4, device=cuda_device)
+    dst = torch.zeros_like(src)
+    rc = _lib.load().gdn_stream_copy(src.data_ptr(), dst.data_ptr(), n, stream_of(cuda_device))
+    assert rc == _lib.GDN_OK
+    torch.cuda.synchronize()
+    assert torch.equal(src, dst)
