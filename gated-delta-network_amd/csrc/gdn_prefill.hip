@@ -1276,7 +1276,8 @@ __device__ __forceinline__ void t_state(
 // and v_new are then the offsets; the end is sp.cend) and from the identity
 // (MAP: the linear parts M into sp.htm; the end is sp.mend).  The three
 // groups of 8 workgroups per head run side by side, s = 0, 1, 2 below, so the
-// serial chain is half as long; prefill_split_fix_kernel then combines them.
+// serial chain is half as long; prefill_split_out_kernel and the output
+// kernel's new_state tiles then combine them.
 // ---------------------------------------------------------------------------
 struct SplitScan {
   int nt0;        // first chunk of the second segment; 0 = one chain

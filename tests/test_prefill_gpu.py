@@ -464,7 +464,8 @@ def _stream(dev):
 
 # Two-segment scan of one sequence (gdn_prefill.hip, SplitScan): the second
 # half of the chunks runs beside the first from a zero state and from the
-# identity, and a combination kernel applies the first half's final state.
+# identity, and the second segment's output and new_state then apply the
+# first half's final state.
 # variant 3 forces it (one sequence of >= 2 chunks), 2 forbids it; the built-in
 # choice takes it from 32 chunks on.
 SPLIT, CHAIN = 3, 2
