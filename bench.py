@@ -283,6 +283,30 @@ def cpu_baseline_decode(B, seconds):
     return el / reps, reps
 
 
+def cpu_baseline_prefill(lens):
+    """One prefill of `lens` through the sequential recurrence restated in C
+    (oracle/gdn_seq.c: the reference's per-token loop, f32, one OpenMP thread
+    per (sequence, v-head) pair); returns (seconds, threads used)."""
+    from oracle import gdn_oracle as O
+
+    inp = O.make_prefill_inputs(lens, seed=2, with_state=len(lens) > 1)
+    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "64")),
+                  len(lens) * 8)
+    t = time.perf_counter()
+    O.prefill_seq_c(**inp)
+    return time.perf_counter() - t, threads
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -406,6 +430,8 @@ def main():
     cpu_s, reps = cpu_baseline_decode(B, args.cpu_seconds)
     cpu_gbs = nbytes / cpu_s / 1e9
     log(f"cpu baseline decode B={B}: {cpu_s * 1e3:.1f} ms/step over {reps} steps")
+    cpu_pre_s, cpu_pre_threads = cpu_baseline_prefill(pre_lens)
+    log(f"cpu baseline prefill 1x8192: {cpu_pre_s:.2f} s ({cpu_pre_threads} threads)")
 
     b200_gbs = O.decode_bytes(64) / (B200_DECODE_MS_B64 * 1e-3) / 1e9
     line = {
@@ -450,7 +476,13 @@ def main():
                      "bytes_per_launch": nbytes},
         "cpu_baseline": {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
                          "sample": f"{reps} decode steps at B={B} "
-                                   f"({cpu_s * 1e3:.1f} ms/step), oracle decode_loop, 1 thread"},
+                                   f"({cpu_s * 1e3:.1f} ms/step), oracle decode_loop (numpy), "
+                                   f"1 thread of {cpu_model()}"},
+        "cpu_baseline_prefill": {"value": round(T8 / cpu_pre_s, 1), "unit": "tokens/s",
+                                 "cores": cpu_pre_threads, "kind": "port",
+                                 "sample": f"one 1x8192 prefill in {cpu_pre_s:.2f} s, oracle "
+                                           f"gdn_seq.c (per-token loop, f32), OpenMP over the "
+                                           f"8 v-heads, {cpu_model()}"},
     }
     print(json.dumps(line), flush=True)
 

@@ -205,3 +205,50 @@ def test_prefill_workspace_argument_checks(cuda_device):
     o_ref, s_ref = O.prefill_seq_c(**inp)
     assert_output_close(out.float().cpu().numpy(), o_ref)
     assert_state_close(ns.cpu().numpy(), s_ref)
+
+
+def test_prefill_graph_replays_two_segment_scan(cuda_device):
+    # One sequence of 2500 tokens (40 chunks: the two-segment scan, its
+    # second-segment output kernel and the new_state tiles), captured once and
+    # replayed with new inputs; every replay equals the eager call.
+    dev = cuda_device
+    T, N = 2500, 1
+    print(f"prefill graph two-segment T={T}", flush=True)
+    st = _prefill_static(T, N, dev)
+    inp = O.make_prefill_inputs([T], seed=50)
+    _fill_prefill(st, inp)
+    scale = float(inp["scale"])
+    ws = prefill.alloc_workspace(T, N, dev)
+    out = torch.empty((T, 8, 128), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((N, 8, 128, 128), dtype=torch.float32, device=dev)
+
+    def call(o, s):
+        prefill.kernel(st["q"], st["k"], st["v"], st["state"], st["A_log"], st["a"],
+                       st["dt_bias"], st["b"], st["cu_seqlens"], scale, o, s, workspace=ws)
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        call(out, ns)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(out, ns)
+    torch.cuda.synchronize()
+
+    for rep in range(3):
+        print(f"  replay {rep}", flush=True)
+        inp = O.make_prefill_inputs([T], seed=51 + rep, slow_decay_heads=(7,) if rep else ())
+        _fill_prefill(st, inp)
+        g.replay()
+        torch.cuda.synchronize()
+        o_g, s_g = out.clone(), ns.clone()
+        o_e = torch.empty_like(out)
+        s_e = torch.empty_like(ns)
+        call(o_e, s_e)
+        torch.cuda.synchronize()
+        assert torch.equal(o_g, o_e), f"replay {rep}: output differs from the eager call"
+        assert torch.equal(s_g, s_e), f"replay {rep}: state differs from the eager call"
+        o_ref, s_ref = O.prefill_seq_c(**inp)
+        assert_output_close(o_g.float().cpu().numpy(), o_ref)
+        assert_state_close(s_g.cpu().numpy(), s_ref)
