@@ -421,10 +421,23 @@ def main():
                           "GBps": round(O.decode_bytes(b) / (mg * 1e-3) / 1e9, 1)}
     log(f"decode sweep (graph us/step, GB/s): {sweep}")
     cfg_ms = {}
+    cfg_detail = {}
+
+    def detail(lens, ms):
+        T, N = sum(lens), len(lens)
+        nt = sum(-(-L // 64) for L in lens)
+        tflops = O.prefill_flops(nt) / (ms * 1e-3) / 1e12
+        return {"ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                "tflops": round(tflops, 2), "mfma_frac": round(tflops / 2500.0, 5),
+                "hbm_gbps": round(O.prefill_bytes(T, N) / (ms * 1e-3) / 1e9, 1)}
+
     for name, lens, kw in (("configs3_varlen6", [6, 49, 294, 1800, 2040, 61], {}),
                            ("configs4_4x8192", [8192] * 4, {"slow_decay_heads": (6, 7)})):
         _, pg = bench_prefill(lens, 10, 2, dev, **kw)
         cfg_ms[name] = round(pg, 4)
+        cfg_detail[name] = detail(lens, pg)
+    cfg_detail["configs2_1x1024"] = detail([1024], pre1k_ms)
+    cfg_detail["north_star_1x8192"] = detail(pre_lens, pre_ms)
     log(f"prefill configs (graph ms per call): {cfg_ms}")
 
     cpu_s, reps = cpu_baseline_decode(B, args.cpu_seconds)
@@ -462,6 +475,7 @@ def main():
         "prefill_ms_1x1024_clone": round(pre1k_clone, 4),
         "decode_sweep": sweep,
         "prefill_ms_configs": cfg_ms,
+        "prefill_configs": cfg_detail,
         "decode_multi_token_us": mtp,
         "prefill_ms_short_batches": short,
         "prefill_roofline": {"bound": "mfma", "achieved": round(pre_tflops, 2), "peak": 2500.0,

@@ -1029,12 +1029,15 @@ struct FragOffsets {
   uint32_t k, t, v, vec;
 };
 
-// Fragments of chunk c (tokens [start, start + len)) for v-head h.
+// Fragments of chunk c (tokens [start, start + len)) for v-head h.  T is
+// lower triangular: the rows of waves 0 and 1 (0..31) are zero in columns
+// 32..63, so those waves load (and multiply) only the first k-step.
 __device__ __forceinline__ void load_t_frag(TFrag &f, int c, int start, int len, int h,
                                                 const Heads &H, const FragOffsets &o,
                                                 const uint16_t *k, const uint16_t *v,
                                                 const float *ws_dcy, const float *ws_eg,
-                                                const uint16_t *ws_w, const float *ws_u) {
+                                                const uint16_t *ws_w, const float *ws_u,
+                                                bool t_upper) {
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
   const uint32_t nlen = static_cast<uint32_t>(len);
   const auto rk = buf_rsrc(k + (static_cast<size_t>(start) * H.qk + h / H.ratio) * kDK,
@@ -1042,10 +1045,13 @@ __device__ __forceinline__ void load_t_frag(TFrag &f, int c, int start, int len,
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) f.kf[kk] = buf_load16(rk, o.k + kk * 64);
   const auto rt = buf_rsrc(ws_w + ch_head * (kChunk * kDK * 2), kTElems * 2);  // T, w region
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    f.th[kk] = buf_load16(rt, o.t + kk * 2048);
-    f.tl[kk] = buf_load16(rt, o.t + kk * 2048 + 16);
+  f.th[0] = buf_load16(rt, o.t);
+  f.tl[0] = buf_load16(rt, o.t + 16);
+  if (t_upper) {
+    f.th[1] = buf_load16(rt, o.t + 2048);
+    f.tl[1] = buf_load16(rt, o.t + 2048 + 16);
+  } else {
+    f.th[1] = f.tl[1] = u32x4{0u, 0u, 0u, 0u};
   }
   const auto rv = buf_rsrc(v + (static_cast<size_t>(start) * H.v + h) * kDV,
                            nlen * static_cast<uint32_t>(H.v) * (kDV * 2));
@@ -1171,6 +1177,7 @@ __device__ __forceinline__ void t_state(
       f32x4 P0 = {0.f, 0.f, 0.f, 0.f}, P1 = P0, P2 = P0;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
+        if (kk == 1 && wave < 2) break;  // T's rows 0..31 are zero in columns 32..63
         const u32x4 yh = *reinterpret_cast<const u32x4 *>(&sYh[r16 * kStrideT + 32 * kk + kg]);
         const u32x4 yl = *reinterpret_cast<const u32x4 *>(&sYl[r16 * kStrideT + 32 * kk + kg]);
         P0 = mfma_bf16(f.th[kk], yh, P0);
@@ -1227,7 +1234,7 @@ __device__ __forceinline__ void t_state(
       i = i < nch ? i : nch - 1;
       const int start = bos + i * kChunk, rem = eos - start;
       load_t_frag(f, c0 + i, start, rem < kChunk ? rem : kChunk, h, H, fo, k, v, ws_dcy, ws_eg,
-                  ws_w, ws_u);
+                  ws_w, ws_u, wave >= 2);
     };
     TFrag fa, fb;
     load(fa, 0);
