@@ -1,0 +1,344 @@
+// Gated DeltaNet over short sequences in blocks of 16 tokens: one workgroup per
+// (sequence, v-head) keeps the whole [V=128, K=128] f32 state in MFMA result
+// tiles for the sequence and applies it block by block in the chunked (WY)
+// form, the intra-block work included.
+//
+// Semantics: the per-token loop of reference/gdn_prefill_ref.py:71-89 (for
+// one token, reference/gdn_decode_ref.py:60-81).  Per block of n <= 16
+// tokens (g = log decay, G = its cumsum within the block, beta = sigmoid(b),
+// S = the state at the block start, k-last: S[v][k]):
+//   A     = strictly-lower(beta_i exp(G_i - G_j) k_i . k_j),  Ti = (I + A)^-1
+//   W     = Ti diag(beta e^G) K,     U = Ti diag(beta) V
+//   v_new = U - W S^T
+//   o_i   = scale (exp(G_i) q_i S^T + sum_{j<=i} exp(G_i - G_j) (q_i . k_j) v_new_j)
+//   S    <- exp(G_last) S + (diag(exp(G_last - G)) v_new)^T K
+// the algebra of the chunk pipeline (gdn_prefill.hip) on 16-token blocks,
+// fused into one launch.  It serves the token-sequential cases: decode of
+// T > 1 tokens per row, and prefill of batches of short sequences.
+//
+// Work mapping (gfx950, wave64, 256 threads): wave w owns the state columns
+// v = 32 w .. 32 w + 31 for all 128 k, as 16 result tiles of S^T (rows k,
+// columns v: 4 consecutive k per lane), which is exactly the B operand of a
+// 16x16x16 MFMA contracting over k (W S^T, q S^T); v_new comes out of those
+// products as tiles of 4 consecutive tokens per lane, the B operand of the
+// update K^T v_new and of P v_new.  K^T and the token-major operands of W
+// and U are read transposed out of the block's K and V rows in LDS
+// (ds_read_b64_tr_b16).  Products whose error reaches the state use split
+// bf16 (x = hi + lo), as in the chunk pipeline; the output path uses single
+// bf16 operands.
+#include "gdn_device.h"
+#include "gdn_host.h"
+
+namespace gdn {
+
+constexpr int kBlk = 16;        // tokens per block
+constexpr int kBStride = 136;   // bf16 row stride of the q/k/v block tiles
+constexpr int kBStrideA = 17;   // f32 row stride of the 16x16 A and Ti tiles
+constexpr int kBStrideW = 132;  // f32 row stride of W
+constexpr int kBStrideP = 24;   // bf16 row stride of P
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
+                  const uint16_t *__restrict__ v, const float *state,
+                  const float *__restrict__ A_log, const uint16_t *__restrict__ a,
+                  const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
+                  const void *__restrict__ cu, int cu64, int T, int fixed_len,
+                  const int *__restrict__ enable, Heads H, float scale,
+                  uint16_t *__restrict__ out, float *new_state) {
+  __shared__ __align__(16) uint16_t sQ[kBlk * kBStride];
+  __shared__ __align__(16) uint16_t sK[kBlk * kBStride];
+  __shared__ __align__(16) uint16_t sV[kBlk * kBStride];
+  __shared__ __align__(16) float sA[kBlk * kBStrideA];
+  __shared__ __align__(16) float sTi[kBlk * kBStrideA];
+  __shared__ __align__(16) float sW[kBlk * kBStrideW];
+  __shared__ __align__(16) uint16_t sP[kBlk * kBStrideP];
+  __shared__ float sG[kBlk], sBeta[kBlk];
+
+  if (enable != nullptr && *enable == 0) return;  // the batch went through the chunks
+  const int h = blockIdx.x % H.v, s = blockIdx.x / H.v;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4, q4 = 4 * g, kg = 8 * g;
+  const int hq = h / H.ratio;
+
+  int bos, len;
+  if (cu != nullptr) {
+    bos = load_cu(cu, cu64, s, T);
+    const int eos = load_cu(cu, cu64, s + 1, T);
+    len = eos > bos ? eos - bos : 0;
+  } else {
+    bos = s * fixed_len;
+    len = fixed_len;
+  }
+  bos = __builtin_amdgcn_readfirstlane(bos);
+  len = __builtin_amdgcn_readfirstlane(len);
+
+  // The state as result tiles of S^T: St[kt][vi] holds S[v][k] at
+  // k = 16 kt + q4 + r, v = 32 wave + 16 vi + r16.
+  const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;
+  f32x4 St[8][2];
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+    for (int vi = 0; vi < 2; ++vi) {
+      const int vc = 32 * wave + 16 * vi + r16;
+      if (state != nullptr && len > 0)
+        St[kt][vi] = *reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + 16 * kt + q4);
+      else
+        St[kt][vi] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  const uint32_t qk_stride = static_cast<uint32_t>(H.qk) * (kDK * 2);
+  const uint32_t v_stride = static_cast<uint32_t>(H.v) * (kDV * 2);
+  // The inputs of a block -- this thread's 16 bytes of its q, k and v rows
+  // (row tid / 16; rows past the sequence read zero through the descriptors'
+  // range) and, in wave 0, the raw gates of token `lane` -- are loaded one
+  // block ahead of use.
+  struct BlockIn {
+    u32x4 q, k, v;
+    uint16_t a, b;
+  };
+  const int row = tid >> 4, c16 = tid & 15;
+  const float rate = expf(A_log[h]), dtb = dt_bias[h];
+  auto load_block = [&](int t0, BlockIn &x) {
+    const int n = len - t0 < kBlk ? len - t0 : kBlk;  // <= 0 past the end: all zero
+    const uint32_t nn = n > 0 ? static_cast<uint32_t>(n) : 0u;
+    const int start = bos + t0;
+    const size_t qk0 = (static_cast<size_t>(start) * H.qk + hq) * kDK;
+    const auto rq = buf_rsrc(q + qk0, nn * qk_stride);
+    const auto rk = buf_rsrc(k + qk0, nn * qk_stride);
+    const size_t v0 = (static_cast<size_t>(start) * H.v + h) * kDV;
+    const auto rv = buf_rsrc(v + v0, nn * v_stride);
+    x.q = buf_load16(rq, row * qk_stride + c16 * 16);
+    x.k = buf_load16(rk, row * qk_stride + c16 * 16);
+    x.v = buf_load16(rv, row * v_stride + c16 * 16);
+    const size_t g0 = static_cast<size_t>(start) * H.v + h;
+    const uint32_t gbytes = nn * static_cast<uint32_t>(H.v) * 2u;
+    const uint32_t goff = static_cast<uint32_t>(lane) * static_cast<uint32_t>(H.v) * 2u;
+    x.a = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(a + g0, gbytes), goff, 0, 0);
+    x.b = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(b + g0, gbytes), goff, 0, 0);
+  };
+  BlockIn cur;
+  if (len > 0) load_block(0, cur);
+  for (int t0 = 0; t0 < len; t0 += kBlk) {
+    const int n = len - t0 < kBlk ? len - t0 : kBlk;
+    const int start = bos + t0;
+
+    // (1) this block's q, k, v rows into LDS; gating and the in-block cumsum
+    //     (wave 0); the next block's inputs requested.
+    {
+      *reinterpret_cast<u32x4 *>(&sQ[row * kBStride + c16 * 8]) = cur.q;
+      *reinterpret_cast<u32x4 *>(&sK[row * kBStride + c16 * 8]) = cur.k;
+      *reinterpret_cast<u32x4 *>(&sV[row * kBStride + c16 * 8]) = cur.v;
+      const uint16_t a_raw = cur.a, b_raw = cur.b;
+      if (t0 + kBlk < len) load_block(t0 + kBlk, cur);
+      if (wave == 0) {
+        const float gl = lane < n ? -rate * softplus20(bf16_to_f32(a_raw) + dtb) : 0.f;
+        const float be = lane < n ? sigmoidf_(bf16_to_f32(b_raw)) : 0.f;
+        float G = gl;
+#pragma unroll
+        for (int off = 1; off < kBlk; off <<= 1) {
+          const float y = __shfl_up(G, off, kBlk);
+          if (r16 >= off) G += y;
+        }
+        if (lane < kBlk) {
+          sG[lane] = G;
+          sBeta[lane] = be;
+        }
+      }
+    }
+    __syncthreads();
+
+    // (2) A = strictly-lower(beta_i e^{G_i - G_j} K K^T) (wave 0) and
+    //     P = mask_{j<=i}(e^{G_i - G_j} Q K^T) (wave 1), 16x16 each.
+    if (wave < 2) {
+      const uint16_t *sX = wave == 0 ? sK : sQ;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const u32x4 af = *reinterpret_cast<const u32x4 *>(&sX[r16 * kBStride + 32 * kk + kg]);
+        const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[r16 * kBStride + 32 * kk + kg]);
+        acc = mfma_bf16(af, bf, acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = q4 + r, j = r16;
+        if (wave == 0) {
+          sA[i * kBStrideA + j] = i > j ? sBeta[i] * expf(sG[i] - sG[j]) * acc[r] : 0.f;
+        } else {
+          const float p = (j <= i && i < n) ? expf(sG[i] - sG[j]) * acc[r] : 0.f;
+          sP[i * kBStrideP + j] = f32_to_bf16(p);
+        }
+      }
+    }
+    __syncthreads();
+
+    // (3) Ti = (I + A)^-1 by forward substitution, lane j < 16 of wave 0
+    //     solving column j.
+    if (wave == 0 && lane < kBlk) {
+      float x[kBlk];
+#pragma unroll
+      for (int i = 0; i < kBlk; ++i) {
+        const float *arow = &sA[i * kBStrideA];
+        float s0 = (i == lane) ? 1.f : 0.f, s1 = 0.f;
+#pragma unroll
+        for (int m = 0; m < i; m += 2) {
+          s0 -= arow[m] * x[m];
+          if (m + 1 < i) s1 -= arow[m + 1] * x[m + 1];
+        }
+        x[i] = s0 + s1;
+      }
+#pragma unroll
+      for (int i = 0; i < kBlk; ++i) sTi[i * kBStrideA + lane] = x[i];
+    }
+    __syncthreads();
+
+    // (4) W = Ti diag(beta e^G) K for the features 32 wave .. +31 (-> LDS, f32)
+    //     and U = Ti diag(beta) V for this wave's columns (registers).  A
+    //     operand: Ti's row r16, tokens q4..q4+3, scaled and split; B operand:
+    //     4 consecutive tokens of one feature, a transposed read of the rows.
+    f32x4 U[2];
+    {
+      const f32x4 ti = {sTi[r16 * kBStrideA + q4], sTi[r16 * kBStrideA + q4 + 1],
+                        sTi[r16 * kBStrideA + q4 + 2], sTi[r16 * kBStrideA + q4 + 3]};
+      f32x4 tw, tu;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float be = sBeta[q4 + e];
+        tu[e] = ti[e] * be;
+        tw[e] = ti[e] * be * expf(sG[q4 + e]);
+      }
+      u32x2 twh, twl, tuh, tul;
+      split4(tw, twh, twl);
+      split4(tu, tuh, tul);
+#pragma unroll
+      for (int ft = 0; ft < 2; ++ft) {
+        const int c0 = 32 * wave + 16 * ft;  // feature tile of W / column tile of U
+        const u32x2 kb = ds_read_tr16(&sK[(q4 + (r16 >> 2)) * kBStride + c0 + 4 * (r16 & 3)]);
+        const u32x2 vb = ds_read_tr16(&sV[(q4 + (r16 >> 2)) * kBStride + c0 + 4 * (r16 & 3)]);
+        f32x4 w = mfma16_bf16(twh, kb, f32x4{0.f, 0.f, 0.f, 0.f});
+        w = mfma16_bf16(twl, kb, w);
+        f32x4 u = mfma16_bf16(tuh, vb, f32x4{0.f, 0.f, 0.f, 0.f});
+        U[ft] = mfma16_bf16(tul, vb, u);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sW[(q4 + r) * kBStrideW + c0 + r16] = w[r];
+      }
+    }
+    __syncthreads();
+
+    // (5) v_new = U - W S^T for this wave's columns (W and S split: three
+    //     products per k-tile).  The state is split here, after the
+    //     intra-block work, so that at the first block its loads overlap it.
+    u32x2 Sh[8][2], Sl[8][2];
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+      for (int vi = 0; vi < 2; ++vi) split4(St[kt][vi], Sh[kt][vi], Sl[kt][vi]);
+    f32x4 vn[2];
+    {
+      f32x4 P0[2], P1[2], P2[2];
+#pragma unroll
+      for (int vi = 0; vi < 2; ++vi) P0[vi] = P1[vi] = P2[vi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt) {
+        const f32x4 wf = *reinterpret_cast<const f32x4 *>(&sW[r16 * kBStrideW + 16 * kt + q4]);
+        u32x2 wh, wl;
+        split4(wf, wh, wl);
+#pragma unroll
+        for (int vi = 0; vi < 2; ++vi) {
+          P0[vi] = mfma16_bf16(wh, Sh[kt][vi], P0[vi]);
+          P1[vi] = mfma16_bf16(wh, Sl[kt][vi], P1[vi]);
+          P2[vi] = mfma16_bf16(wl, Sh[kt][vi], P2[vi]);
+        }
+      }
+#pragma unroll
+      for (int vi = 0; vi < 2; ++vi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vn[vi][r] = U[vi][r] - ((P0[vi][r] + P1[vi][r]) + P2[vi][r]);
+    }
+
+    // (6) o = scale (e^{G_i} q_i S^T + P v_new) for this wave's columns.
+    {
+      f32x4 O[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt) {
+        const u32x2 qa = *reinterpret_cast<const u32x2 *>(&sQ[r16 * kBStride + 16 * kt + q4]);
+#pragma unroll
+        for (int vi = 0; vi < 2; ++vi) {
+          O[vi] = mfma16_bf16(qa, Sh[kt][vi], O[vi]);
+          O[vi] = mfma16_bf16(qa, Sl[kt][vi], O[vi]);
+        }
+      }
+      float eg[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) eg[r] = expf(sG[q4 + r]);
+      const u32x2 pa = *reinterpret_cast<const u32x2 *>(&sP[r16 * kBStrideP + q4]);
+#pragma unroll
+      for (int vi = 0; vi < 2; ++vi) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) O[vi][r] *= eg[r];
+        const u32x2 vb = {pk_bf16(vn[vi][0], vn[vi][1]), pk_bf16(vn[vi][2], vn[vi][3])};
+        O[vi] = mfma16_bf16(pa, vb, O[vi]);
+        const int vc = 32 * wave + 16 * vi + r16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (q4 + r < n)
+            out[(static_cast<size_t>(start) + q4 + r) * H.v * kDV + h * kDV + vc] =
+                f32_to_bf16(scale * O[vi][r]);
+      }
+    }
+
+    // (7) S <- e^{G_last} S + K^T (D v_new), D = e^{G_last - G}: A = K^T rows
+    //     (a transposed read of the K rows), B = D v_new split.
+    {
+      const float G_last = sG[kBlk - 1];
+      const float eg_last = expf(G_last);
+      u32x2 dvh[2], dvl[2];
+#pragma unroll
+      for (int vi = 0; vi < 2; ++vi) {
+        f32x4 dv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dv[r] = expf(G_last - sG[q4 + r]) * vn[vi][r];
+        split4(dv, dvh[vi], dvl[vi]);
+      }
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt) {
+        const u32x2 ka = ds_read_tr16(&sK[(q4 + (r16 >> 2)) * kBStride + 16 * kt + 4 * (r16 & 3)]);
+#pragma unroll
+        for (int vi = 0; vi < 2; ++vi) {
+          f32x4 acc = St[kt][vi];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] *= eg_last;
+          acc = mfma16_bf16(ka, dvh[vi], acc);
+          St[kt][vi] = mfma16_bf16(ka, dvl[vi], acc);
+        }
+      }
+    }
+    __syncthreads();  // the block's LDS tiles are free for the next block
+  }
+
+  // Final state; all zeros for a zero-length sequence (gdn_prefill_ref.py:61-62).
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+    for (int vi = 0; vi < 2; ++vi) {
+      const int vc = 32 * wave + 16 * vi + r16;
+      *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + 16 * kt + q4) = St[kt][vi];
+    }
+}
+
+int block_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
+                 const float *A_log, const uint16_t *a, const float *dt_bias, const uint16_t *b,
+                 const void *cu, int cu64, int num_seqs, int T, int fixed_len, const int *enable,
+                 const Heads &H, float scale, uint16_t *out, float *new_state,
+                 hipStream_t stream, const char *what) {
+  const long long blocks = static_cast<long long>(num_seqs) * H.v;
+  if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "%s: too many sequences for one launch", what);
+  if (blocks == 0) return GDN_OK;
+  hipLaunchKernelGGL(block_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, q, k,
+                     v, state, A_log, a, dt_bias, b, cu, cu64, T, fixed_len, enable, H, scale, out,
+                     new_state);
+  return check_launch(what);
+}
+
+}  // namespace gdn

@@ -141,4 +141,85 @@ __device__ __forceinline__ void unpack8(const u32x4 p, float *x) {
   }
 }
 
+
+// Buffer descriptor (gfx9 word 3 = 0x00020000: raw 32-bit records) over
+// `bytes` bytes at a wave-uniform base.  Loads through it take the base in
+// SGPRs and a 32-bit per-lane byte offset that never changes across chunks,
+// so a prefetch loop needs no address registers: with 64-bit VGPR addresses
+// the compiler recomputed them every chunk and, reusing registers of loads
+// still in flight, had to wait for the newest prefetch set at the loop head.
+// A load at or past `bytes` returns zero: the rows past the end of a chunk.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+// One float at a wave-uniform address, as a vector load issued in program
+// order with the fragments it belongs to.
+__device__ __forceinline__ float buf_load_f32(const float *p) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(p, 4), 0u, 0, 0));
+}
+
+// Gating of token `lane` of a chunk of `len` tokens from `start` (v-head h):
+// g = log decay, beta = sigmoid(b); both loads go through descriptors bounded
+// at the chunk's end and are issued before any arithmetic; padding tokens
+// (lane >= len) get g = beta = 0.
+__device__ __forceinline__ void chunk_gates(int lane, int start, int len, int h, const Heads &H,
+                                            const float *A_log, const uint16_t *a,
+                                            const float *dt_bias, const uint16_t *b, float &gl,
+                                            float &be) {
+  const size_t base = static_cast<size_t>(start) * H.v + h;
+  const uint32_t bytes = static_cast<uint32_t>(len) * static_cast<uint32_t>(H.v) * 2u;
+  const uint32_t off = static_cast<uint32_t>(lane) * static_cast<uint32_t>(H.v) * 2u;
+  const uint16_t ar = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(a + base, bytes), off, 0, 0);
+  const uint16_t br = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(b + base, bytes), off, 0, 0);
+  const float al = A_log[h], db = dt_bias[h];
+  gl = lane < len ? gdn_log_decay(al, bf16_to_f32(ar), db) : 0.f;
+  be = lane < len ? sigmoidf_(bf16_to_f32(br)) : 0.f;
+}
+
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// gfx950 ds_read_b64_tr_b16: within each group of 16 lanes, source lane s
+// reads the four 16-bit values D[s][0..3] at its own LDS address and lane t
+// receives D[4j + (t >> 2)][t & 3], j = 0..3 (pinned by an on-device probe
+// of the instruction).  So with lane s of group g addressing row
+// 8g + 4h + (s >> 2), column c0 + 4 (s & 3) of a row-major tile, lane t
+// gets the tile's column c0 + t at rows 8g + 4h .. 8g + 4h + 3: half h of
+// a transposed MFMA operand fragment.
+__device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t *p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                       (lds_s16x4 *)(const_cast<uint16_t *>(p))));
+}
+
+// v_mfma_f32_16x16x16_bf16: A lane l holds A[l & 15][4*(l >> 4) + e], B lane l
+// holds B[4*(l >> 4) + e][l & 15] (e = 0..3), D as for the 16x16x32 form.  D's
+// rows 4*(l >> 4) + r are exactly B's k-rows, so a result tile feeds the next
+// product as its B operand without leaving the lane.
+__device__ __forceinline__ f32x4 mfma16_bf16(const u32x2 a, const u32x2 b, const f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                    __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+}
+
+// Split of four floats into (hi, lo) bf16 pairs for the K=16 MFMA.
+__device__ __forceinline__ void split4(const f32x4 x, u32x2 &hi, u32x2 &lo) {
+  uint32_t h0, h1, l0, l1;
+  split2(x[0], x[1], h0, l0);
+  split2(x[2], x[3], h1, l1);
+  hi = u32x2{h0, h1};
+  lo = u32x2{l0, l1};
+}
+
+// acc += A * B with both operands split (hi*hi + hi*lo + lo*hi).
+__device__ __forceinline__ f32x4 mfma16_x3(const u32x2 ah, const u32x2 al, const u32x2 bh,
+                                           const u32x2 bl, f32x4 acc) {
+  acc = mfma16_bf16(ah, bh, acc);
+  acc = mfma16_bf16(ah, bl, acc);
+  return mfma16_bf16(al, bh, acc);
+}
+
 }  // namespace gdn

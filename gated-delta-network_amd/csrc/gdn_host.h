@@ -55,6 +55,38 @@ int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, co
                      uint16_t *out, float *new_state, hipStream_t stream, int variant,
                      const char *what);
 int recurrent_num_variants();
+// The variant of recurrent_launch that runs block_launch.
+int recurrent_block_variant();
+
+// The same cases in 16-token blocks of the chunked form (gdn_block.hip): one
+// workgroup per (sequence, v-head).  Arguments as recurrent_launch's.
+int block_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
+                 const float *A_log, const uint16_t *a, const float *dt_bias, const uint16_t *b,
+                 const void *cu, int cu64, int num_seqs, int T, int fixed_len, const int *enable,
+                 const Heads &H, float scale, uint16_t *out, float *new_state,
+                 hipStream_t stream, const char *what);
+
+// Path cost models in microseconds, fitted to graph-replay sweeps of each
+// path on MI355X (sequence count N = 1..256 of equal lengths L = 8..256,
+// multi-token decode B = 1..128 with 4..16 tokens).  L = longest sequence,
+// T = tokens, nt = chunks of 64, g = N * hv (sequence, v-head) groups.
+// Token by token (recurrent kernel): the serial token chain plus VALU work
+// per token and state traffic per group.
+__host__ __device__ inline float cost_by_token(float L, float T, float hv, float g) {
+  return 3.0f + 0.24f * L + 0.003f * T * hv + 0.021f * g;
+}
+// 16-token blocks (block kernel): one workgroup per group, two resident per
+// CU (512 on the chip), ~5 us per block alone on a CU and ~6.3 us two to a CU.
+__host__ __device__ inline float cost_by_block(float L, float g) {
+  const float rounds = ceilf(g / 512.0f), blocks = ceilf(L / 16.0f);
+  return 5.0f + 0.019f * g + rounds * blocks * (g <= 256.0f ? 5.0f : 6.3f);
+}
+// Chunks: fixed launches, per-sequence work up to ~40 sequences and the
+// per-chunk throughput beyond, plus the serial chunk chain of the longest.
+__host__ __device__ inline float cost_by_chunks(float L, float nt, float hv, float g) {
+  const float per_seq = fminf(0.13f * g, 11.0f + 0.081f * g);
+  return 20.0f + fmaxf(per_seq, 0.081f * nt * hv) + 0.5f * ceilf(L / 64.0f);
+}
 
 // One decode step (gdn_decode.hip) with head layout H; variant as in
 // gdn_decode_fwd_variant.  Validates its arguments; messages start with `what`.

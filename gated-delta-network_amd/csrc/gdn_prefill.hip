@@ -124,14 +124,13 @@ static PrefillLayout prefill_layout(int T, int N, const Heads &H) {
 // else the rule in the file header from the chunk count and the longest
 // sequence.
 //
-// Path choice (choose != 0): the token-sequential kernel takes the whole batch
-// when choose == 1 and no sequence is longer than rec_max tokens, or when
-// choose == 2 and the cost model below favours it.  Then every sequence gets
-// zero chunks and the path flag offsets[N + 1] is 1 (else 0).
-// Cost model (microseconds, fitted on MI355X): token by token
-//   0.24 * longest + 0.024 * T + 0.17 * N      (serial tokens, VALU work, state traffic)
-// chunked
-//   20 + 1.05 * ceil(longest / 64) + 1.05 * N  (fixed launches, serial chunks, per-sequence work)
+// Path choice (choose != 0): one sequential kernel (token by token or in
+// 16-token blocks) takes the whole batch when choose == 1 and no sequence is
+// longer than rec_max tokens, or when its cost model (cost_by_token for
+// choose == 2, cost_by_block for 3; gdn_host.h) is at most the chunks'
+// (cost_by_chunks) at the batch's longest sequence and chunk count.  Then
+// every sequence gets zero chunks and the path flag offsets[N + 1] is 1
+// (else 0).
 // ---------------------------------------------------------------------------
 // Maximum of x over the workgroup into *dst (LDS, initially <= every x): a
 // butterfly within each wave, then one LDS atomic per wave (1024 atomics on
@@ -144,32 +143,43 @@ __device__ __forceinline__ void block_max_into(int x, int *dst) {
   }
   if ((threadIdx.x & 63) == 0) atomicMax(dst, x);
 }
+// Sum of x over the workgroup into *dst (LDS, initially 0), the same way.
+__device__ __forceinline__ void block_sum_into(int x, int *dst) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+  if ((threadIdx.x & 63) == 0) atomicAdd(dst, x);
+}
 
 __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int cu64, int N, int T,
                                                               int nt_max, int choose, int rec_max,
-                                                              int form, int4 *chunks, int *offsets) {
+                                                              int hv, int form, int4 *chunks,
+                                                              int *offsets) {
   __shared__ int s_incl[1024];
-  __shared__ int s_longest, s_most_chunks;
+  __shared__ int s_longest, s_most_chunks, s_chunks;
   const int tid = threadIdx.x;
-  if (tid == 0) s_longest = s_most_chunks = 0;
+  if (tid == 0) s_longest = s_most_chunks = s_chunks = 0;
   __syncthreads();
   if (choose != 0) {
-    int longest = 0;
+    int longest = 0, nch = 0;
     for (int s = tid; s < N; s += 1024) {
-      const int len = load_cu(cu, cu64, s + 1, T) - load_cu(cu, cu64, s, T);
+      int len = load_cu(cu, cu64, s + 1, T) - load_cu(cu, cu64, s, T);
+      len = len < 0 ? 0 : len;
       longest = len > longest ? len : longest;
+      nch += (len + kChunk - 1) / kChunk;
     }
     block_max_into(longest, &s_longest);
+    block_sum_into(nch, &s_chunks);
   }
   __syncthreads();
   bool sequential = false;
   if (choose == 1) {
     sequential = s_longest <= rec_max;
-  } else if (choose == 2) {
-    const float L = static_cast<float>(s_longest);
-    const float by_token = 0.24f * L + 0.024f * static_cast<float>(T) + 0.17f * static_cast<float>(N);
-    const float by_chunk = 20.0f + 1.05f * ceilf(L / kChunk) + 1.05f * static_cast<float>(N);
-    sequential = by_token <= by_chunk;
+  } else if (choose >= 2) {
+    const float L = static_cast<float>(s_longest), fhv = static_cast<float>(hv);
+    const float g = static_cast<float>(N) * fhv;
+    const float by_seq = choose == 2 ? cost_by_token(L, static_cast<float>(T), fhv, g)
+                                     : cost_by_block(L, g);
+    sequential = by_seq <= cost_by_chunks(L, static_cast<float>(s_chunks), fhv, g);
   }
   if (tid == 0) offsets[N + 1] = sequential ? 1 : 0;
   long long carry = 0;
@@ -242,45 +252,6 @@ __device__ __forceinline__ int4 chunk_info(const int4 *chunks, int c, int single
                    __builtin_amdgcn_readfirstlane(e.z), __builtin_amdgcn_readfirstlane(e.w));
 }
 
-// Buffer descriptor (gfx9 word 3 = 0x00020000: raw 32-bit records) over
-// `bytes` bytes at a wave-uniform base.  Loads through it take the base in
-// SGPRs and a 32-bit per-lane byte offset that never changes across chunks,
-// so a prefetch loop needs no address registers: with 64-bit VGPR addresses
-// the compiler recomputed them every chunk and, reusing registers of loads
-// still in flight, had to wait for the newest prefetch set at the loop head.
-// A load at or past `bytes` returns zero: the rows past the end of a chunk.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), bytes,
-                                           0x00020000);
-}
-__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
-}
-// One float at a wave-uniform address, as a vector load issued in program
-// order with the fragments it belongs to.
-__device__ __forceinline__ float buf_load_f32(const float *p) {
-  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(p, 4), 0u, 0, 0));
-}
-
-// Gating of token `lane` of a chunk of `len` tokens from `start` (v-head h):
-// g = log decay, beta = sigmoid(b); both loads go through descriptors bounded
-// at the chunk's end and are issued before any arithmetic; padding tokens
-// (lane >= len) get g = beta = 0.
-__device__ __forceinline__ void chunk_gates(int lane, int start, int len, int h, const Heads &H,
-                                            const float *A_log, const uint16_t *a,
-                                            const float *dt_bias, const uint16_t *b, float &gl,
-                                            float &be) {
-  const size_t base = static_cast<size_t>(start) * H.v + h;
-  const uint32_t bytes = static_cast<uint32_t>(len) * static_cast<uint32_t>(H.v) * 2u;
-  const uint32_t off = static_cast<uint32_t>(lane) * static_cast<uint32_t>(H.v) * 2u;
-  const uint16_t ar = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(a + base, bytes), off, 0, 0);
-  const uint16_t br = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(b + base, bytes), off, 0, 0);
-  const float al = A_log[h], db = dt_bias[h];
-  gl = lane < len ? gdn_log_decay(al, bf16_to_f32(ar), db) : 0.f;
-  be = lane < len ? sigmoidf_(bf16_to_f32(br)) : 0.f;
-}
-
-
 // Workgroup id -> (chunk c, v-head h) for the per-(chunk, head) kernels, so
 // that the `ratio` v-heads reading one q/k head of one chunk are dispatched
 // back to back on the same XCD: ids are dealt round-robin over the 8 XCDs,
@@ -299,47 +270,6 @@ __device__ __forceinline__ bool chunk_head_of(int id, int nt, const Heads &H, in
   c = static_cast<int>(P / H.qk);
   h = static_cast<int>(P - static_cast<long long>(c) * H.qk) * H.ratio + r;
   return true;
-}
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// gfx950 ds_read_b64_tr_b16: within each group of 16 lanes, source lane s
-// reads the four 16-bit values D[s][0..3] at its own LDS address and lane t
-// receives D[4j + (t >> 2)][t & 3], j = 0..3 (pinned by an on-device probe
-// of the instruction).  So with lane s of group g addressing row
-// 8g + 4h + (s >> 2), column c0 + 4 (s & 3) of a row-major tile, lane t
-// gets the tile's column c0 + t at rows 8g + 4h .. 8g + 4h + 3: half h of
-// a transposed MFMA operand fragment.
-__device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t *p) {
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                       (lds_s16x4 *)(const_cast<uint16_t *>(p))));
-}
-
-// v_mfma_f32_16x16x16_bf16: A lane l holds A[l & 15][4*(l >> 4) + e], B lane l
-// holds B[4*(l >> 4) + e][l & 15] (e = 0..3), D as for the 16x16x32 form.  D's
-// rows 4*(l >> 4) + r are exactly B's k-rows, so a result tile feeds the next
-// product as its B operand without leaving the lane.
-__device__ __forceinline__ f32x4 mfma16_bf16(const u32x2 a, const u32x2 b, const f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
-                                                    __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
-}
-
-// Split of four floats into (hi, lo) bf16 pairs for the K=16 MFMA.
-__device__ __forceinline__ void split4(const f32x4 x, u32x2 &hi, u32x2 &lo) {
-  uint32_t h0, h1, l0, l1;
-  split2(x[0], x[1], h0, l0);
-  split2(x[2], x[3], h1, l1);
-  hi = u32x2{h0, h1};
-  lo = u32x2{l0, l1};
-}
-
-// acc += A * B with both operands split (hi*hi + hi*lo + lo*hi).
-__device__ __forceinline__ f32x4 mfma16_x3(const u32x2 ah, const u32x2 al, const u32x2 bh,
-                                           const u32x2 bl, f32x4 acc) {
-  acc = mfma16_bf16(ah, bh, acc);
-  acc = mfma16_bf16(ah, bl, acc);
-  return mfma16_bf16(al, bh, acc);
 }
 
 // Transposed [*][64] bf16 tiles in LDS (rows of 128 bytes, no padding) store
@@ -1797,14 +1727,18 @@ void prefill_output_kernel(
   }
 }
 
-// Path choice between the token-sequential kernel (gdn_recurrent.hip) and the
-// chunk pipeline, from a sweep of both on MI355X.  A batch of at most
-// kRecurrentMaxLen tokens runs token by token (one sequence of 64 tokens:
-// 18.6 us vs 25.9 us chunked; of 128: 33.7 vs 27.9 us).  Batches with a mean
-// sequence length above kCandidateMeanLen always take the chunks; the others
-// are decided on the device from their longest sequence (index kernel).
+// Path choice between a sequential kernel and the chunk pipeline, from
+// sweeps of all three paths on MI355X.  A batch of at most kRecurrentMaxLen
+// tokens runs token by token (one sequence of 64 tokens: 20.1 us vs 21.3 us
+// chunked, 25.8 us in blocks).  Otherwise the sequential candidate is the
+// block kernel (gdn_block.hip) or the token-by-token kernel, whichever the
+// cost models (gdn_host.h) rate faster at the mean length, and the device
+// compares its cost model with the chunks' at the batch's longest sequence
+// (index kernel) -- unless the host already knows the chunks win: the
+// candidate's cost at the mean length (a lower bound on the longest) exceeds
+// the chunks' at the largest longest sequence (T) and chunk count (nt_max)
+// possible.
 constexpr int kRecurrentMaxLen = 96;
-constexpr int kCandidateMeanLen = 32;
 
 // Two-segment scan of one sequence (state kernel, SplitScan): three groups of
 // 8 workgroups per v-head, one per CU, so it needs 24 H.v <= 256; the built-in
@@ -1887,28 +1821,42 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   uint16_t *ht = reinterpret_cast<uint16_t *>(ws + L.ht);
   uint16_t *vnt = reinterpret_cast<uint16_t *>(ws + L.vnt);
 
-  // Path choice: the whole batch runs token by token (one launch) or through
-  // the chunk pipeline.  Decided on the host when T and N settle it, else on
-  // the device by the index kernel, which then sets the path flag read by the
-  // token-sequential and state kernels (and leaves the chunk table empty).
-  //   rec_max >= 0 (explicit): token by token iff the longest sequence has at
+  // Path choice: the whole batch runs through one sequential kernel (one
+  // launch) or through the chunk pipeline.  Decided on the host when T and N
+  // settle it, else on the device by the index kernel, which then sets the
+  // path flag read by the sequential and state kernels (and leaves the chunk
+  // table empty).
+  //   rec_max >= 0 (explicit): sequential iff the longest sequence has at
   //                            most rec_max tokens;
   //   rec_max == -2:           always chunks;
-  //   rec_max == -1 (built in): token by token if T <= kRecurrentMaxLen; chunks
-  //                            for one longer sequence or a mean length above
-  //                            kCandidateMeanLen; else the device cost model.
-  int choose = 0;  // 0 chunks, 1 by rec_max, 2 by cost model
+  //   rec_max == -1 (built in): token by token if T <= kRecurrentMaxLen;
+  //                            chunks for one longer sequence; else the cost
+  //                            models (see kRecurrentMaxLen).
+  // The sequential kernel is the recurrent tiling rec_variant (the block
+  // kernel when it names it; built in: the token-by-token tiling, or under
+  // the cost models the faster kind at the mean length).
+  const int block_var = recurrent_block_variant();
+  int seq_var = rec_variant;
+  int choose = 0;  // 0 chunks, 1 by rec_max, 2 token vs chunks, 3 blocks vs chunks
   bool host_sequential = false;
   if (rec_max >= 0) {
     host_sequential = rec_max >= T;
     choose = N > 1 ? 1 : 0;
   } else if (rec_max == -1) {
     host_sequential = T <= kRecurrentMaxLen;
-    choose = (N > 1 && static_cast<long long>(T) <= static_cast<long long>(kCandidateMeanLen) * N) ? 2 : 0;
+    if (!host_sequential && N > 1) {
+      const float fT = static_cast<float>(T), fhv = static_cast<float>(H.v);
+      const float g = static_cast<float>(N) * fhv, mean = ceilf(fT / static_cast<float>(N));
+      const float by_token = cost_by_token(mean, fT, fhv, g), by_block = cost_by_block(mean, g);
+      if (seq_var < 0 && by_block < by_token) seq_var = block_var;
+      const bool blocks = seq_var == block_var;
+      const float seq_lo = blocks ? by_block : by_token;
+      if (seq_lo <= cost_by_chunks(fT, static_cast<float>(L.nt_max), fhv, g)) choose = blocks ? 3 : 2;
+    }
   }
   if (host_sequential)
     return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
-                            nullptr, H, scale, output, new_state, stream, rec_variant,
+                            nullptr, H, scale, output, new_state, stream, seq_var,
                             "gdn_prefill_fwd");
   // One sequence is [0, T) by the cu_seqlens contract: its chunks follow
   // from T, and the kernels compute them instead of reading a table.
@@ -1928,12 +1876,12 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   }
   if (single_T < 0) {
     hipLaunchKernelGGL(prefill_index_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, cu64, N, T,
-                       L.nt_max, choose, rec_max, form, chunks, offsets);
+                       L.nt_max, choose, rec_max, H.v, form, chunks, offsets);
     if ((rc = check_launch("gdn_prefill_fwd(index)"))) return rc;
   }
   if (choose != 0) {
     rc = recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
-                          offsets + N + 1, H, scale, output, new_state, stream, rec_variant,
+                          offsets + N + 1, H, scale, output, new_state, stream, seq_var,
                           "gdn_prefill_fwd");
     if (rc) return rc;
   }

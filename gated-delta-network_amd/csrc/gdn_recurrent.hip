@@ -221,7 +221,10 @@ void launch_rec(long long groups, hipStream_t stream, const uint16_t *q, const u
 
 }  // namespace
 
-int recurrent_num_variants() { return kNumRecVariants; }
+// Variants 0 .. kNumRecVariants - 1: the row tilings above; kNumRecVariants:
+// the 16-token block kernel (gdn_block.hip).
+int recurrent_num_variants() { return kNumRecVariants + 1; }
+int recurrent_block_variant() { return kNumRecVariants; }
 
 // Built-in tiling from a sweep on MI355X: few (sequence, head) groups -> the
 // smallest row blocks (the serial token loop is spread over the most waves);
@@ -240,7 +243,10 @@ int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, co
                      const char *what) {
   const long long groups = static_cast<long long>(num_seqs) * H.v;
   if (variant < 0) variant = recurrent_default_variant(groups);
-  if (variant >= kNumRecVariants)
+  if (variant == kNumRecVariants)
+    return block_launch(q, k, v, state, A_log, a, dt_bias, b, cu, cu64, num_seqs, T, fixed_len,
+                        enable, H, scale, out, new_state, stream, what);
+  if (variant > kNumRecVariants)
     return fail(GDN_ERR_INVALID, "%s: recurrent tiling %d out of range", what, variant);
   const RecVariant rv = kRecVariants[variant];
   if (groups * (kDV / (4 * rv.waves * rv.passes)) > 0x7fffffffLL)
@@ -309,10 +315,19 @@ static int multi_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
   }
   if (overlaps(output, out_bytes, new_state, state_bytes))
     return fail(GDN_ERR_INVALID, "%s: output overlaps new_state", what);
-  // One token per row is the plain decode step, whose kernel is tuned for it.
+  // One token per row is the plain decode step, whose kernel is tuned for it;
+  // more go token by token or in 16-token blocks, whichever the cost models
+  // (gdn_host.h) rate faster (B = 64: 4 tokens 18.8 vs 19.5 us, 8 tokens
+  // 26.3 vs 19.9 us, 16 tokens 41.2 vs 20.6 us).
   if (tokens == 1 && variant == -1)
     return decode_launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
                          stream, -1, H, what);
+  if (variant == -1) {
+    const float L = static_cast<float>(tokens), fhv = static_cast<float>(H.v);
+    const float g = static_cast<float>(batch) * fhv;
+    if (cost_by_block(L, g) < cost_by_token(L, static_cast<float>(total), fhv, g))
+      variant = recurrent_block_variant();
+  }
   return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, nullptr, 0, batch,
                           static_cast<int>(total), tokens, nullptr, H, scale, output, new_state,
                           static_cast<hipStream_t>(stream), variant, what);

@@ -144,7 +144,7 @@ def _multi_args(**over):
     (dict(batch=-1), "batch"),
     (dict(v=None), "null"),
     (dict(scale=0.0), "scale"),
-    (dict(variant=10), "variant"),
+    (dict(variant=11), "variant"),
     (dict(variant=-2), "variant"),
     (dict(new_state=(16 << 20) + 8), "aligned"),
     # output is [B*T, 8, 128] bf16 = 12 KiB: ending inside v
@@ -165,7 +165,7 @@ def test_decode_multi_zero_batch_is_a_no_op():
 
 @pytest.mark.parametrize("tuning, needle", [
     ((-1, -3, -1), "recurrent_max_len"),
-    ((-1, -1, 10), "recurrent tiling"),
+    ((-1, -1, 11), "recurrent tiling"),
     ((4, -1, -1), "variant"),
     ((-2, -1, -1), "variant"),
 ])

@@ -109,16 +109,40 @@ def test_routing_zero_length_sequences_get_zero_state(cuda_device):
         _check(out, ns, inp)
 
 
-def _expected_sequential(lens):
-    """The built-in path choice of gdn_prefill_fwd (gdn_prefill.hip), restated."""
+def _cost_by_token(L, T, hv, g):
+    return 3 + 0.24 * L + 0.003 * T * hv + 0.021 * g
+
+
+def _cost_by_block(L, g):
+    return 5 + 0.019 * g + math.ceil(g / 512) * math.ceil(L / 16) * (5 if g <= 256 else 6.3)
+
+
+def _cost_by_chunks(L, nt, hv, g):
+    return 20 + max(min(0.13 * g, 11 + 0.081 * g), 0.081 * nt * hv) + 0.5 * math.ceil(L / 64)
+
+
+def _expected_path(lens, hv=8):
+    """The built-in path choice of gdn_prefill_fwd (gdn_prefill.hip, cost
+    models of gdn_host.h), restated: "token", "block" or "chunks"."""
     T, N, L = sum(lens), len(lens), max(lens)
     if T <= 96:
-        return True
-    if N == 1 or T > 32 * N:
-        return False
-    by_token = 0.24 * L + 0.024 * T + 0.17 * N
-    by_chunk = 20.0 + 1.05 * math.ceil(L / 64) + 1.05 * N
-    return by_token <= by_chunk
+        return "token"
+    if N == 1:
+        return "chunks"
+    g, mean = N * hv, math.ceil(T / N)
+    by_token, by_block = _cost_by_token(mean, T, hv, g), _cost_by_block(mean, g)
+    kind = "block" if by_block < by_token else "token"
+    if min(by_token, by_block) > _cost_by_chunks(T, O.max_chunks(T, N), hv, g):
+        return "chunks"
+    nt = sum(math.ceil(n / 64) for n in lens)
+    seq = _cost_by_block(L, g) if kind == "block" else _cost_by_token(L, T, hv, g)
+    return kind if seq <= _cost_by_chunks(L, nt, hv, g) else "chunks"
+
+
+def _expected_multi_kind(B, T, hv=8):
+    """The built-in kernel of gdn_decode_multi_fwd for T > 1 tokens per row."""
+    g = B * hv
+    return "block" if _cost_by_block(T, g) < _cost_by_token(T, B * T, hv, g) else "token"
 
 
 def _path_flag(dev, T, N):
@@ -135,26 +159,30 @@ def _lens_1500():
     return lens
 
 
-# Batches the host leaves to the device (mean length <= 32, T > 96).
+# Batches the host leaves to the device (T > 96, N > 1), with the path the
+# cost models pick: token by token, 16-token blocks or chunks.
 DEVICE_CHOICE = {
-    "256x1": [1] * 256,
-    "64x16": [16] * 64,
-    "mixed40": [3, 17, 96, 0, 40] * 8,
-    "1500": _lens_1500(),
-    "10x2+200": [2] * 10 + [200],
+    "256x1": ([1] * 256, "token"),
+    "64x16": ([16] * 64, "block"),
+    "mixed40": ([3, 17, 96, 0, 40] * 8, "block"),
+    "1500": (_lens_1500(), "token"),
+    "10x2+200": ([2] * 10 + [200], "chunks"),
+    "16x8": ([8] * 16, "token"),
+    "32x128": ([128] * 32, "block"),
+    "3x40+300": ([40] * 3 + [300], "chunks"),
 }
 
 
 @pytest.mark.parametrize("name", list(DEVICE_CHOICE))
 def test_device_path_choice(cuda_device, name):
-    lens = DEVICE_CHOICE[name]
+    lens, want = DEVICE_CHOICE[name]
     T, N = sum(lens), len(lens)
-    want = _expected_sequential(lens)
-    print(f"device path choice {name}: T={T} N={N} sequential={want}", flush=True)
+    assert _expected_path(lens) == want
+    print(f"device path choice {name}: T={T} N={N} path={want}", flush=True)
     inp = O.make_prefill_inputs(lens, seed=15)
     out, ns = _prefill(_to_dev(inp, cuda_device), cuda_device)
-    assert _path_flag(cuda_device, T, N) == int(want)
-    _check(out, ns, inp, tight=want)
+    assert _path_flag(cuda_device, T, N) == int(want != "chunks")
+    _check(out, ns, inp, tight=want == "token")
 
 
 def test_recurrent_tilings_are_identical(cuda_device):
@@ -195,12 +223,12 @@ def _decode_multi(d, B, T, dev, in_place=False, variant=-1):
     return out, ns
 
 
-@pytest.mark.parametrize("B, T", [(1, 2), (3, 5), (16, 4), (64, 2), (64, 8)])
+@pytest.mark.parametrize("B, T", [(1, 2), (3, 5), (16, 4), (64, 2), (64, 8), (32, 16)])
 def test_multi_token_decode_matches_oracle(cuda_device, B, T):
     print(f"multi-token decode B={B} T={T}", flush=True)
     inp, dec = _multi_inputs(B, T, seed=20 + B + T)
     out, ns = _decode_multi(_to_dev(dec, cuda_device), B, T, cuda_device)
-    _check(out.reshape(B * T, 8, 128), ns, inp, tight=True)
+    _check(out.reshape(B * T, 8, 128), ns, inp, tight=_expected_multi_kind(B, T) == "token")
 
 
 def test_multi_token_decode_equals_successive_steps(cuda_device):
@@ -244,3 +272,61 @@ def test_multi_token_decode_tilings_are_identical(cuda_device):
         o, s = _decode_multi(d, B, T, cuda_device, variant=var)
         assert torch.equal(o, ref_o) and torch.equal(s, ref_s), f"tiling {var}"
     _check(ref_o.reshape(B * T, 8, 128), ref_s, inp, tight=True)
+
+
+# ---------------------------------------------------------------------------
+# the 16-token block kernel (gdn_block.hip; recurrent variant BLOCK)
+# ---------------------------------------------------------------------------
+
+BLOCK = 10
+
+
+def _state_err(ns, inp):
+    _, s_ref = O.prefill_seq_c(**inp)
+    s = ns.cpu().numpy()
+    return float(np.abs(s - s_ref).max() / max(np.abs(s_ref).max(), 1e-30))
+
+
+@pytest.mark.parametrize("lens, with_state", SHORT_CASES + [([17, 31, 32, 33], True)])
+def test_block_kernel_short_prefill_matches_oracle(cuda_device, lens, with_state):
+    print(f"block kernel prefill lens={lens} state={with_state}", flush=True)
+    inp = O.make_prefill_inputs(lens, seed=60 + len(lens), with_state=with_state)
+    out, ns = _prefill(_to_dev(inp, cuda_device), cuda_device, recurrent_max_len=ALL_SEQUENTIAL,
+                       recurrent_variant=BLOCK)
+    print(f"  state error {_state_err(ns, inp):.2e} of max|S|", flush=True)
+    _check(out, ns, inp)
+
+
+@pytest.mark.parametrize("B, T", [(1, 2), (3, 5), (16, 4), (64, 8), (4, 33), (2, 16), (2, 17)])
+def test_block_kernel_multi_token_decode(cuda_device, B, T):
+    print(f"block kernel multi-token decode B={B} T={T}", flush=True)
+    inp, dec = _multi_inputs(B, T, seed=70 + B + T)
+    out, ns = _decode_multi(_to_dev(dec, cuda_device), B, T, cuda_device, variant=BLOCK)
+    print(f"  state error {_state_err(ns, inp):.2e} of max|S|", flush=True)
+    _check(out.reshape(B * T, 8, 128), ns, inp)
+
+
+def test_block_kernel_extreme_gates_in_place_and_no_state(cuda_device):
+    # Gates around softplus' threshold, beta saturated at 0 and 1, near-unit
+    # and underflowing decays (as the chunk pipeline's extreme-gate test).
+    lens = [40, 16, 100]
+    inp = O.make_prefill_inputs(lens, seed=71)
+    rng = np.random.default_rng(71)
+    T = sum(lens)
+    a_h = np.array([30.0, -30.0, 20.0, 0.0, 19.5, -5.0, 5.0, 1.0], np.float32)
+    b_h = np.array([-40.0, 40.0, 0.0, 8.0, -8.0, 1.0, -1.0, 0.0], np.float32)
+    inp["a"][:] = O.bf16_round(a_h[None, :] + rng.normal(0, 0.5, (T, 8)).astype(np.float32))
+    inp["b"][:] = O.bf16_round(b_h[None, :] + rng.normal(0, 0.5, (T, 8)).astype(np.float32))
+    inp["A_log"][:] = np.array([-10.0, 2.7, 0.0, -20.0, 1.0, 0.5, 0.1, 2.0], np.float32)
+    print("block kernel extreme gates", flush=True)
+    d = _to_dev(inp, cuda_device)
+    out, ns = _prefill(d, cuda_device, recurrent_max_len=ALL_SEQUENTIAL, recurrent_variant=BLOCK)
+    assert torch.isfinite(out.float()).all() and torch.isfinite(ns).all()
+    _check(out, ns, inp)
+    oi, si = _prefill(d, cuda_device, in_place=True, recurrent_max_len=ALL_SEQUENTIAL,
+                      recurrent_variant=BLOCK)
+    assert torch.equal(oi, out) and torch.equal(si, ns)
+    inp["state"] = None
+    o0, s0 = _prefill(_to_dev(inp, cuda_device), cuda_device, recurrent_max_len=ALL_SEQUENTIAL,
+                      recurrent_variant=BLOCK)
+    _check(o0, s0, inp)
