@@ -70,7 +70,8 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, *, va
     tensor or None; output [B,T,8,128] bf16; new_state [B,8,128,128] f32.
     ``new_state`` may be ``state`` itself (in-place update).  ``variant``
     picks a tiling (gdn_decode_fwd_variant for T=1, gdn_decode_multi_fwd for
-    T>1); the default is the built-in one.
+    T>1: 0..9 token by token, 10 the 16-token block kernel); the default is
+    the built-in one.
     """
     lib = _lib.load()
     four = isinstance(q, torch.Tensor) and q.dim() == 4

@@ -123,9 +123,11 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
     sequence (0 and -1 take it from 32 chunks on).  ``workspace``: a caller-owned uint8
     buffer (``alloc_workspace``) used instead of the per-stream cache.
     ``recurrent_max_len``: a batch whose longest sequence has at most this
-    many tokens runs token by token instead of through the chunks (-1
-    built-in, -2 never);
-    ``recurrent_variant``: that kernel's row tiling (gdn_prefill_fwd_tuned).
+    many tokens runs through the sequential kernel instead of the chunks (-1
+    built-in: token by token, in 16-token blocks or chunks by fitted cost
+    models; -2 never);
+    ``recurrent_variant``: the sequential kernel (gdn_prefill_fwd_tuned):
+    0..9 a token-by-token row tiling, 10 the 16-token block kernel.
     """
     lib = _lib.load()
     T, N, dev, heads = _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output,

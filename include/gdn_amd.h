@@ -79,8 +79,8 @@ int gdn_decode_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 
 /*
  * Decode of `tokens` >= 1 consecutive tokens per batch row (multi-token /
  * speculative decode): for each row, the T = 1 step of gdn_decode_fwd applied
- * token after token, the state carried in registers between tokens and written
- * once at the end.  No counterpart in the reference, whose decode asserts
+ * token after token, the state read once, carried on chip between tokens and
+ * written once at the end.  No counterpart in the reference, whose decode asserts
  * T == 1 (reference/gdn_decode_ref.py:32-36); it extends the same entry point
  * kernel(q, k, v, state, ...) of solutions/gdn_decode_qk4_v8_d128_k_last/
  * solution/triton/kernel.py:85 to T > 1, and equals gdn_prefill_fwd on `batch`
@@ -92,7 +92,12 @@ int gdn_decode_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 
  *
  * variant: row tiling of the token-sequential kernel (0..9: 4, 8, 16, 8, 16,
  * 32, 16, 64, 32, 64 rows per workgroup with 64, 128, 256, 64, 128, 256, 64,
- * 256, 64, 64 threads), -1 = built-in (tokens == 1 then runs gdn_decode_fwd).
+ * 256, 64, 64 threads; every tiling gives identical results), 10 = the block
+ * kernel (one workgroup per row and v-head applies the tokens in blocks of 16
+ * in the chunked form on MFMA; same function within the stated tolerances,
+ * not bit for bit), -1 = built-in: tokens == 1 runs gdn_decode_fwd, more run
+ * token by token or in blocks by a cost model fitted on MI355X (blocks from
+ * about 6 tokens at 64 rows, 12 at 16 rows).
  */
 int gdn_decode_multi_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                          const float *state, const float *A_log, const gdn_bf16 *a,
@@ -147,14 +152,19 @@ size_t gdn_prefill_workspace_bytes(int total_tokens, int num_seqs);
  * sequence gets an all-zero new_state, as the reference does.  new_state may
  * alias state; output must not overlap any input.
  *
- * The batch takes one of two paths: every sequence token by token with the
- * state in registers (one launch), or all through the chunk-64 pipeline.  A
- * batch of at most 96 tokens goes token by token; one with a mean sequence
- * length above 32 tokens through the chunks; for the others (many short
- * sequences) the device compares a cost model of both paths, evaluated from
- * the longest sequence, T and N.  Results agree within the stated tolerance
- * either way (the reference measured the same crossover between its
- * sequential scan and chunked kernels, OPTIMIZATION_LOG.md:79,170-184).
+ * The batch takes one of three paths: every sequence token by token with the
+ * state in registers (one launch), every sequence in 16-token blocks with the
+ * state in MFMA tiles (one launch: the block kernel of gdn_decode_multi_fwd),
+ * or all through the chunk-64 pipeline.  A batch of at most 96 tokens goes
+ * token by token and one sequence through the chunks; for the others the
+ * host picks the faster sequential kind at the mean length and, unless the
+ * chunks win for any longest sequence, the device compares cost models of
+ * it and of the chunks from the longest sequence, the chunk count, T and N
+ * (fitted on MI355X: many short-to-medium sequences go in blocks, e.g. 64 x
+ * 256 tokens 115 us vs 171 us through the chunks).  Results agree within the
+ * stated tolerance either way (the reference measured the same crossover
+ * between its sequential scan and chunked kernels,
+ * OPTIMIZATION_LOG.md:79,170-184).
  */
 int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                     const float *state, const float *A_log, const gdn_bf16 *a,
@@ -198,9 +208,12 @@ int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16
  *   state_tiling       the form, as the variant of gdn_prefill_fwd_variant
  *                      (-1 built-in)
  *   recurrent_max_len  a batch whose longest sequence has at most this many
- *                      tokens runs token by token; -1 = built-in, -2 = never
- *                      (always chunked)
- *   recurrent_tiling   as the variant of gdn_decode_multi_fwd (-1 built-in)
+ *                      tokens runs through the sequential kernel; -1 =
+ *                      built-in, -2 = never (always chunked)
+ *   recurrent_tiling   the sequential kernel, as the variant of
+ *                      gdn_decode_multi_fwd (10 = blocks; -1 built-in: token
+ *                      by token, or under the built-in path choice the kind
+ *                      it picks)
  */
 int gdn_prefill_fwd_tuned(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                           const float *state, const float *A_log, const gdn_bf16 *a,

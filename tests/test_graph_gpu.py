@@ -252,3 +252,60 @@ def test_prefill_graph_replays_two_segment_scan(cuda_device):
         o_ref, s_ref = O.prefill_seq_c(**inp)
         assert_output_close(o_g.float().cpu().numpy(), o_ref)
         assert_state_close(s_g.cpu().numpy(), s_ref)
+
+
+# Same T = 1024 and N = 64 for every replay; the device picks the path per
+# replay from the new cu_seqlens: 16-token blocks or the chunks.
+PATH_REPLAYS = [
+    ([16] * 64, 1),
+    ([1000] + [0] * 62 + [24], 0),
+    ([15] * 63 + [79], 1),
+    ([0] * 63 + [1024], 0),
+]
+
+
+def test_prefill_graph_replays_follow_the_device_path_choice(cuda_device):
+    dev = cuda_device
+    T, N = 1024, 64
+    print(f"prefill graph device path choice T={T} N={N}", flush=True)
+    st = _prefill_static(T, N, dev)
+    inp = O.make_prefill_inputs(PATH_REPLAYS[0][0], seed=60)
+    _fill_prefill(st, inp)
+    scale = float(inp["scale"])
+    ws = prefill.alloc_workspace(T, N, dev)
+    flag_at = (O.max_chunks(T, N) * 16 + 255) // 256 * 256 + (N + 1) * 4
+    out = torch.empty((T, 8, 128), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((N, 8, 128, 128), dtype=torch.float32, device=dev)
+
+    def call(o, s):
+        prefill.kernel(st["q"], st["k"], st["v"], st["state"], st["A_log"], st["a"],
+                       st["dt_bias"], st["b"], st["cu_seqlens"], scale, o, s, workspace=ws)
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        call(out, ns)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(out, ns)
+    torch.cuda.synchronize()
+
+    for rep, (lens, want_flag) in enumerate(PATH_REPLAYS[1:] + PATH_REPLAYS[:1]):
+        print(f"  replay {rep} longest={max(lens)}", flush=True)
+        inp = O.make_prefill_inputs(lens, seed=61 + rep)
+        _fill_prefill(st, inp)
+        g.replay()
+        torch.cuda.synchronize()
+        flag = int(ws[flag_at:flag_at + 4].cpu().numpy().view(np.int32)[0])
+        assert flag == want_flag, f"replay {rep}: path flag {flag}"
+        o_g, s_g = out.clone(), ns.clone()
+        o_e = torch.empty_like(out)
+        s_e = torch.empty_like(ns)
+        call(o_e, s_e)
+        torch.cuda.synchronize()
+        assert torch.equal(o_g, o_e), f"replay {rep}: output differs from the eager call"
+        assert torch.equal(s_g, s_e), f"replay {rep}: state differs from the eager call"
+        o_ref, s_ref = O.prefill_seq_c(**inp)
+        assert_output_close(o_g.float().cpu().numpy(), o_ref)
+        assert_state_close(s_g.cpu().numpy(), s_ref)
