@@ -33,7 +33,7 @@ namespace gdn {
 
 constexpr int kBlk = 16;        // tokens per block
 constexpr int kBStride = 136;   // bf16 row stride of the q/k/v block tiles
-constexpr int kBStrideA = 17;   // f32 row stride of the 16x16 A and Ti tiles
+constexpr int kBStrideA = 20;   // f32 row stride of the 16x16 A^T and Ti tiles
 constexpr int kBStrideW = 132;  // f32 row stride of W
 constexpr int kBStrideP = 24;   // bf16 row stride of P
 
@@ -48,11 +48,11 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
   __shared__ __align__(16) uint16_t sQ[kBlk * kBStride];
   __shared__ __align__(16) uint16_t sK[kBlk * kBStride];
   __shared__ __align__(16) uint16_t sV[kBlk * kBStride];
-  __shared__ __align__(16) float sA[kBlk * kBStrideA];
+  __shared__ __align__(16) float sAt[kBlk * kBStrideA];
   __shared__ __align__(16) float sTi[kBlk * kBStrideA];
   __shared__ __align__(16) float sW[kBlk * kBStrideW];
   __shared__ __align__(16) uint16_t sP[kBlk * kBStrideP];
-  __shared__ float sG[kBlk], sBeta[kBlk];
+  __shared__ float sG[2][kBlk], sBeta[2][kBlk];  // by block parity
 
   if (enable != nullptr && *enable == 0) return;  // the batch went through the chunks
   const int h = blockIdx.x % H.v, s = blockIdx.x / H.v;
@@ -118,41 +118,46 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
     x.a = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(a + g0, gbytes), goff, 0, 0);
     x.b = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(b + g0, gbytes), goff, 0, 0);
   };
+  // Gating of a block of n tokens (one wave, token `lane`): log decay,
+  // in-block cumsum G and beta into the LDS buffer of the block's parity.
+  auto gate_block = [&](int n, uint16_t a_raw, uint16_t b_raw, int par) {
+    const float gl = lane < n ? -rate * softplus20(bf16_to_f32(a_raw) + dtb) : 0.f;
+    const float be = lane < n ? sigmoidf_(bf16_to_f32(b_raw)) : 0.f;
+    float G = gl;
+#pragma unroll
+    for (int off = 1; off < kBlk; off <<= 1) {
+      const float y = __shfl_up(G, off, kBlk);
+      if (r16 >= off) G += y;
+    }
+    if (lane < kBlk) {
+      sG[par][lane] = G;
+      sBeta[par][lane] = be;
+    }
+  };
   BlockIn cur;
-  if (len > 0) load_block(0, cur);
+  if (len > 0) {
+    load_block(0, cur);
+    if (wave == 0) gate_block(len < kBlk ? len : kBlk, cur.a, cur.b, 0);
+  }
   for (int t0 = 0; t0 < len; t0 += kBlk) {
     const int n = len - t0 < kBlk ? len - t0 : kBlk;
     const int start = bos + t0;
+    const int par = (t0 / kBlk) & 1;
+    const float *bG = sG[par], *bBeta = sBeta[par];
 
-    // (1) this block's q, k, v rows into LDS; gating and the in-block cumsum
-    //     (wave 0); the next block's inputs requested.
-    {
-      *reinterpret_cast<u32x4 *>(&sQ[row * kBStride + c16 * 8]) = cur.q;
-      *reinterpret_cast<u32x4 *>(&sK[row * kBStride + c16 * 8]) = cur.k;
-      *reinterpret_cast<u32x4 *>(&sV[row * kBStride + c16 * 8]) = cur.v;
-      const uint16_t a_raw = cur.a, b_raw = cur.b;
-      if (t0 + kBlk < len) load_block(t0 + kBlk, cur);
-      if (wave == 0) {
-        const float gl = lane < n ? -rate * softplus20(bf16_to_f32(a_raw) + dtb) : 0.f;
-        const float be = lane < n ? sigmoidf_(bf16_to_f32(b_raw)) : 0.f;
-        float G = gl;
-#pragma unroll
-        for (int off = 1; off < kBlk; off <<= 1) {
-          const float y = __shfl_up(G, off, kBlk);
-          if (r16 >= off) G += y;
-        }
-        if (lane < kBlk) {
-          sG[lane] = G;
-          sBeta[lane] = be;
-        }
-      }
-    }
+    // (1) this block's q, k, v rows into LDS (its gates are there already);
+    //     the next block's inputs requested.
+    *reinterpret_cast<u32x4 *>(&sQ[row * kBStride + c16 * 8]) = cur.q;
+    *reinterpret_cast<u32x4 *>(&sK[row * kBStride + c16 * 8]) = cur.k;
+    *reinterpret_cast<u32x4 *>(&sV[row * kBStride + c16 * 8]) = cur.v;
+    if (t0 + kBlk < len) load_block(t0 + kBlk, cur);
     __syncthreads();
 
-    // (2) A = strictly-lower(beta_i e^{G_i - G_j} K K^T) (wave 0) and
-    //     P = mask_{j<=i}(e^{G_i - G_j} Q K^T) (wave 1), 16x16 each.
-    if (wave < 2) {
-      const uint16_t *sX = wave == 0 ? sK : sQ;
+    // (2) A = strictly-lower(beta_i e^{G_i - G_j} K K^T) (wave 0), stored
+    //     transposed: sAt[j][i] = A_ij.
+    //     G_i - G_j <= 0 wherever an entry is kept (g <= 0); the clamp keeps
+    //     the discarded entries finite.
+    auto masked_qk = [&](const uint16_t *sX, f32x4 &e) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
@@ -160,66 +165,94 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
         const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[r16 * kBStride + 32 * kk + kg]);
         acc = mfma_bf16(af, bf, acc);
       }
+      const float Gj = bG[r16];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) e[r] = expf(fminf(bG[q4 + r] - Gj, 0.f)) * acc[r];
+    };
+    if (wave == 0) {
+      f32x4 e;
+      masked_qk(sK, e);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = q4 + r, j = r16;
-        if (wave == 0) {
-          sA[i * kBStrideA + j] = i > j ? sBeta[i] * expf(sG[i] - sG[j]) * acc[r] : 0.f;
-        } else {
-          const float p = (j <= i && i < n) ? expf(sG[i] - sG[j]) * acc[r] : 0.f;
-          sP[i * kBStrideP + j] = f32_to_bf16(p);
-        }
+        sAt[j * kBStrideA + i] = i > j ? bBeta[i] * e[r] : 0.f;
       }
     }
     __syncthreads();
 
-    // (3) Ti = (I + A)^-1 by forward substitution, lane j < 16 of wave 0
-    //     solving column j.
-    if (wave == 0 && lane < kBlk) {
-      float x[kBlk];
+    // (3) wave 0: Ti = (I + A)^-1 by column-oriented forward substitution,
+    //     lane j < 16 solving column j (each solved x_m is applied to all
+    //     later rows at once, so the serial chain is one FMA per row);
+    //     wave 1: P = mask_{j<=i}(e^{G_i - G_j} Q K^T); wave 2: the next
+    //     block's gates.  Then every wave splits its state for step (5).
+    if (wave == 0) {
+      if (lane < kBlk) {
+        float x[kBlk];
 #pragma unroll
-      for (int i = 0; i < kBlk; ++i) {
-        const float *arow = &sA[i * kBStrideA];
-        float s0 = (i == lane) ? 1.f : 0.f, s1 = 0.f;
+        for (int i = 0; i < kBlk; ++i) x[i] = i == lane ? 1.f : 0.f;
 #pragma unroll
-        for (int m = 0; m < i; m += 2) {
-          s0 -= arow[m] * x[m];
-          if (m + 1 < i) s1 -= arow[m + 1] * x[m + 1];
+        for (int m = 0; m < kBlk - 1; ++m) {
+          const float xm = x[m];
+#pragma unroll
+          for (int i = m + 1; i < kBlk; ++i) x[i] -= sAt[m * kBStrideA + i] * xm;
         }
-        x[i] = s0 + s1;
-      }
 #pragma unroll
-      for (int i = 0; i < kBlk; ++i) sTi[i * kBStrideA + lane] = x[i];
+        for (int i = 0; i < kBlk; ++i) sTi[i * kBStrideA + lane] = x[i];
+      }
+    } else if (wave == 1) {
+      f32x4 e;
+      masked_qk(sQ, e);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = q4 + r, j = r16;
+        sP[i * kBStrideP + j] = f32_to_bf16((j <= i && i < n) ? e[r] : 0.f);
+      }
+    } else if (wave == 2 && t0 + kBlk < len) {
+      const int n1 = len - t0 - kBlk < kBlk ? len - t0 - kBlk : kBlk;
+      gate_block(n1, cur.a, cur.b, par ^ 1);
     }
+    // The state split for the K=32 products of step (5): slot 8 g + e of
+    // k-block kk is k = 32 kk + 4 g + e (e < 4) or 32 kk + 16 + 4 g + e - 4
+    // (the k of two state tiles), the same map for the A operands.
+    u32x4 Sh[4][2], Sl[4][2];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int vi = 0; vi < 2; ++vi) {
+        u32x2 h0, l0, h1, l1;
+        split4(St[2 * kk][vi], h0, l0);
+        split4(St[2 * kk + 1][vi], h1, l1);
+        Sh[kk][vi] = u32x4{h0[0], h0[1], h1[0], h1[1]};
+        Sl[kk][vi] = u32x4{l0[0], l0[1], l1[0], l1[1]};
+      }
     __syncthreads();
 
     // (4) W = Ti diag(beta e^G) K for the features 32 wave .. +31 (-> LDS, f32)
-    //     and U = Ti diag(beta) V for this wave's columns (registers).  A
-    //     operand: Ti's row r16, tokens q4..q4+3, scaled and split; B operand:
-    //     4 consecutive tokens of one feature, a transposed read of the rows.
+    //     and U = Ti diag(beta) V for this wave's columns (registers).  One
+    //     K=32 product each: slots 8 g + e carry Ti's hi part (e < 4) and lo
+    //     part (e >= 4) of token 4 g + e mod 4 against the same K (V) entry
+    //     twice, a transposed read of the rows.
     f32x4 U[2];
     {
-      const f32x4 ti = {sTi[r16 * kBStrideA + q4], sTi[r16 * kBStrideA + q4 + 1],
-                        sTi[r16 * kBStrideA + q4 + 2], sTi[r16 * kBStrideA + q4 + 3]};
+      const f32x4 ti = *reinterpret_cast<const f32x4 *>(&sTi[r16 * kBStrideA + q4]);
       f32x4 tw, tu;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float be = sBeta[q4 + e];
+        const float be = bBeta[q4 + e];
         tu[e] = ti[e] * be;
-        tw[e] = ti[e] * be * expf(sG[q4 + e]);
+        tw[e] = ti[e] * be * expf(bG[q4 + e]);
       }
       u32x2 twh, twl, tuh, tul;
       split4(tw, twh, twl);
       split4(tu, tuh, tul);
+      const u32x4 twa = {twh[0], twh[1], twl[0], twl[1]}, tua = {tuh[0], tuh[1], tul[0], tul[1]};
 #pragma unroll
       for (int ft = 0; ft < 2; ++ft) {
         const int c0 = 32 * wave + 16 * ft;  // feature tile of W / column tile of U
         const u32x2 kb = ds_read_tr16(&sK[(q4 + (r16 >> 2)) * kBStride + c0 + 4 * (r16 & 3)]);
         const u32x2 vb = ds_read_tr16(&sV[(q4 + (r16 >> 2)) * kBStride + c0 + 4 * (r16 & 3)]);
-        f32x4 w = mfma16_bf16(twh, kb, f32x4{0.f, 0.f, 0.f, 0.f});
-        w = mfma16_bf16(twl, kb, w);
-        f32x4 u = mfma16_bf16(tuh, vb, f32x4{0.f, 0.f, 0.f, 0.f});
-        U[ft] = mfma16_bf16(tul, vb, u);
+        const f32x4 w = mfma_bf16(twa, u32x4{kb[0], kb[1], kb[0], kb[1]}, f32x4{0.f, 0.f, 0.f, 0.f});
+        U[ft] = mfma_bf16(tua, u32x4{vb[0], vb[1], vb[0], vb[1]}, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
         for (int r = 0; r < 4; ++r) sW[(q4 + r) * kBStrideW + c0 + r16] = w[r];
       }
@@ -227,28 +260,24 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
     __syncthreads();
 
     // (5) v_new = U - W S^T for this wave's columns (W and S split: three
-    //     products per k-tile).  The state is split here, after the
-    //     intra-block work, so that at the first block its loads overlap it.
-    u32x2 Sh[8][2], Sl[8][2];
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
-#pragma unroll
-      for (int vi = 0; vi < 2; ++vi) split4(St[kt][vi], Sh[kt][vi], Sl[kt][vi]);
+    //     K=32 products per 32 k).
     f32x4 vn[2];
     {
       f32x4 P0[2], P1[2], P2[2];
 #pragma unroll
       for (int vi = 0; vi < 2; ++vi) P0[vi] = P1[vi] = P2[vi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kt = 0; kt < 8; ++kt) {
-        const f32x4 wf = *reinterpret_cast<const f32x4 *>(&sW[r16 * kBStrideW + 16 * kt + q4]);
-        u32x2 wh, wl;
-        split4(wf, wh, wl);
+      for (int kk = 0; kk < 4; ++kk) {
+        const float *wrow = &sW[r16 * kBStrideW + 32 * kk + q4];
+        u32x2 h0, l0, h1, l1;
+        split4(*reinterpret_cast<const f32x4 *>(wrow), h0, l0);
+        split4(*reinterpret_cast<const f32x4 *>(wrow + 16), h1, l1);
+        const u32x4 wh = {h0[0], h0[1], h1[0], h1[1]}, wl = {l0[0], l0[1], l1[0], l1[1]};
 #pragma unroll
         for (int vi = 0; vi < 2; ++vi) {
-          P0[vi] = mfma16_bf16(wh, Sh[kt][vi], P0[vi]);
-          P1[vi] = mfma16_bf16(wh, Sl[kt][vi], P1[vi]);
-          P2[vi] = mfma16_bf16(wl, Sh[kt][vi], P2[vi]);
+          P0[vi] = mfma_bf16(wh, Sh[kk][vi], P0[vi]);
+          P1[vi] = mfma_bf16(wh, Sl[kk][vi], P1[vi]);
+          P2[vi] = mfma_bf16(wl, Sh[kk][vi], P2[vi]);
         }
       }
 #pragma unroll
@@ -261,56 +290,67 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
     {
       f32x4 O[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int kt = 0; kt < 8; ++kt) {
-        const u32x2 qa = *reinterpret_cast<const u32x2 *>(&sQ[r16 * kBStride + 16 * kt + q4]);
+      for (int kk = 0; kk < 4; ++kk) {
+        const uint16_t *qrow = &sQ[r16 * kBStride + 32 * kk + q4];
+        const u32x2 q0 = *reinterpret_cast<const u32x2 *>(qrow);
+        const u32x2 q1 = *reinterpret_cast<const u32x2 *>(qrow + 16);
+        const u32x4 qa = {q0[0], q0[1], q1[0], q1[1]};
 #pragma unroll
         for (int vi = 0; vi < 2; ++vi) {
-          O[vi] = mfma16_bf16(qa, Sh[kt][vi], O[vi]);
-          O[vi] = mfma16_bf16(qa, Sl[kt][vi], O[vi]);
+          O[vi] = mfma_bf16(qa, Sh[kk][vi], O[vi]);
+          O[vi] = mfma_bf16(qa, Sl[kk][vi], O[vi]);
         }
       }
       float eg[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) eg[r] = expf(sG[q4 + r]);
+      for (int r = 0; r < 4; ++r) eg[r] = expf(bG[q4 + r]);
       const u32x2 pa = *reinterpret_cast<const u32x2 *>(&sP[r16 * kBStrideP + q4]);
+      // rows past the block's n tokens fall outside the descriptor: dropped
+      const uint32_t ostride = static_cast<uint32_t>(H.v) * kDV * 2u;
+      const auto ro = buf_rsrc(out + (static_cast<size_t>(start) * H.v + h) * kDV,
+                               static_cast<uint32_t>(n) * ostride);
 #pragma unroll
       for (int vi = 0; vi < 2; ++vi) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) O[vi][r] *= eg[r];
         const u32x2 vb = {pk_bf16(vn[vi][0], vn[vi][1]), pk_bf16(vn[vi][2], vn[vi][3])};
         O[vi] = mfma16_bf16(pa, vb, O[vi]);
-        const int vc = 32 * wave + 16 * vi + r16;
+        const uint32_t vc2 = static_cast<uint32_t>(32 * wave + 16 * vi + r16) * 2u;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (q4 + r < n)
-            out[(static_cast<size_t>(start) + q4 + r) * H.v * kDV + h * kDV + vc] =
-                f32_to_bf16(scale * O[vi][r]);
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(scale * O[vi][r]), ro,
+                                                static_cast<uint32_t>(q4 + r) * ostride + vc2, 0, 0);
       }
     }
 
     // (7) S <- e^{G_last} S + K^T (D v_new), D = e^{G_last - G}: A = K^T rows
     //     (a transposed read of the K rows), B = D v_new split.
     {
-      const float G_last = sG[kBlk - 1];
+      const float G_last = bG[kBlk - 1];
       const float eg_last = expf(G_last);
       u32x2 dvh[2], dvl[2];
 #pragma unroll
       for (int vi = 0; vi < 2; ++vi) {
         f32x4 dv;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dv[r] = expf(G_last - sG[q4 + r]) * vn[vi][r];
+        for (int r = 0; r < 4; ++r) dv[r] = expf(G_last - bG[q4 + r]) * vn[vi][r];
         split4(dv, dvh[vi], dvl[vi]);
       }
+      // one K=32 product per tile: slots 8 g + e pair K^T's token 4 g + e mod 4
+      // with D v_new's hi part (e < 4) and lo part (e >= 4)
+      u32x4 dvb[2];
+#pragma unroll
+      for (int vi = 0; vi < 2; ++vi) dvb[vi] = u32x4{dvh[vi][0], dvh[vi][1], dvl[vi][0], dvl[vi][1]};
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
         const u32x2 ka = ds_read_tr16(&sK[(q4 + (r16 >> 2)) * kBStride + 16 * kt + 4 * (r16 & 3)]);
+        const u32x4 kaa = {ka[0], ka[1], ka[0], ka[1]};
 #pragma unroll
         for (int vi = 0; vi < 2; ++vi) {
           f32x4 acc = St[kt][vi];
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[r] *= eg_last;
-          acc = mfma16_bf16(ka, dvh[vi], acc);
-          St[kt][vi] = mfma16_bf16(ka, dvl[vi], acc);
+          St[kt][vi] = mfma_bf16(kaa, dvb[vi], acc);
         }
       }
     }
