@@ -34,8 +34,10 @@ namespace gdn {
 constexpr int kBlk = 16;        // tokens per block
 constexpr int kBStride = 136;   // bf16 row stride of the q/k/v block tiles
 constexpr int kBStrideA = 20;   // f32 row stride of the 16x16 A^T and Ti tiles
-constexpr int kBStrideW = 132;  // f32 row stride of W
 constexpr int kBStrideP = 24;   // bf16 row stride of P
+// Smallest pending decay factor of the state tiles (step (7)): the tiles hold
+// at most 2^60 times the state, far inside f32 range.
+constexpr float kMinDecay = 0x1p-60f;
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
@@ -50,9 +52,11 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
   __shared__ __align__(16) uint16_t sV[kBlk * kBStride];
   __shared__ __align__(16) float sAt[kBlk * kBStrideA];
   __shared__ __align__(16) float sTi[kBlk * kBStrideA];
-  __shared__ __align__(16) float sW[kBlk * kBStrideW];
+  __shared__ __align__(16) uint16_t sWh[kBlk * kBStride];  // W split: hi
+  __shared__ __align__(16) uint16_t sWl[kBlk * kBStride];  //          lo
   __shared__ __align__(16) uint16_t sP[kBlk * kBStrideP];
-  __shared__ float sG[2][kBlk], sBeta[2][kBlk];  // by block parity
+  // by block parity: G, beta, e^G and e^(G_last - G) of each token
+  __shared__ float sG[2][kBlk], sBeta[2][kBlk], sEG[2][kBlk], sED[2][kBlk];
 
   if (enable != nullptr && *enable == 0) return;  // the batch went through the chunks
   const int h = blockIdx.x % H.v, s = blockIdx.x / H.v;
@@ -119,7 +123,8 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
     x.b = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(b + g0, gbytes), goff, 0, 0);
   };
   // Gating of a block of n tokens (one wave, token `lane`): log decay,
-  // in-block cumsum G and beta into the LDS buffer of the block's parity.
+  // in-block cumsum G, beta and the decay factors into the LDS buffer of the
+  // block's parity.
   auto gate_block = [&](int n, uint16_t a_raw, uint16_t b_raw, int par) {
     const float gl = lane < n ? -rate * softplus20(bf16_to_f32(a_raw) + dtb) : 0.f;
     const float be = lane < n ? sigmoidf_(bf16_to_f32(b_raw)) : 0.f;
@@ -129,11 +134,15 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
       const float y = __shfl_up(G, off, kBlk);
       if (r16 >= off) G += y;
     }
+    const float G_last = __shfl(G, kBlk - 1, kBlk);
     if (lane < kBlk) {
       sG[par][lane] = G;
       sBeta[par][lane] = be;
+      sEG[par][lane] = expf(G);
+      sED[par][lane] = expf(G_last - G);
     }
   };
+  float c = 1.f;  // the state is c * St (decay applied lazily, step (7))
   BlockIn cur;
   if (len > 0) {
     load_block(0, cur);
@@ -143,7 +152,7 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
     const int n = len - t0 < kBlk ? len - t0 : kBlk;
     const int start = bos + t0;
     const int par = (t0 / kBlk) & 1;
-    const float *bG = sG[par], *bBeta = sBeta[par];
+    const float *bG = sG[par], *bBeta = sBeta[par], *bEG = sEG[par], *bED = sED[par];
 
     // (1) this block's q, k, v rows into LDS (its gates are there already);
     //     the next block's inputs requested.
@@ -227,7 +236,7 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
       }
     __syncthreads();
 
-    // (4) W = Ti diag(beta e^G) K for the features 32 wave .. +31 (-> LDS, f32)
+    // (4) W = Ti diag(beta e^G) K for the features 32 wave .. +31 (-> LDS, split)
     //     and U = Ti diag(beta) V for this wave's columns (registers).  One
     //     K=32 product each: slots 8 g + e carry Ti's hi part (e < 4) and lo
     //     part (e >= 4) of token 4 g + e mod 4 against the same K (V) entry
@@ -240,7 +249,7 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
       for (int e = 0; e < 4; ++e) {
         const float be = bBeta[q4 + e];
         tu[e] = ti[e] * be;
-        tw[e] = ti[e] * be * expf(bG[q4 + e]);
+        tw[e] = ti[e] * be * bEG[q4 + e];
       }
       u32x2 twh, twl, tuh, tul;
       split4(tw, twh, twl);
@@ -253,8 +262,13 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
         const u32x2 vb = ds_read_tr16(&sV[(q4 + (r16 >> 2)) * kBStride + c0 + 4 * (r16 & 3)]);
         const f32x4 w = mfma_bf16(twa, u32x4{kb[0], kb[1], kb[0], kb[1]}, f32x4{0.f, 0.f, 0.f, 0.f});
         U[ft] = mfma_bf16(tua, u32x4{vb[0], vb[1], vb[0], vb[1]}, f32x4{0.f, 0.f, 0.f, 0.f});
+        // W as bf16 hi/lo (the A operands of step (5), split once here)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sW[(q4 + r) * kBStrideW + c0 + r16] = w[r];
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t wb = __float_as_uint(w[r]) & 0xffff0000u;
+          sWh[(q4 + r) * kBStride + c0 + r16] = static_cast<uint16_t>(wb >> 16);
+          sWl[(q4 + r) * kBStride + c0 + r16] = f32_to_bf16(w[r] - __uint_as_float(wb));
+        }
       }
     }
     __syncthreads();
@@ -268,10 +282,11 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
       for (int vi = 0; vi < 2; ++vi) P0[vi] = P1[vi] = P2[vi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const float *wrow = &sW[r16 * kBStrideW + 32 * kk + q4];
-        u32x2 h0, l0, h1, l1;
-        split4(*reinterpret_cast<const f32x4 *>(wrow), h0, l0);
-        split4(*reinterpret_cast<const f32x4 *>(wrow + 16), h1, l1);
+        const int wo = r16 * kBStride + 32 * kk + q4;
+        const u32x2 h0 = *reinterpret_cast<const u32x2 *>(&sWh[wo]);
+        const u32x2 h1 = *reinterpret_cast<const u32x2 *>(&sWh[wo + 16]);
+        const u32x2 l0 = *reinterpret_cast<const u32x2 *>(&sWl[wo]);
+        const u32x2 l1 = *reinterpret_cast<const u32x2 *>(&sWl[wo + 16]);
         const u32x4 wh = {h0[0], h0[1], h1[0], h1[1]}, wl = {l0[0], l0[1], l1[0], l1[1]};
 #pragma unroll
         for (int vi = 0; vi < 2; ++vi) {
@@ -283,7 +298,7 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
 #pragma unroll
       for (int vi = 0; vi < 2; ++vi)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) vn[vi][r] = U[vi][r] - ((P0[vi][r] + P1[vi][r]) + P2[vi][r]);
+        for (int r = 0; r < 4; ++r) vn[vi][r] = U[vi][r] - c * ((P0[vi][r] + P1[vi][r]) + P2[vi][r]);
     }
 
     // (6) o = scale (e^{G_i} q_i S^T + P v_new) for this wave's columns.
@@ -303,7 +318,7 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
       }
       float eg[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) eg[r] = expf(bG[q4 + r]);
+      for (int r = 0; r < 4; ++r) eg[r] = c * bEG[q4 + r];
       const u32x2 pa = *reinterpret_cast<const u32x2 *>(&sP[r16 * kBStrideP + q4]);
       // rows past the block's n tokens fall outside the descriptor: dropped
       const uint32_t ostride = static_cast<uint32_t>(H.v) * kDV * 2u;
@@ -324,46 +339,59 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
     }
 
     // (7) S <- e^{G_last} S + K^T (D v_new), D = e^{G_last - G}: A = K^T rows
-    //     (a transposed read of the K rows), B = D v_new split.
+    //     (a transposed read of the K rows), B = D v_new split.  The tiles
+    //     hold S / c; the block's decay e^{G_last} only moves c, and the
+    //     update is added as K^T (D v_new) / c -- unless c would fall below
+    //     kMinDecay (or to zero), when the tiles take c e^{G_last} and c
+    //     returns to 1.
     {
-      const float G_last = bG[kBlk - 1];
-      const float eg_last = expf(G_last);
-      u32x2 dvh[2], dvl[2];
+      float cn = c * bEG[kBlk - 1];
+      const bool rescale = !(cn >= kMinDecay);
+      if (rescale) {
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+          for (int vi = 0; vi < 2; ++vi)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) St[kt][vi][r] *= cn;
+        cn = 1.f;
+      }
+      const float inv = 1.f / cn;
+      u32x4 dvb[2];
 #pragma unroll
       for (int vi = 0; vi < 2; ++vi) {
         f32x4 dv;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dv[r] = expf(G_last - bG[q4 + r]) * vn[vi][r];
-        split4(dv, dvh[vi], dvl[vi]);
+        for (int r = 0; r < 4; ++r) dv[r] = bED[q4 + r] * inv * vn[vi][r];
+        u32x2 dvh, dvl;
+        split4(dv, dvh, dvl);
+        // one K=32 product per tile: slots 8 g + e pair K^T's token
+        // 4 g + e mod 4 with D v_new's hi part (e < 4) and lo part (e >= 4)
+        dvb[vi] = u32x4{dvh[0], dvh[1], dvl[0], dvl[1]};
       }
-      // one K=32 product per tile: slots 8 g + e pair K^T's token 4 g + e mod 4
-      // with D v_new's hi part (e < 4) and lo part (e >= 4)
-      u32x4 dvb[2];
-#pragma unroll
-      for (int vi = 0; vi < 2; ++vi) dvb[vi] = u32x4{dvh[vi][0], dvh[vi][1], dvl[vi][0], dvl[vi][1]};
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
         const u32x2 ka = ds_read_tr16(&sK[(q4 + (r16 >> 2)) * kBStride + 16 * kt + 4 * (r16 & 3)]);
         const u32x4 kaa = {ka[0], ka[1], ka[0], ka[1]};
 #pragma unroll
-        for (int vi = 0; vi < 2; ++vi) {
-          f32x4 acc = St[kt][vi];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[r] *= eg_last;
-          St[kt][vi] = mfma_bf16(kaa, dvb[vi], acc);
-        }
+        for (int vi = 0; vi < 2; ++vi) St[kt][vi] = mfma_bf16(kaa, dvb[vi], St[kt][vi]);
       }
+      c = cn;
     }
     __syncthreads();  // the block's LDS tiles are free for the next block
   }
 
-  // Final state; all zeros for a zero-length sequence (gdn_prefill_ref.py:61-62).
+  // Final state c St; all zeros for a zero-length sequence
+  // (gdn_prefill_ref.py:61-62).
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
     for (int vi = 0; vi < 2; ++vi) {
       const int vc = 32 * wave + 16 * vi + r16;
-      *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + 16 * kt + q4) = St[kt][vi];
+      f32x4 x = St[kt][vi];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] *= c;
+      *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + 16 * kt + q4) = x;
     }
 }
 
