@@ -76,10 +76,11 @@ __host__ __device__ inline float cost_by_token(float L, float T, float hv, float
   return 3.0f + 0.24f * L + 0.003f * T * hv + 0.021f * g;
 }
 // 16-token blocks (block kernel): one workgroup per group, two resident per
-// CU (512 on the chip), ~5 us per block alone on a CU and ~6.3 us two to a CU.
+// CU (512 on the chip), ~3.5 us per block alone on a CU and ~4.7 us two to a
+// CU, plus the state's traffic per group.
 __host__ __device__ inline float cost_by_block(float L, float g) {
   const float rounds = ceilf(g / 512.0f), blocks = ceilf(L / 16.0f);
-  return 5.0f + 0.019f * g + rounds * blocks * (g <= 256.0f ? 5.0f : 6.3f);
+  return 5.5f + 0.021f * g + rounds * blocks * (g <= 256.0f ? 3.5f : 4.7f);
 }
 // Chunks: fixed launches, per-sequence work up to ~40 sequences and the
 // per-chunk throughput beyond, plus the serial chunk chain of the longest.

@@ -114,7 +114,7 @@ def _cost_by_token(L, T, hv, g):
 
 
 def _cost_by_block(L, g):
-    return 5 + 0.019 * g + math.ceil(g / 512) * math.ceil(L / 16) * (5 if g <= 256 else 6.3)
+    return 5.5 + 0.021 * g + math.ceil(g / 512) * math.ceil(L / 16) * (3.5 if g <= 256 else 4.7)
 
 
 def _cost_by_chunks(L, nt, hv, g):
