@@ -58,10 +58,12 @@ def _dev_inputs(inp, dev):
 ONLY_WORKLOADS = {
     "decode_b64": ("decode", (64, 1)),
     "decode_b64_t4": ("decode", (64, 4)),
+    "decode_b64_t16": ("decode", (64, 16)),
     "prefill_1x8192": ("prefill", [8192]),
     "prefill_4x8192": ("prefill", [8192] * 4),
     "prefill_1x1024": ("prefill", [1024]),
     "prefill_64x16": ("prefill", [16] * 64),
+    "prefill_64x256": ("prefill", [256] * 64),
     "prefill_configs3": ("prefill", [6, 49, 294, 1800, 2040, 61]),
     "prefill_8x2048": ("prefill", [2048] * 8),
 }
@@ -400,12 +402,13 @@ def main():
         f"1x1024 graph {pre1k_ms:.3f} ms, eager {pre1k_eager:.3f} ms")
 
     mtp = {}
-    for T in (2, 4, 8):
+    for T in (2, 4, 8, 16):
         _, mg = bench_decode(64, 50, 5, dev, tokens=T)
         mtp[f"B64_T{T}"] = round(mg * 1e3, 2)
     log(f"multi-token decode B=64 (us per call): {mtp}")
     short = {}
-    for name, lens in (("256x1", [1] * 256), ("64x16", [16] * 64), ("1x64", [64])):
+    for name, lens in (("256x1", [1] * 256), ("64x16", [16] * 64), ("1x64", [64]),
+                       ("32x64", [64] * 32), ("64x256", [256] * 64)):
         _, pg = bench_prefill(lens, 20, 3, dev)
         short[name] = round(pg, 4)
     log(f"short-sequence prefill (ms per call): {short}")
