@@ -154,7 +154,8 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
                                                               int nt_max, int choose, int rec_max,
                                                               int hv, int form, int4 *chunks,
                                                               int *offsets) {
-  __shared__ int s_incl[1024];
+  __shared__ int s_incl[1024], s_bos[1024], s_eos[1024];
+  __shared__ int s_wsum[16];
   __shared__ int s_longest, s_most_chunks, s_chunks;
   const int tid = threadIdx.x;
   if (tid == 0) s_longest = s_most_chunks = s_chunks = 0;
@@ -192,16 +193,23 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
       int eos = load_cu(cu, cu64, s + 1, T);
       eos = eos < bos ? bos : eos;
       n = (eos - bos + kChunk - 1) / kChunk;
+      s_bos[tid] = bos;
+      s_eos[tid] = eos;
     }
     most_chunks = n > most_chunks ? n : most_chunks;
-    s_incl[tid] = n;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-      const int y = tid >= off ? s_incl[tid - off] : 0;
-      __syncthreads();
-      s_incl[tid] += y;
-      __syncthreads();
+    // inclusive scan of n over the tile: within each wave by lane shifts,
+    // then the totals of the earlier waves
+    int incl = n;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off);
+      if ((tid & 63) >= off) incl += y;
     }
+    if ((tid & 63) == 63) s_wsum[tid >> 6] = incl;
+    __syncthreads();
+    for (int w = 0; w < (tid >> 6); ++w) incl += s_wsum[w];
+    s_incl[tid] = incl;
+    __syncthreads();
     const int tile_total = s_incl[1023];
     if (s < N) {
       const long long first = carry + s_incl[tid] - n;
@@ -218,10 +226,8 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
       }
       const int excl = lo == 0 ? 0 : s_incl[lo - 1];
       const int sq = base + lo, local = r - excl;
-      const int bos = load_cu(cu, cu64, sq, T);
-      int eos = load_cu(cu, cu64, sq + 1, T);
-      eos = eos < bos ? bos : eos;
-      const int start = bos + local * kChunk;
+      const int eos = s_eos[lo];
+      const int start = s_bos[lo] + local * kChunk;
       const int len = eos - start < kChunk ? eos - start : kChunk;
       chunks[c] = make_int4(sq, start, len, local);
     }
