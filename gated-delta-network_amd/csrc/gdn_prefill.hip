@@ -395,10 +395,15 @@ __device__ __forceinline__ void wy_intra(
   }
   __syncthreads();
 
-  // A = strictly-lower(beta_i exp(G_i - G_j) K K^T); wave w owns rows 16w..16w+15.
+  // A = strictly-lower(beta_i exp(G_i - G_j) K K^T): its ten lower 16x16
+  // tiles dealt three, three, two and two to the waves.  G_i - G_j <= 0 for
+  // every kept entry (g <= 0); the clamp keeps the others finite.
   {
-    const int mb = wave;
-    for (int nb = 0; nb <= mb; ++nb) {
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    for (int t = wv; t < 10; t += 4) {
+      // t = 0..9 -> (mb, nb) = (3,3) (3,2) (3,1) (3,0) (2,2) (2,1) (2,0) (1,1) (1,0) (0,0)
+      const int mb = t < 4 ? 3 : t < 7 ? 2 : t < 9 ? 1 : 0;
+      const int nb = t < 4 ? 3 - t : t < 7 ? 6 - t : t < 9 ? 8 - t : 0;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
@@ -406,10 +411,12 @@ __device__ __forceinline__ void wy_intra(
         const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[(16 * nb + r16) * kStrideK + 32 * kk + kg]);
         acc = mfma_bf16(af, bf, acc);
       }
+      const float Gj = sG[16 * nb + r16];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * mb + 4 * g + r, j = 16 * nb + r16;
-        sA[i * kStrideA4 + j] = (i > j && i < len) ? sBeta[i] * expf(sG[i] - sG[j]) * acc[r] : 0.f;
+        const float e = sBeta[i] * expf(fminf(sG[i] - Gj, 0.f)) * acc[r];
+        sA[i * kStrideA4 + j] = (i > j && i < len) ? e : 0.f;
       }
     }
   }
@@ -417,20 +424,19 @@ __device__ __forceinline__ void wy_intra(
 
   if (!isK) transpose_into(sVt, false);
 
-  // Diagonal blocks D_w = (I + A_ww)^-1: wave w, lane j < 16 solves column j.
+  // Diagonal blocks D_w = (I + A_ww)^-1: wave w, lane j < 16 solves column j,
+  // column-oriented (each solved x_m is applied to all later rows at once, so
+  // the serial chain is one FMA per row).
   if (lane < 16) {
     const int base = 16 * wave;
     float x[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float *arow = &sA[(base + i) * kStrideA4 + base];
-      float s0 = (i == lane) ? 1.f : 0.f, s1 = 0.f;
+    for (int i = 0; i < 16; ++i) x[i] = i == lane ? 1.f : 0.f;
 #pragma unroll
-      for (int m = 0; m < i; m += 2) {
-        s0 -= arow[m] * x[m];
-        if (m + 1 < i) s1 -= arow[m + 1] * x[m + 1];
-      }
-      x[i] = s0 + s1;
+    for (int m = 0; m < 15; ++m) {
+      const float xm = x[m];
+#pragma unroll
+      for (int i = m + 1; i < 16; ++i) x[i] -= sA[(base + i) * kStrideA4 + base + m] * xm;
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i)
@@ -602,10 +608,15 @@ __device__ __forceinline__ void t_intra(
   }
   __syncthreads();
 
-  // A = strictly-lower(beta_i exp(G_i - G_j) K K^T); wave w owns rows 16w..16w+15.
+  // A = strictly-lower(beta_i exp(G_i - G_j) K K^T): its ten lower 16x16
+  // tiles dealt three, three, two and two to the waves.  G_i - G_j <= 0 for
+  // every kept entry (g <= 0); the clamp keeps the others finite.
   {
-    const int mb = wave;
-    for (int nb = 0; nb <= mb; ++nb) {
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    for (int t = wv; t < 10; t += 4) {
+      // t = 0..9 -> (mb, nb) = (3,3) (3,2) (3,1) (3,0) (2,2) (2,1) (2,0) (1,1) (1,0) (0,0)
+      const int mb = t < 4 ? 3 : t < 7 ? 2 : t < 9 ? 1 : 0;
+      const int nb = t < 4 ? 3 - t : t < 7 ? 6 - t : t < 9 ? 8 - t : 0;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
@@ -613,29 +624,30 @@ __device__ __forceinline__ void t_intra(
         const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[(16 * nb + r16) * kStrideK + 32 * kk + kg]);
         acc = mfma_bf16(af, bf, acc);
       }
+      const float Gj = sG[16 * nb + r16];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * mb + 4 * g + r, j = 16 * nb + r16;
-        sA[i * kStrideA4 + j] = (i > j && i < len) ? sBeta[i] * expf(sG[i] - sG[j]) * acc[r] : 0.f;
+        const float e = sBeta[i] * expf(fminf(sG[i] - Gj, 0.f)) * acc[r];
+        sA[i * kStrideA4 + j] = (i > j && i < len) ? e : 0.f;
       }
     }
   }
   __syncthreads();
 
-  // Diagonal blocks D_w = (I + A_ww)^-1: wave w, lane j < 16 solves column j.
+  // Diagonal blocks D_w = (I + A_ww)^-1: wave w, lane j < 16 solves column j,
+  // column-oriented (each solved x_m is applied to all later rows at once, so
+  // the serial chain is one FMA per row).
   if (lane < 16) {
     const int base = 16 * wave;
     float x[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float *arow = &sA[(base + i) * kStrideA4 + base];
-      float s0 = (i == lane) ? 1.f : 0.f, s1 = 0.f;
+    for (int i = 0; i < 16; ++i) x[i] = i == lane ? 1.f : 0.f;
 #pragma unroll
-      for (int m = 0; m < i; m += 2) {
-        s0 -= arow[m] * x[m];
-        if (m + 1 < i) s1 -= arow[m + 1] * x[m + 1];
-      }
-      x[i] = s0 + s1;
+    for (int m = 0; m < 15; ++m) {
+      const float xm = x[m];
+#pragma unroll
+      for (int i = m + 1; i < 16; ++i) x[i] -= sA[(base + i) * kStrideA4 + base + m] * xm;
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i)
