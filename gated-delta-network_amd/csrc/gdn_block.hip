@@ -38,7 +38,14 @@ constexpr int kBStrideP = 24;   // bf16 row stride of P
 // Smallest pending decay factor of the state tiles (step (7)): the tiles hold
 // at most 2^60 times the state, far inside f32 range.
 constexpr float kMinDecay = 0x1p-60f;
+// Largest (sequence, v-head) count that runs as two 64-column workgroups.
+constexpr long long kBlockHalfMaxPairs = 128;
 
+// CV = 16-column state tiles per wave: 2 (the workgroup holds all 128
+// columns) or 1 (two workgroups per (sequence, v-head), each 64 columns, for
+// batches too small to fill the CUs: each repeats the intra-block work and
+// owns half the state products).
+template <int CV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
                   const uint16_t *__restrict__ v, const float *state,
@@ -59,7 +66,10 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
   __shared__ float sG[2][kBlk], sBeta[2][kBlk], sEG[2][kBlk], sED[2][kBlk];
 
   if (enable != nullptr && *enable == 0) return;  // the batch went through the chunks
-  const int h = blockIdx.x % H.v, s = blockIdx.x / H.v;
+  const int half = CV == 2 ? 0 : static_cast<int>(blockIdx.x & 1u);
+  const int pair = CV == 2 ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x >> 1);
+  const int h = pair % H.v, s = pair / H.v;
+  const int col0 = 64 * half + 16 * CV * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4, q4 = 4 * g, kg = 8 * g;
@@ -80,12 +90,12 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
   // The state as result tiles of S^T: St[kt][vi] holds S[v][k] at
   // k = 16 kt + q4 + r, v = 32 wave + 16 vi + r16.
   const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;
-  f32x4 St[8][2];
+  f32x4 St[8][CV];
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-    for (int vi = 0; vi < 2; ++vi) {
-      const int vc = 32 * wave + 16 * vi + r16;
+    for (int vi = 0; vi < CV; ++vi) {
+      const int vc = col0 + 16 * vi + r16;
       if (state != nullptr && len > 0)
         St[kt][vi] = *reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + 16 * kt + q4);
       else
@@ -223,11 +233,11 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
     // The state split for the K=32 products of step (5): slot 8 g + e of
     // k-block kk is k = 32 kk + 4 g + e (e < 4) or 32 kk + 16 + 4 g + e - 4
     // (the k of two state tiles), the same map for the A operands.
-    u32x4 Sh[4][2], Sl[4][2];
+    u32x4 Sh[4][CV], Sl[4][CV];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-      for (int vi = 0; vi < 2; ++vi) {
+      for (int vi = 0; vi < CV; ++vi) {
         u32x2 h0, l0, h1, l1;
         split4(St[2 * kk][vi], h0, l0);
         split4(St[2 * kk + 1][vi], h1, l1);
@@ -241,7 +251,7 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
     //     K=32 product each: slots 8 g + e carry Ti's hi part (e < 4) and lo
     //     part (e >= 4) of token 4 g + e mod 4 against the same K (V) entry
     //     twice, a transposed read of the rows.
-    f32x4 U[2];
+    f32x4 U[CV];
     {
       const f32x4 ti = *reinterpret_cast<const f32x4 *>(&sTi[r16 * kBStrideA + q4]);
       f32x4 tw, tu;
@@ -256,12 +266,16 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
       split4(tu, tuh, tul);
       const u32x4 twa = {twh[0], twh[1], twl[0], twl[1]}, tua = {tuh[0], tuh[1], tul[0], tul[1]};
 #pragma unroll
-      for (int ft = 0; ft < 2; ++ft) {
-        const int c0 = 32 * wave + 16 * ft;  // feature tile of W / column tile of U
+      for (int vi = 0; vi < CV; ++vi) {  // U for this wave's state columns
+        const int u0 = col0 + 16 * vi;
+        const u32x2 vb = ds_read_tr16(&sV[(q4 + (r16 >> 2)) * kBStride + u0 + 4 * (r16 & 3)]);
+        U[vi] = mfma_bf16(tua, u32x4{vb[0], vb[1], vb[0], vb[1]}, f32x4{0.f, 0.f, 0.f, 0.f});
+      }
+#pragma unroll
+      for (int ft = 0; ft < 2; ++ft) {  // W for the features 32 wave .. +31 (all 128 per block)
+        const int c0 = 32 * wave + 16 * ft;
         const u32x2 kb = ds_read_tr16(&sK[(q4 + (r16 >> 2)) * kBStride + c0 + 4 * (r16 & 3)]);
-        const u32x2 vb = ds_read_tr16(&sV[(q4 + (r16 >> 2)) * kBStride + c0 + 4 * (r16 & 3)]);
         const f32x4 w = mfma_bf16(twa, u32x4{kb[0], kb[1], kb[0], kb[1]}, f32x4{0.f, 0.f, 0.f, 0.f});
-        U[ft] = mfma_bf16(tua, u32x4{vb[0], vb[1], vb[0], vb[1]}, f32x4{0.f, 0.f, 0.f, 0.f});
         // W as bf16 hi/lo (the A operands of step (5), split once here)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -275,11 +289,11 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
 
     // (5) v_new = U - W S^T for this wave's columns (W and S split: three
     //     K=32 products per 32 k).
-    f32x4 vn[2];
+    f32x4 vn[CV];
     {
-      f32x4 P0[2], P1[2], P2[2];
+      f32x4 P0[CV], P1[CV], P2[CV];
 #pragma unroll
-      for (int vi = 0; vi < 2; ++vi) P0[vi] = P1[vi] = P2[vi] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int vi = 0; vi < CV; ++vi) P0[vi] = P1[vi] = P2[vi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const int wo = r16 * kBStride + 32 * kk + q4;
@@ -289,21 +303,23 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
         const u32x2 l1 = *reinterpret_cast<const u32x2 *>(&sWl[wo + 16]);
         const u32x4 wh = {h0[0], h0[1], h1[0], h1[1]}, wl = {l0[0], l0[1], l1[0], l1[1]};
 #pragma unroll
-        for (int vi = 0; vi < 2; ++vi) {
+        for (int vi = 0; vi < CV; ++vi) {
           P0[vi] = mfma_bf16(wh, Sh[kk][vi], P0[vi]);
           P1[vi] = mfma_bf16(wh, Sl[kk][vi], P1[vi]);
           P2[vi] = mfma_bf16(wl, Sh[kk][vi], P2[vi]);
         }
       }
 #pragma unroll
-      for (int vi = 0; vi < 2; ++vi)
+      for (int vi = 0; vi < CV; ++vi)
 #pragma unroll
         for (int r = 0; r < 4; ++r) vn[vi][r] = U[vi][r] - c * ((P0[vi][r] + P1[vi][r]) + P2[vi][r]);
     }
 
     // (6) o = scale (e^{G_i} q_i S^T + P v_new) for this wave's columns.
     {
-      f32x4 O[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      f32x4 O[CV];
+#pragma unroll
+      for (int vi = 0; vi < CV; ++vi) O[vi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const uint16_t *qrow = &sQ[r16 * kBStride + 32 * kk + q4];
@@ -311,7 +327,7 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
         const u32x2 q1 = *reinterpret_cast<const u32x2 *>(qrow + 16);
         const u32x4 qa = {q0[0], q0[1], q1[0], q1[1]};
 #pragma unroll
-        for (int vi = 0; vi < 2; ++vi) {
+        for (int vi = 0; vi < CV; ++vi) {
           O[vi] = mfma_bf16(qa, Sh[kk][vi], O[vi]);
           O[vi] = mfma_bf16(qa, Sl[kk][vi], O[vi]);
         }
@@ -325,12 +341,12 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
       const auto ro = buf_rsrc(out + (static_cast<size_t>(start) * H.v + h) * kDV,
                                static_cast<uint32_t>(n) * ostride);
 #pragma unroll
-      for (int vi = 0; vi < 2; ++vi) {
+      for (int vi = 0; vi < CV; ++vi) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) O[vi][r] *= eg[r];
         const u32x2 vb = {pk_bf16(vn[vi][0], vn[vi][1]), pk_bf16(vn[vi][2], vn[vi][3])};
         O[vi] = mfma16_bf16(pa, vb, O[vi]);
-        const uint32_t vc2 = static_cast<uint32_t>(32 * wave + 16 * vi + r16) * 2u;
+        const uint32_t vc2 = static_cast<uint32_t>(col0 + 16 * vi + r16) * 2u;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(scale * O[vi][r]), ro,
@@ -351,15 +367,15 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-          for (int vi = 0; vi < 2; ++vi)
+          for (int vi = 0; vi < CV; ++vi)
 #pragma unroll
             for (int r = 0; r < 4; ++r) St[kt][vi][r] *= cn;
         cn = 1.f;
       }
       const float inv = 1.f / cn;
-      u32x4 dvb[2];
+      u32x4 dvb[CV];
 #pragma unroll
-      for (int vi = 0; vi < 2; ++vi) {
+      for (int vi = 0; vi < CV; ++vi) {
         f32x4 dv;
 #pragma unroll
         for (int r = 0; r < 4; ++r) dv[r] = bED[q4 + r] * inv * vn[vi][r];
@@ -374,7 +390,7 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
         const u32x2 ka = ds_read_tr16(&sK[(q4 + (r16 >> 2)) * kBStride + 16 * kt + 4 * (r16 & 3)]);
         const u32x4 kaa = {ka[0], ka[1], ka[0], ka[1]};
 #pragma unroll
-        for (int vi = 0; vi < 2; ++vi) St[kt][vi] = mfma_bf16(kaa, dvb[vi], St[kt][vi]);
+        for (int vi = 0; vi < CV; ++vi) St[kt][vi] = mfma_bf16(kaa, dvb[vi], St[kt][vi]);
       }
       c = cn;
     }
@@ -386,8 +402,8 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-    for (int vi = 0; vi < 2; ++vi) {
-      const int vc = 32 * wave + 16 * vi + r16;
+    for (int vi = 0; vi < CV; ++vi) {
+      const int vc = col0 + 16 * vi + r16;
       f32x4 x = St[kt][vi];
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[r] *= c;
@@ -400,12 +416,20 @@ int block_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const 
                  const void *cu, int cu64, int num_seqs, int T, int fixed_len, const int *enable,
                  const Heads &H, float scale, uint16_t *out, float *new_state,
                  hipStream_t stream, const char *what) {
-  const long long blocks = static_cast<long long>(num_seqs) * H.v;
-  if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "%s: too many sequences for one launch", what);
-  if (blocks == 0) return GDN_OK;
-  hipLaunchKernelGGL(block_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, q, k,
-                     v, state, A_log, a, dt_bias, b, cu, cu64, T, fixed_len, enable, H, scale, out,
-                     new_state);
+  const long long pairs = static_cast<long long>(num_seqs) * H.v;
+  if (pairs > 0x3fffffffLL) return fail(GDN_ERR_INVALID, "%s: too many sequences for one launch", what);
+  if (pairs == 0) return GDN_OK;
+  // Two workgroups of 64 columns per (sequence, v-head) while that still
+  // leaves every workgroup a CU of its own (kBlockHalfMaxPairs), one of 128
+  // columns otherwise.
+  if (pairs <= kBlockHalfMaxPairs)
+    hipLaunchKernelGGL(block_kernel<1>, dim3(static_cast<unsigned>(2 * pairs)), dim3(256), 0, stream,
+                       q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T, fixed_len, enable, H,
+                       scale, out, new_state);
+  else
+    hipLaunchKernelGGL(block_kernel<2>, dim3(static_cast<unsigned>(pairs)), dim3(256), 0, stream,
+                       q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T, fixed_len, enable, H,
+                       scale, out, new_state);
   return check_launch(what);
 }
 

@@ -75,12 +75,14 @@ int block_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const 
 __host__ __device__ inline float cost_by_token(float L, float T, float hv, float g) {
   return 3.0f + 0.24f * L + 0.003f * T * hv + 0.021f * g;
 }
-// 16-token blocks (block kernel): one workgroup per group, two resident per
-// CU (512 on the chip), ~3.5 us per block alone on a CU and ~4.7 us two to a
-// CU, plus the state's traffic per group.
+// 16-token blocks (block kernel): two workgroups of 64 columns per group up
+// to 128 groups (~2.8 us per block), then one of 128 columns per group, two
+// resident per CU (512 on the chip): ~3.5 us per block alone on a CU, ~4.7 us
+// two to a CU; plus the state's traffic per group.
 __host__ __device__ inline float cost_by_block(float L, float g) {
   const float rounds = ceilf(g / 512.0f), blocks = ceilf(L / 16.0f);
-  return 5.5f + 0.021f * g + rounds * blocks * (g <= 256.0f ? 3.5f : 4.7f);
+  const float per_block = g <= 128.0f ? 2.8f : g <= 256.0f ? 3.5f : 4.7f;
+  return 4.5f + 0.015f * g + 0.006f * fmaxf(g - 256.0f, 0.0f) + rounds * blocks * per_block;
 }
 // Chunks: fixed launches, per-sequence work up to ~40 sequences and the
 // per-chunk throughput beyond, plus the serial chunk chain of the longest.

@@ -1747,8 +1747,9 @@ void prefill_output_kernel(
 
 // Path choice between a sequential kernel and the chunk pipeline, from
 // sweeps of all three paths on MI355X.  A batch of at most kRecurrentMaxLen
-// tokens runs token by token (one sequence of 64 tokens: 20.1 us vs 21.3 us
-// chunked, 25.8 us in blocks).  Otherwise the sequential candidate is the
+// tokens runs sequentially: token by token, or one sequence in blocks when
+// the cost models favour them (one sequence of 64 tokens: 16.1 us in blocks,
+// 20.1 us token by token, 20.7 us chunked).  Otherwise the sequential candidate is the
 // block kernel (gdn_block.hip) or the token-by-token kernel, whichever the
 // cost models (gdn_host.h) rate faster at the mean length, and the device
 // compares its cost model with the chunks' at the batch's longest sequence
@@ -1862,6 +1863,11 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     choose = N > 1 ? 1 : 0;
   } else if (rec_max == -1) {
     host_sequential = T <= kRecurrentMaxLen;
+    if (host_sequential && N == 1 && seq_var < 0) {
+      // one short sequence: token by token or in blocks, by the cost models
+      const float fT = static_cast<float>(T), fhv = static_cast<float>(H.v);
+      if (cost_by_block(fT, fhv) < cost_by_token(fT, fT, fhv, fhv)) seq_var = block_var;
+    }
     if (!host_sequential && N > 1) {
       const float fT = static_cast<float>(T), fhv = static_cast<float>(H.v);
       const float g = static_cast<float>(N) * fhv, mean = ceilf(fT / static_cast<float>(N));

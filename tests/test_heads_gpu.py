@@ -18,6 +18,7 @@ import numpy as np
 import pytest
 import torch
 
+from test_recurrent_gpu import _expected_multi_kind  # noqa: E402
 from conftest import assert_output_close, assert_state_close
 from oracle import gdn_oracle as O
 
@@ -94,7 +95,10 @@ def test_multi_token_decode_heads_matches_oracle(cuda_device, heads):
     out, ns = _decode(_to_dev(dec, cuda_device), cuda_device)
     o_ref, s_ref = O.prefill_seq_c(**inp)
     assert_output_close(out.reshape(B * T, heads[1], 128).float().cpu().numpy(), o_ref)
-    assert_state_close(ns.cpu().numpy(), s_ref, rel_atol=1e-5)
+    # token by token holds the f32 sequential bound; the block kernel (split
+    # bf16 products) the parity tolerance
+    token = _expected_multi_kind(B, T, hv=heads[1]) == "token"
+    assert_state_close(ns.cpu().numpy(), s_ref, rel_atol=1e-5 if token else 1e-3)
 
 
 @pytest.mark.parametrize("heads", HEADS)

@@ -114,7 +114,9 @@ def _cost_by_token(L, T, hv, g):
 
 
 def _cost_by_block(L, g):
-    return 5.5 + 0.021 * g + math.ceil(g / 512) * math.ceil(L / 16) * (3.5 if g <= 256 else 4.7)
+    per_block = 2.8 if g <= 128 else 3.5 if g <= 256 else 4.7
+    return (4.5 + 0.015 * g + 0.006 * max(g - 256, 0)
+            + math.ceil(g / 512) * math.ceil(L / 16) * per_block)
 
 
 def _cost_by_chunks(L, nt, hv, g):
@@ -126,6 +128,8 @@ def _expected_path(lens, hv=8):
     models of gdn_host.h), restated: "token", "block" or "chunks"."""
     T, N, L = sum(lens), len(lens), max(lens)
     if T <= 96:
+        if N == 1 and _cost_by_block(T, hv) < _cost_by_token(T, T, hv, hv):
+            return "block"
         return "token"
     if N == 1:
         return "chunks"
@@ -167,7 +171,7 @@ DEVICE_CHOICE = {
     "mixed40": ([3, 17, 96, 0, 40] * 8, "block"),
     "1500": (_lens_1500(), "token"),
     "10x2+200": ([2] * 10 + [200], "chunks"),
-    "16x8": ([8] * 16, "token"),
+    "16x8": ([8] * 16, "block"),
     "32x128": ([128] * 32, "block"),
     "3x40+300": ([40] * 3 + [300], "chunks"),
 }
