@@ -97,7 +97,7 @@ int gdn_decode_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 
  * in the chunked form on MFMA; same function within the stated tolerances,
  * not bit for bit), -1 = built-in: tokens == 1 runs gdn_decode_fwd, more run
  * token by token or in blocks by a cost model fitted on MI355X (blocks from
- * about 5 tokens at 64 rows, 10 at 16 rows).
+ * about 5 tokens at 64 rows, 8 at 16 rows).
  */
 int gdn_decode_multi_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                          const float *state, const float *A_log, const gdn_bf16 *a,
@@ -155,8 +155,9 @@ size_t gdn_prefill_workspace_bytes(int total_tokens, int num_seqs);
  * The batch takes one of three paths: every sequence token by token with the
  * state in registers (one launch), every sequence in 16-token blocks with the
  * state in MFMA tiles (one launch: the block kernel of gdn_decode_multi_fwd),
- * or all through the chunk-64 pipeline.  A batch of at most 96 tokens goes
- * token by token and one sequence through the chunks; for the others the
+ * or all through the chunk-64 pipeline.  A batch of at most 96 tokens runs
+ * sequentially (one sequence in blocks when a cost model favours them),
+ * a longer single sequence through the chunks; for the others the
  * host picks the faster sequential kind at the mean length and, unless the
  * chunks win for any longest sequence, the device compares cost models of
  * it and of the chunks from the longest sequence, the chunk count, T and N
