@@ -82,7 +82,7 @@ __host__ __device__ inline float cost_by_token(float L, float T, float hv, float
 __host__ __device__ inline float cost_by_block(float L, float g) {
   const float rounds = ceilf(g / 512.0f), blocks = ceilf(L / 16.0f);
   const float per_block = g <= 128.0f ? 2.8f : g <= 256.0f ? 3.5f : 4.7f;
-  return 4.5f + 0.015f * g + 0.006f * fmaxf(g - 256.0f, 0.0f) + rounds * blocks * per_block;
+  return 4.5f + 0.015f * g + 0.008f * fmaxf(g - 256.0f, 0.0f) + rounds * blocks * per_block;
 }
 // Chunks: fixed launches, per-sequence work up to ~40 sequences and the
 // per-chunk throughput beyond, plus the serial chunk chain of the longest.

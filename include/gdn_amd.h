@@ -97,7 +97,7 @@ int gdn_decode_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 
  * in the chunked form on MFMA; same function within the stated tolerances,
  * not bit for bit), -1 = built-in: tokens == 1 runs gdn_decode_fwd, more run
  * token by token or in blocks by a cost model fitted on MI355X (blocks from
- * about 5 tokens at 64 rows, 8 at 16 rows).
+ * about 4 tokens at 64 rows, 6 at 16 rows).
  */
 int gdn_decode_multi_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                          const float *state, const float *A_log, const gdn_bf16 *a,

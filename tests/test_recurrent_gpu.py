@@ -115,7 +115,7 @@ def _cost_by_token(L, T, hv, g):
 
 def _cost_by_block(L, g):
     per_block = 2.8 if g <= 128 else 3.5 if g <= 256 else 4.7
-    return (4.5 + 0.015 * g + 0.006 * max(g - 256, 0)
+    return (4.5 + 0.015 * g + 0.008 * max(g - 256, 0)
             + math.ceil(g / 512) * math.ceil(L / 16) * per_block)
 
 
