@@ -16,16 +16,17 @@
 // fused into one launch.  It serves the token-sequential cases: decode of
 // T > 1 tokens per row, and prefill of batches of short sequences.
 //
-// Work mapping (gfx950, wave64, 256 threads): wave w owns the state columns
-// v = 32 w .. 32 w + 31 for all 128 k, as 16 result tiles of S^T (rows k,
-// columns v: 4 consecutive k per lane), which is exactly the B operand of a
-// 16x16x16 MFMA contracting over k (W S^T, q S^T); v_new comes out of those
+// Work mapping (gfx950, wave64, 256 threads): wave w owns 32 state columns
+// (or 16, when two workgroups share a (sequence, v-head): block_kernel<1>)
+// for all 128 k, as result tiles of S^T (rows k, columns v: 4 consecutive k
+// per lane), the B operand layout of an MFMA contracting over k (W S^T,
+// q S^T; two k-tiles form one K=32 operand); v_new comes out of those
 // products as tiles of 4 consecutive tokens per lane, the B operand of the
 // update K^T v_new and of P v_new.  K^T and the token-major operands of W
 // and U are read transposed out of the block's K and V rows in LDS
 // (ds_read_b64_tr_b16).  Products whose error reaches the state use split
-// bf16 (x = hi + lo), as in the chunk pipeline; the output path uses single
-// bf16 operands.
+// bf16 (x = hi + lo), as in the chunk pipeline; P v_new uses single bf16
+// operands.
 #include "gdn_device.h"
 #include "gdn_host.h"
 

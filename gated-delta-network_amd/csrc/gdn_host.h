@@ -59,7 +59,8 @@ int recurrent_num_variants();
 int recurrent_block_variant();
 
 // The same cases in 16-token blocks of the chunked form (gdn_block.hip): one
-// workgroup per (sequence, v-head).  Arguments as recurrent_launch's.
+// workgroup per (sequence, v-head), or two (64 state columns each) for
+// batches of at most 128 such pairs.  Arguments as recurrent_launch's.
 int block_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
                  const float *A_log, const uint16_t *a, const float *dt_bias, const uint16_t *b,
                  const void *cu, int cu64, int num_seqs, int T, int fixed_len, const int *enable,
