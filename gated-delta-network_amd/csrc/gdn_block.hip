@@ -52,7 +52,7 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
                   const uint16_t *__restrict__ v, const float *state,
                   const float *__restrict__ A_log, const uint16_t *__restrict__ a,
                   const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
-                  const void *__restrict__ cu, int cu64, int T, int fixed_len,
+                  const void *__restrict__ cu, int cu64, int N, int T, int fixed_len,
                   const int *__restrict__ enable, Heads H, float scale,
                   uint16_t *__restrict__ out, float *new_state) {
   __shared__ __align__(16) uint16_t sQ[kBlk * kBStride];
@@ -343,10 +343,12 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
                                static_cast<uint32_t>(n) * ostride);
 #pragma unroll
       for (int vi = 0; vi < CV; ++vi) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) O[vi][r] *= eg[r];
+        // P v_new in a tile of its own, added by VALU: no accumulation chain
+        // mixes the 16x16x32 and 16x16x16 MFMA shapes.
         const u32x2 vb = {pk_bf16(vn[vi][0], vn[vi][1]), pk_bf16(vn[vi][2], vn[vi][3])};
-        O[vi] = mfma16_bf16(pa, vb, O[vi]);
+        const f32x4 pv = mfma16_bf16(pa, vb, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int r = 0; r < 4; ++r) O[vi][r] = fmaf(O[vi][r], eg[r], pv[r]);
         const uint32_t vc2 = static_cast<uint32_t>(col0 + 16 * vi + r16) * 2u;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -410,6 +412,8 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
       for (int r = 0; r < 4; ++r) x[r] *= c;
       *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + 16 * kt + q4) = x;
     }
+  // A packed batch: rows outside every sequence get zeros.
+  if (cu != nullptr) zero_uncovered_rows(out, cu, cu64, N, T, H.v, blockIdx.x, gridDim.x);
 }
 
 int block_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
@@ -425,11 +429,11 @@ int block_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const 
   // columns otherwise.
   if (pairs <= kBlockHalfMaxPairs)
     hipLaunchKernelGGL(block_kernel<1>, dim3(static_cast<unsigned>(2 * pairs)), dim3(256), 0, stream,
-                       q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T, fixed_len, enable, H,
+                       q, k, v, state, A_log, a, dt_bias, b, cu, cu64, num_seqs, T, fixed_len, enable, H,
                        scale, out, new_state);
   else
     hipLaunchKernelGGL(block_kernel<2>, dim3(static_cast<unsigned>(pairs)), dim3(256), 0, stream,
-                       q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T, fixed_len, enable, H,
+                       q, k, v, state, A_log, a, dt_bias, b, cu, cu64, num_seqs, T, fixed_len, enable, H,
                        scale, out, new_state);
   return check_launch(what);
 }

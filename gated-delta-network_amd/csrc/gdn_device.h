@@ -88,6 +88,43 @@ __device__ __forceinline__ int load_cu(const void *cu, int is64, int i, int T) {
   return static_cast<int>(x > T ? T : x);
 }
 
+// Token rows of a packed batch that no sequence covers -- [0, cu[0]) and
+// [cu[N], T) -- get a zero output, as in the reference, which zero-fills its
+// output and writes only the rows [cu[s], cu[s+1]) of each sequence
+// (reference/gdn_prefill_ref.py:49-51,56-62).  Workgroup `wg` of `nwg` clears
+// its share with 16-byte stores (out is 16-byte aligned; a token row is
+// hv * 256 bytes).  A batch spanning [0, T), the usual case, costs two uniform
+// loads and a compare.
+__device__ __forceinline__ void zero_uncovered_rows(uint16_t *out, const void *cu, int cu64, int N,
+                                                    int T, int hv, unsigned wg, unsigned nwg) {
+  const int lo = load_cu(cu, cu64, 0, T);
+  int hi = load_cu(cu, cu64, N, T);
+  hi = hi < lo ? lo : hi;
+  if (lo == 0 && hi == T) return;
+  const size_t per_row = static_cast<size_t>(hv) * (kDV / 8);  // 16-byte units per token row
+  const size_t head = static_cast<size_t>(lo) * per_row;
+  const size_t total = head + static_cast<size_t>(T - hi) * per_row;
+  const size_t step = static_cast<size_t>(nwg) * blockDim.x;
+  for (size_t i = static_cast<size_t>(wg) * blockDim.x + threadIdx.x; i < total; i += step) {
+    const size_t u = i < head ? i : i - head + static_cast<size_t>(hi) * per_row;
+    *reinterpret_cast<uint4 *>(out + u * 8) = make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+// A batch of one sequence runs without a chunk table: its tokens are
+// [cu[0], cu[1]) (clamped to [0, T]), read on the device by every kernel that
+// needs them, so no host read of cu_seqlens is ever required.  cu == nullptr:
+// the batch has a chunk table (more than one sequence).
+struct OneSeq {
+  const void *cu;
+  int cu64, T;
+};
+__device__ __forceinline__ void one_seq_bounds(const OneSeq &o, int &bos, int &eos) {
+  bos = load_cu(o.cu, o.cu64, 0, o.T);
+  eos = load_cu(o.cu, o.cu64, 1, o.T);
+  eos = eos < bos ? bos : eos;
+}
+
 }  // namespace gdn
 
 namespace gdn {

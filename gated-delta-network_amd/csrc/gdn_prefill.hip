@@ -244,11 +244,13 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
   for (int c = nt + tid; c < nt_max; c += 1024) chunks[c] = make_int4(-1, 0, 0, 0);
 }
 
-// Chunk c of the table; for a single sequence (single_T = its length T >= 0)
-// there is no table and the entry is computed directly.
-__device__ __forceinline__ int4 chunk_info(const int4 *chunks, int c, int single_T) {
-  if (single_T >= 0) {
-    const int start = c * kChunk, rest = single_T - start;
+// Chunk c of the table; for a single sequence (one.cu != nullptr) there is no
+// table and the entry is computed from the sequence's bounds.
+__device__ __forceinline__ int4 chunk_info(const int4 *chunks, int c, const OneSeq &one) {
+  if (one.cu != nullptr) {
+    int bos, eos;
+    one_seq_bounds(one, bos, eos);
+    const int start = bos + c * kChunk, rest = eos - start;
     return rest > 0 ? make_int4(0, start, rest < kChunk ? rest : kChunk, c) : make_int4(-1, 0, 0, 0);
   }
   // the same entry in every lane: keep it in SGPRs (buffer descriptors built
@@ -728,7 +730,7 @@ __global__ __launch_bounds__(256) void prefill_intra_wy_kernel(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
-    const int4 *__restrict__ chunks, int single_T, int nt_max, Heads H,
+    const int4 *__restrict__ chunks, OneSeq one, int nt_max, Heads H,
     const int *__restrict__ form_flag, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
     float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u,
     uint16_t *__restrict__ ws_kt) {
@@ -736,7 +738,7 @@ __global__ __launch_bounds__(256) void prefill_intra_wy_kernel(
   if (form_flag != nullptr && *form_flag != 0) return;
   int c, h;
   if (!chunk_head_of(blockIdx.x, nt_max, H, c, h)) return;
-  const int4 ch = chunk_info(chunks, c, single_T);
+  const int4 ch = chunk_info(chunks, c, one);
   if (ch.x < 0) return;
   wy_intra(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u,
            ws_kt);
@@ -745,7 +747,7 @@ __global__ __launch_bounds__(256) void prefill_intra_wy_kernel(
 __global__ __launch_bounds__(256) void prefill_intra_t_kernel(
     const uint16_t *__restrict__ k, const float *__restrict__ A_log,
     const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
-    const uint16_t *__restrict__ b, const int4 *__restrict__ chunks, int single_T, int nt_max,
+    const uint16_t *__restrict__ b, const int4 *__restrict__ chunks, OneSeq one, int nt_max,
     Heads H, const int *__restrict__ form_flag, float *__restrict__ ws_G,
     float *__restrict__ ws_dcy, float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w,
     float *__restrict__ ws_u) {
@@ -753,7 +755,7 @@ __global__ __launch_bounds__(256) void prefill_intra_t_kernel(
   if (form_flag != nullptr && *form_flag != 1) return;
   int c, h;
   if (!chunk_head_of(blockIdx.x, nt_max, H, c, h)) return;
-  const int4 ch = chunk_info(chunks, c, single_T);
+  const int4 ch = chunk_info(chunks, c, one);
   if (ch.x < 0) return;
   t_intra(smem, c, h, ch.y, ch.z, k, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u);
 }
@@ -1244,7 +1246,8 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
     const uint16_t *k, const uint16_t *v, const float *state, float *new_state,
     const int4 *chunks, const int *offsets, const float *ws_dcy, const float *ws_eg,
     const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt, uint16_t *ws_ht,
-    uint16_t *ws_vnt, int N, int single_T, Heads H, int form, SplitScan sp) {
+    uint16_t *ws_vnt, int N, OneSeq one, Heads H, int form, SplitScan sp, const void *cu,
+    int cu64, int T, uint16_t *out) {
   __shared__ __align__(16) char smem[kStateWyLds > kStateTLds ? kStateWyLds : kStateTLds];
   constexpr int NVB = kDV / 16;
   const int h = blockIdx.x % H.v;
@@ -1253,45 +1256,46 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in SGPRs
 
-  // This workgroup's chunks: c0 .. c0 + nch - 1.
-  int c0 = 0, nch = (single_T + kChunk - 1) / kChunk;
+  // This workgroup's chunks: c0 .. c0 + nch - 1; the sequence's tokens [bos, eos).
+  int c0 = 0, nch = 0, bos = 0, eos = 0;
   size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;  // [V][K]
-  if (sp.nt0 > 0) {  // two-segment scan of one sequence (single_T >= 0, WY form)
-    sbase = static_cast<size_t>(h) * kDV * kDK;
-    if (s == 2) {
-      wy_state<true>(smem, sp.nt0, nch - sp.nt0, h, vb * 16, wave, lane, sbase, nullptr, sp.mend,
-                     ws_dcy, ws_eg, ws_w, ws_u, ws_kt, sp.htm, ws_vnt, H, sp.nt0);
-      return;
-    }
-    if (s == 0) {
-      nch = sp.nt0;
-      new_state = sp.send;
-    } else {
-      c0 = sp.nt0;
-      nch -= sp.nt0;
-      state = nullptr;
-      new_state = sp.cend;
-    }
-  } else if (single_T < 0) {
-    if (offsets[N + 1]) return;  // the token-sequential kernel owns the batch
+  if (one.cu != nullptr) {
+    one_seq_bounds(one, bos, eos);
+    nch = (eos - bos + kChunk - 1) / kChunk;
+  } else {
+    if (offsets[N + 1]) return;  // the sequential kernel owns the batch
     if (form < 0) form = offsets[N + 2];
     c0 = offsets[s];
     nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
-  }
-  if (form == 1) {
-    // the T form reads K and V itself: the sequence's tokens [bos, eos)
-    int bos = 0, eos = single_T;
-    if (single_T < 0 && nch > 0) {
+    if (form == 1 && nch > 0) {  // the T form's token range
       const int4 first = chunks[c0], last = chunks[c0 + nch - 1];
       bos = first.y;
       eos = last.y + last.z;
     }
+  }
+  if (sp.nt0 > 0) {  // two-segment scan of one sequence (WY form)
+    sbase = static_cast<size_t>(h) * kDV * kDK;
+    if (s == 2) {
+      wy_state<true>(smem, sp.nt0, nch - sp.nt0, h, vb * 16, wave, lane, sbase, nullptr, sp.mend,
+                     ws_dcy, ws_eg, ws_w, ws_u, ws_kt, sp.htm, ws_vnt, H, sp.nt0);
+    } else if (s == 0) {
+      wy_state<false>(smem, 0, nch < sp.nt0 ? nch : sp.nt0, h, vb * 16, wave, lane, sbase, state,
+                      sp.send, ws_dcy, ws_eg, ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0);
+    } else {
+      wy_state<false>(smem, sp.nt0, nch - sp.nt0, h, vb * 16, wave, lane, sbase, nullptr, sp.cend,
+                      ws_dcy, ws_eg, ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0);
+    }
+  } else if (form == 1) {
+    // the T form reads K and V itself: the sequence's tokens [bos, eos)
     t_state(smem, c0, nch, bos, eos, h, vb * 16, wave, lane, sbase, k, v, state, new_state, ws_dcy,
             ws_eg, ws_w, ws_u, ws_ht, ws_vnt, H);
-  }
-  else
+  } else {
     wy_state<false>(smem, c0, nch, h, vb * 16, wave, lane, sbase, state, new_state, ws_dcy, ws_eg,
                     ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0);
+  }
+  // The chunk pipeline owns the batch: rows outside every sequence get zeros
+  // (after the chain, so that the common case's check costs the chain nothing).
+  zero_uncovered_rows(out, cu, cu64, N, T, H.v, blockIdx.x, gridDim.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1320,7 +1324,7 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
 constexpr int kSplitOutLds = 2 * kChunk * kStrideK * 2 + kDV * kStrideK * 2 + kChunk * kStrideT * 2 + kChunk * 4;
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_split_out_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
-                              int T, int nt, Heads H, SplitScan sp,
+                              OneSeq one, Heads H, SplitScan sp,
                               const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_w,
                               const float *__restrict__ ws_u, const uint16_t *__restrict__ ws_ht,
                               float scale, uint16_t *__restrict__ out) {
@@ -1330,7 +1334,11 @@ void prefill_split_out_kernel(const uint16_t *__restrict__ q, const uint16_t *__
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int id = blockIdx.x;
   const int c = sp.nt0 + id / H.v, h = id % H.v;
-  const int start = c * kChunk, len = T - start < kChunk ? T - start : kChunk;
+  int bos, eos;
+  one_seq_bounds(one, bos, eos);
+  const int start = bos + c * kChunk, rest = eos - start;
+  if (rest <= 0) return;  // past the sequence's last chunk
+  const int len = rest < kChunk ? rest : kChunk;
   const int hq = h / H.ratio;
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
   const int r16 = lane & 15, g = lane >> 4, kg = 8 * g, q4 = 4 * g;
@@ -1601,7 +1609,7 @@ __device__ __forceinline__ void split_state_tile(char *smem, int f, const Heads 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 void prefill_output_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
-    const int4 *__restrict__ chunks, int single_T, int nt_max, Heads H,
+    const int4 *__restrict__ chunks, OneSeq one, int nt_max, Heads H,
     const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
     uint16_t *__restrict__ out, SplitScan sp, float *__restrict__ new_state) {
   // 27 KB of LDS and at most 128 VGPRs: four workgroups per CU.
@@ -1619,7 +1627,7 @@ void prefill_output_kernel(
   }
   int c, h;
   if (!chunk_head_of(blockIdx.x - nfix, nt_max, H, c, h)) return;
-  const int4 ch = chunk_info(chunks, c, single_T);
+  const int4 ch = chunk_info(chunks, c, one);
   if (ch.x < 0) return;
   const int start = ch.y, len = ch.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1745,6 +1753,12 @@ void prefill_output_kernel(
   }
 }
 
+// The output of a batch without sequences (N == 0): every row is zero.
+__global__ __launch_bounds__(256) void prefill_zero_kernel(uint16_t *out, const void *cu, int cu64,
+                                                           int T, int hv) {
+  zero_uncovered_rows(out, cu, cu64, 0, T, hv, blockIdx.x, gridDim.x);
+}
+
 // Path choice between a sequential kernel and the chunk pipeline, from
 // sweeps of all three paths on MI355X.  A batch of at most kRecurrentMaxLen
 // tokens runs sequentially: token by token, or one sequence in blocks when
@@ -1788,6 +1802,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: q/k/v must be 16-byte aligned");
   if (!aligned(new_state, 16) || (state && !aligned(state, 16)))
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: state/new_state must be 16-byte aligned");
+  if (!aligned(output, 16)) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: output must be 16-byte aligned");
   if (!aligned(cu_seqlens, cu64 ? 8 : 4))
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: cu_seqlens misaligned");
   if (variant < -1 || variant > 3)
@@ -1796,11 +1811,16 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   if (rec_max < -2) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: recurrent_max_len %d < -2", rec_max);
   if (rec_variant < -1 || rec_variant >= recurrent_num_variants())
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown recurrent tiling %d", rec_variant);
-  if (N == 0) return GDN_OK;
+  if (N == 0 && T == 0) return GDN_OK;
 
-  const PrefillLayout L = prefill_layout(T, N, H);
-  if (!workspace || ws_bytes < L.total)
+  // (a batch without sequences only zero-fills the output: no workspace needed)
+  PrefillLayout L = prefill_layout(T, N, H);
+  if (N == 0) {
+    workspace = nullptr;
+    L.total = 0;
+  } else if (!workspace || ws_bytes < L.total) {
     return fail(GDN_ERR_WORKSPACE, "gdn_prefill_fwd: workspace of %zu bytes, %zu needed", ws_bytes, L.total);
+  }
   if (!aligned(workspace, 256)) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: workspace must be 256-byte aligned");
 
   const size_t nT = static_cast<size_t>(T), nN = static_cast<size_t>(N);
@@ -1828,6 +1848,13 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: outputs/workspace overlap");
 
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  if (N == 0) {  // no sequence: every output row is zero
+    const size_t units = nT * nV * (kDV / 8);
+    const unsigned grid = static_cast<unsigned>(units / 256 + 1 < 1024 ? units / 256 + 1 : 1024);
+    hipLaunchKernelGGL(prefill_zero_kernel, dim3(grid), dim3(256), 0, stream, output, cu_seqlens,
+                       cu64, T, H.v);
+    return check_launch("gdn_prefill_fwd(zero)");
+  }
   char *ws = static_cast<char *>(workspace);
   int4 *chunks = reinterpret_cast<int4 *>(ws + L.chunks);
   int *offsets = reinterpret_cast<int *>(ws + L.offsets);
@@ -1882,9 +1909,10 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
                             nullptr, H, scale, output, new_state, stream, seq_var,
                             "gdn_prefill_fwd");
-  // One sequence is [0, T) by the cu_seqlens contract: its chunks follow
-  // from T, and the kernels compute them instead of reading a table.
-  const int single_T = (N == 1 && choose == 0) ? T : -1;
+  // One sequence needs no chunk table: the kernels read its bounds
+  // [cu[0], cu[1]) themselves and compute its chunks.
+  const OneSeq one{(N == 1 && choose == 0) ? cu_seqlens : nullptr, cu64, T};
+  const bool single = one.cu != nullptr;
   int rc = GDN_OK;
   // Form of the per-chunk operands: `variant` when 0 (WY) or 1 (T); else the
   // index kernel's rule (T iff at least 128 chunks and three times the
@@ -1895,10 +1923,10 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   int form = variant >= 2 ? 0 : variant;
   if (form < 0) {
     const long long mean_chunks = ((static_cast<long long>(T) + N - 1) / N + kChunk - 1) / kChunk;
-    const bool t_possible = single_T < 0 && N > 2 && L.nt_max >= 128 && L.nt_max >= 3 * mean_chunks;
+    const bool t_possible = !single && N > 2 && L.nt_max >= 128 && L.nt_max >= 3 * mean_chunks;
     form = t_possible ? -1 : 0;
   }
-  if (single_T < 0) {
+  if (!single) {
     hipLaunchKernelGGL(prefill_index_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, cu64, N, T,
                        L.nt_max, choose, rec_max, H.v, form, chunks, offsets);
     if ((rc = check_launch("gdn_prefill_fwd(index)"))) return rc;
@@ -1916,17 +1944,17 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     const int *flag = form < 0 ? offsets + N + 2 : nullptr;
     if (form != 1) {
       hipLaunchKernelGGL(prefill_intra_wy_kernel, dim3(grid), dim3(256), 0, stream, k, v, A_log, a,
-                         dt_bias, b, chunks, single_T, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu, kt);
+                         dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu, kt);
       if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
     }
     if (form != 0) {
       hipLaunchKernelGGL(prefill_intra_t_kernel, dim3(grid), dim3(256), 0, stream, k, A_log, a,
-                         dt_bias, b, chunks, single_T, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu);
+                         dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu);
       if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
     }
   }
   SplitScan sp{0, nullptr, nullptr, nullptr, nullptr};
-  if (single_T >= 0 && form == 0 && variant != 2 && L.nt_max >= 2 && 24 * H.v <= 256 &&
+  if (single && form == 0 && variant != 2 && L.nt_max >= 2 && 24 * H.v <= 256 &&
       (variant == 3 || L.nt_max >= kSplitMinChunks)) {
     sp.nt0 = split_first(L.nt_max);
     sp.htm = reinterpret_cast<uint16_t *>(ws + L.htm);
@@ -1938,13 +1966,13 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
   hipLaunchKernelGGL(prefill_state_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                      k, v, state, new_state, chunks, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N,
-                     single_T, H, form, sp);
+                     one, H, form, sp, cu_seqlens, cu64, T, output);
   if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
   if (sp.nt0 > 0) {
     // new_state and the output of the second segment's chunks
     const unsigned split_grid = static_cast<unsigned>((L.nt_max - sp.nt0) * H.v);
-    hipLaunchKernelGGL(prefill_split_out_kernel, dim3(split_grid), dim3(256), 0, stream, q, k, T,
-                       L.nt_max, H, sp, wsG, wsw, wsu, ht, scale, output);
+    hipLaunchKernelGGL(prefill_split_out_kernel, dim3(split_grid), dim3(256), 0, stream, q, k, one,
+                       H, sp, wsG, wsw, wsu, ht, scale, output);
     if ((rc = check_launch("gdn_prefill_fwd(split)"))) return rc;
   }
   if (L.nt_max > 0) {
@@ -1953,7 +1981,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     const int out_chunks = sp.nt0 > 0 ? sp.nt0 : L.nt_max;
     const long long out_grid = chunk_head_grid(out_chunks, H) + (sp.nt0 > 0 ? kStateTiles * H.v : 0);
     hipLaunchKernelGGL(prefill_output_kernel, dim3(static_cast<unsigned>(out_grid)), dim3(256), 0,
-                       stream, q, k, chunks, single_T, out_chunks, H, wsG, ht, vnt, scale, output,
+                       stream, q, k, chunks, one, out_chunks, H, wsG, ht, vnt, scale, output,
                        sp, new_state);
     if ((rc = check_launch("gdn_prefill_fwd(output)"))) return rc;
   }

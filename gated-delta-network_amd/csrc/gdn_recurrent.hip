@@ -41,9 +41,9 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
     const uint16_t *__restrict__ v, const float *state, const float *__restrict__ A_log,
     const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
-    const uint16_t *__restrict__ b, const void *__restrict__ cu, int cu64, int T, int fixed_len,
-    const int *__restrict__ enable, Heads H, float scale, uint16_t *__restrict__ out,
-    float *new_state) {
+    const uint16_t *__restrict__ b, const void *__restrict__ cu, int cu64, int N, int T,
+    int fixed_len, const int *__restrict__ enable, Heads H, float scale,
+    uint16_t *__restrict__ out, float *new_state) {
   constexpr int kRows = 4 * WAVES * PASSES;
   constexpr int kTiles = kDV / kRows;
   static_assert(kDV % kRows == 0, "row block must divide 128");
@@ -195,6 +195,8 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
     *reinterpret_cast<f32x4 *>(new_state + off) = Sa[p];
     *reinterpret_cast<f32x4 *>(new_state + off + 64) = Sb[p];
   }
+  // A packed batch: rows outside every sequence get zeros.
+  if (cu != nullptr) zero_uncovered_rows(out, cu, cu64, N, T, H.v, blockIdx.x, gridDim.x);
 }
 
 namespace {
@@ -210,12 +212,12 @@ constexpr int kNumRecVariants = sizeof(kRecVariants) / sizeof(kRecVariants[0]);
 template <int W, int P>
 void launch_rec(long long groups, hipStream_t stream, const uint16_t *q, const uint16_t *k,
                 const uint16_t *v, const float *state, const float *A_log, const uint16_t *a,
-                const float *dt_bias, const uint16_t *b, const void *cu, int cu64, int T,
+                const float *dt_bias, const uint16_t *b, const void *cu, int cu64, int N, int T,
                 int fixed_len, const int *enable, const Heads &H, float scale, uint16_t *out,
                 float *new_state) {
   const long long blocks = groups * (kDV / (4 * W * P));
   hipLaunchKernelGGL((recurrent_kernel<W, P>), dim3(static_cast<unsigned>(blocks)), dim3(64 * W),
-                     0, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T, fixed_len,
+                     0, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, N, T, fixed_len,
                      enable, H, scale, out, new_state);
 }
 
@@ -253,8 +255,8 @@ int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, co
     return fail(GDN_ERR_INVALID, "%s: too many sequences for one launch", what);
 #define GDN_REC(W, P)                                                                          \
   if (rv.waves == W && rv.passes == P)                                                        \
-    launch_rec<W, P>(groups, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, T,       \
-                     fixed_len, enable, H, scale, out, new_state);
+    launch_rec<W, P>(groups, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, num_seqs, \
+                     T, fixed_len, enable, H, scale, out, new_state);
   GDN_REC(1, 1)
   GDN_REC(2, 1)
   GDN_REC(4, 1)

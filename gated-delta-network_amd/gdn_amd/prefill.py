@@ -15,7 +15,13 @@ cache (fla_kernels.py:950-957), which was keyed by name only.  A caller that
 must not allocate inside the call (HIP graph capture, a serving loop) passes
 its own buffer as ``workspace=`` (see ``alloc_workspace``); nothing in the
 call then allocates, copies to the host or synchronises, so one captured graph
-serves any batch of the same (T, N), including new cu_seqlens contents.
+serves any batch of the same (T, N), including new cu_seqlens contents.  A
+graph captured without ``workspace=`` writes into the cached buffer of its
+stream; once a capture has used a cached buffer, that buffer is never freed
+(a larger call later gets a new one), so the graph can always replay into it.
+
+Rows of ``output`` outside every sequence (before cu_seqlens[0] or from
+cu_seqlens[N] on) are written as zeros, as the reference's zero-filled output.
 """
 
 from __future__ import annotations
@@ -28,7 +34,8 @@ from . import _lib
 from ._common import DK, DV, H_QK, HV, check_output, check_tensor, dense, resolve_scale, stream_of
 
 _ws_lock = threading.Lock()
-_workspaces: dict = {}
+_workspaces: dict = {}  # (device, stream) -> [buffer, used by a graph capture]
+_retired: list = []     # replaced buffers that a captured graph may still write
 
 
 def workspace_bytes(total_tokens: int, num_seqs: int, heads=(H_QK, HV)) -> int:
@@ -64,12 +71,17 @@ def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     """A byte buffer of at least nbytes, reused by later calls on the same
     stream (work on one stream is ordered, so reuse needs no sync)."""
     key = (dev.index, stream)
+    capturing = torch.cuda.is_current_stream_capturing()
     with _ws_lock:
-        buf = _workspaces.get(key)
-        if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
-            _workspaces[key] = buf
-        return buf
+        entry = _workspaces.get(key)
+        if entry is None or entry[0].numel() < nbytes:
+            if entry is not None and entry[1]:
+                _retired.append(entry[0])
+            entry = [torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev), False]
+            _workspaces[key] = entry
+        if capturing:
+            entry[1] = True
+        return entry[0]
 
 
 def _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state):
@@ -115,7 +127,8 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
 
     q, k [T,4,128] bf16; v [T,8,128] bf16; state [N,8,128,128] f32 k-last or
     None; A_log, dt_bias [8] f32; a, b [T,8] bf16; cu_seqlens [N+1] int32/int64
-    on the device (0 = cu[0] <= ... <= cu[N] = T); scale float, 0-d tensor or
+    on the device (monotone, within [0, T]; rows outside [cu[0], cu[N]) get
+    zeros); scale float, 0-d tensor or
     None; output [T,8,128] bf16; new_state [N,8,128,128] f32 (may be state).
     ``variant`` picks the form of the per-chunk operands
     (gdn_prefill_fwd_variant): 0 WY, 1 T, -1 the built-in choice; 2 WY with
@@ -138,6 +151,12 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
     q, k, v, a, b, A_log, dt_bias, cu_seqlens = (
         dense(t) for t in (q, k, v, a, b, A_log, dt_bias, cu_seqlens))
     stream = stream_of(dev)
+    # the kernels store 16 bytes at a time: a view at another offset is
+    # computed into an aligned buffer and copied (as the reference's own
+    # output.copy_, fla_kernels.py:1052)
+    dest = output
+    if output.data_ptr() % 16:
+        output = torch.empty_like(output)
     nbytes = workspace_bytes(T, N, heads)
     if workspace is None:
         ws = _workspace(dev, stream, nbytes)
@@ -159,6 +178,8 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
     else:
         rc = lib.gdn_prefill_fwd_variant(*args, int(variant))
     _lib.check(rc, "gdn_prefill_fwd")
+    if dest is not output:
+        dest.copy_(output)
 
 
 def run(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale):

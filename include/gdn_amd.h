@@ -146,11 +146,17 @@ size_t gdn_prefill_workspace_bytes(int total_tokens, int num_seqs);
  *   scale      > 0, already resolved    output     [T, 8, 128] bf16
  *   new_state  [N, 8, 128, 128] f32     workspace  >= gdn_prefill_workspace_bytes(T, N)
  *
- * cu_seqlens stays on the device and is never read by the host: it must start
- * at 0, be non-decreasing and end at T (a violating batch leaves the outputs
- * unspecified but never accesses memory out of bounds).  A zero-length
- * sequence gets an all-zero new_state, as the reference does.  new_state may
- * alias state; output must not overlap any input.
+ * cu_seqlens stays on the device and is never read by the host.  Sequence s
+ * is the tokens [cu_seqlens[s], cu_seqlens[s+1]); the offsets must be
+ * non-decreasing and within [0, T], but need not start at 0 or end at T: as
+ * in the reference (gdn_prefill_ref.py:49-62), the output rows before
+ * cu_seqlens[0] and from cu_seqlens[N] on are written as zeros, and a single
+ * sequence's state covers exactly its own tokens (a decreasing batch leaves
+ * the outputs unspecified but never accesses memory out of bounds).  With
+ * num_seqs = 0 the whole output is zeroed and the workspace may be NULL.  A
+ * zero-length sequence gets an all-zero new_state, as the reference does.
+ * new_state may alias state; output must be 16-byte aligned and must not
+ * overlap any input.
  *
  * The batch takes one of three paths: every sequence token by token with the
  * state in registers (one launch), every sequence in 16-token blocks with the

@@ -239,6 +239,30 @@ def test_prefill_packing_invariance_and_zero_length():
             assert np.array_equal(S[s], S1[0])
 
 
+@pytest.mark.parametrize("cu", [[0, 100], [20, 90], [7, 7, 50, 110], [64, 64], [33]])
+def test_prefill_partial_cu_is_a_shifted_batch(cu):
+    # offsets that do not span [0, T) (reference/gdn_prefill_ref.py:49-62):
+    # the rows outside [cu[0], cu[N]) stay zero, and the covered rows equal
+    # the same batch cut out of the buffer with offsets shifted to start at 0
+    # (checked in C and numpy, so both oracles follow the reference here).
+    T = 128
+    N = len(cu) - 1
+    inp = O.make_prefill_inputs([T], seed=24, with_state=False)
+    rng = np.random.default_rng(25)
+    inp["state"] = (0.05 * rng.standard_normal((N, O.HV, O.DV, O.DK))).astype(np.float32)
+    inp["cu_seqlens"] = np.array(cu, np.int64)
+    lo, hi = cu[0], cu[-1]
+    cut = {k: (v[lo:hi] if k in ("q", "k", "v", "a", "b") else v) for k, v in inp.items()}
+    cut["cu_seqlens"] = np.array(cu, np.int64) - lo
+    o_cut, S_cut = O.prefill_seq(**cut)
+    for fn in (O.prefill_seq, O.prefill_seq_c):
+        o, S = fn(**inp)
+        assert not o[:lo].any() and not o[hi:].any()
+        if hi > lo:
+            assert np.abs(o[lo:hi] - o_cut).max() <= 2 ** -7 * np.abs(o_cut).max()
+        assert S.shape == S_cut.shape and (N == 0 or np.abs(S - S_cut).max() < 1e-6)
+
+
 def test_prefill_state_none_equals_zero_state():
     inp = O.make_prefill_inputs([12, 7], seed=23, with_state=False)
     o1, S1 = O.prefill_seq(**inp)
