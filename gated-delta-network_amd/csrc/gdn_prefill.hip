@@ -50,6 +50,8 @@
 // when the other operand is exact in bf16 (K, V).  u, w, T and the state stay
 // f32.  The output path (Q S, Q K^T, P v_new) uses single bf16 operands: its
 // error stays ~2^-9 relative, far inside the bf16 output tolerance.
+#include <mutex>
+
 #include "gdn_device.h"
 #include "gdn_host.h"
 
@@ -2053,4 +2055,80 @@ extern "C" int gdn_prefill_fwd_heads(const gdn_bf16 *q, const gdn_bf16 *k, const
                              num_seqs, total_tokens, scale, output, new_state, workspace,
                              workspace_bytes, stream, state_tiling, recurrent_max_len,
                              recurrent_tiling, num_qk_heads, num_v_heads);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free prefill.  The workspace is `scratch`, a file-scope device
+// array of GDN_PREFILL_SCRATCH_BYTES: every GPU the library runs on holds its
+// own copy, at its own address, until the process ends.  That address is
+// looked up once per device (hipGetSymbolAddress with the device current, on
+// the entry point's first call there) and only the looked-up pointer is
+// handed to the kernels: in host code the array's name is a stand-in, not a
+// device address.  Nothing in the workspace needs to start at zero -- every
+// region is written by an earlier kernel of the same call before it is read
+// -- so the previous call's contents are harmless.  All calls on one GPU
+// share its array: calls that overlap in time on one GPU (different streams
+// or host threads without ordering) race on it.
+// ---------------------------------------------------------------------------
+namespace gdn {
+
+static __device__ __align__(256) unsigned char scratch[GDN_PREFILL_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mutex;
+static void *g_scratch_ptr[kMaxScratchDevices];
+
+// The scratch array of the device `stream` runs on, which must be the current
+// device (the lookup resolves the array of the current device).
+static int device_scratch(void *stream, void **ptr) {
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess || cur < 0 || cur >= kMaxScratchDevices)
+    return fail(GDN_ERR_LAUNCH, "gdn_prefill_fwd_noalloc: no usable current device (%s)",
+                hipGetErrorString(e));
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess)
+      return fail(GDN_ERR_INVALID, "gdn_prefill_fwd_noalloc: bad stream (%s)", hipGetErrorString(e));
+    if (sdev != cur)
+      return fail(GDN_ERR_INVALID, "gdn_prefill_fwd_noalloc: the stream is on device %d, the "
+                  "current device is %d", static_cast<int>(sdev), cur);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[cur] == nullptr) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(GDN_ERR_LAUNCH, "gdn_prefill_fwd_noalloc: hipGetSymbolAddress(scratch) on device "
+                  "%d failed: %s", cur, hipGetErrorString(e));
+    g_scratch_ptr[cur] = p;
+  }
+  *ptr = g_scratch_ptr[cur];
+  return GDN_OK;
+}
+
+}  // namespace gdn
+
+extern "C" int gdn_prefill_fwd_noalloc(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                                       const float *state, const float *A_log, const gdn_bf16 *a,
+                                       const float *dt_bias, const gdn_bf16 *b,
+                                       const void *cu_seqlens, int cu_seqlens_is_int64,
+                                       int num_seqs, int total_tokens, float scale,
+                                       gdn_bf16 *output, float *new_state, void *stream) {
+  gdn::clear_error();
+  if (total_tokens < 0 || num_seqs < 0)
+    return gdn::fail(GDN_ERR_INVALID, "gdn_prefill_fwd_noalloc: num_seqs=%d, total_tokens=%d",
+                     num_seqs, total_tokens);
+  const size_t need = gdn_prefill_workspace_bytes(total_tokens, num_seqs);
+  if (need > GDN_PREFILL_SCRATCH_BYTES)
+    return gdn::fail(GDN_ERR_WORKSPACE, "gdn_prefill_fwd_noalloc: %d tokens in %d sequences need "
+                     "%zu bytes of workspace, more than the %zu-byte static scratch (use "
+                     "gdn_prefill_fwd with a workspace)", total_tokens, num_seqs, need,
+                     static_cast<size_t>(GDN_PREFILL_SCRATCH_BYTES));
+  void *ws = nullptr;
+  if (int rc = gdn::device_scratch(stream, &ws)) return rc;
+  return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
+                             num_seqs, total_tokens, scale, output, new_state, ws,
+                             GDN_PREFILL_SCRATCH_BYTES, stream, -1, -1, -1, gdn::kHQK, gdn::kHV);
 }

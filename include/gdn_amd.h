@@ -250,6 +250,27 @@ int gdn_prefill_fwd_heads(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
                           int state_tiling, int recurrent_max_len, int recurrent_tiling);
 
 /*
+ * gdn_prefill_fwd without a workspace argument: an entry point that
+ * allocates nothing, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, semantics,
+ * kernels and results as gdn_prefill_fwd; the workspace is a static device
+ * array of GDN_PREFILL_SCRATCH_BYTES per GPU, held until the process ends, so
+ * a batch needing more (gdn_prefill_workspace_bytes(T, N) above the maximum:
+ * e.g. one sequence of more than ~3,700 tokens) is refused with
+ * GDN_ERR_WORKSPACE.  `stream` must belong to the current device.  Calls that
+ * overlap in time on one GPU share that array and race: order them (one
+ * stream, or events).  The first call on a device looks up the array's
+ * device address (no allocation).
+ */
+#define GDN_PREFILL_SCRATCH_BYTES (64u << 20)
+int gdn_prefill_fwd_noalloc(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
+                            const float *state, const float *A_log, const gdn_bf16 *a,
+                            const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
+                            int cu_seqlens_is_int64, int num_seqs, int total_tokens, float scale,
+                            gdn_bf16 *output, float *new_state, void *stream);
+
+/*
  * Measurement support (no counterpart in the reference): copies `bytes`
  * bytes from src to dst in the decode kernel's access pattern (one wave per
  * 32 KiB, every load before the first store, non-temporal), i.e. the HBM
