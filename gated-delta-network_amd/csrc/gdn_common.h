@@ -1,0 +1,67 @@
+// Definitions shared by the kernels and the host-side planning code.  This
+// header includes no HIP header, so the host-side code (gdn_args.cpp) also
+// builds with a plain host compiler -- the CPU sanitizer build does that,
+// defining __host__ and __device__ empty on its command line.
+#pragma once
+
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace gdn {
+
+constexpr int kHQK = 4;    // q/k heads of the reference definitions
+constexpr int kHV = 8;     // their v heads; v-head h reads q/k head h / 2
+constexpr int kDK = 128;   // key head size
+constexpr int kDV = 128;   // value head size
+constexpr int kChunk = 64; // prefill chunk length
+
+// Head layout of a call: qk q/k heads, v v-heads, v a multiple of qk; v-head h
+// reads q/k head h / ratio (GVA without copies).  Head size is always 128.
+struct Heads {
+  int qk, v, ratio;
+};
+
+// Path cost models in microseconds, fitted to graph-replay sweeps of each
+// path on MI355X (sequence count N = 1..256 of equal lengths L = 8..256,
+// multi-token decode B = 1..128 with 4..16 tokens).  L = longest sequence,
+// T = tokens, nt = chunks of 64, g = N * hv (sequence, v-head) groups.
+// Token by token (recurrent kernel): the serial token chain plus VALU work
+// per token and state traffic per group.
+__host__ __device__ inline float cost_by_token(float L, float T, float hv, float g) {
+  return 3.0f + 0.24f * L + 0.003f * T * hv + 0.021f * g;
+}
+// 16-token blocks (block kernel): two workgroups of 64 columns per group up
+// to 128 groups (~2.8 us per block), then one of 128 columns per group, two
+// resident per CU (512 on the chip): ~3.5 us per block alone on a CU, ~4.7 us
+// two to a CU; plus the state's traffic per group.
+__host__ __device__ inline float cost_by_block(float L, float g) {
+  const float rounds = ceilf(g / 512.0f), blocks = ceilf(L / 16.0f);
+  const float per_block = g <= 128.0f ? 2.8f : g <= 256.0f ? 3.5f : 4.7f;
+  return 4.5f + 0.015f * g + 0.008f * fmaxf(g - 256.0f, 0.0f) + rounds * blocks * per_block;
+}
+// Chunks: fixed launches, per-sequence work up to ~40 sequences and the
+// per-chunk throughput beyond, plus the serial chunk chain of the longest.
+__host__ __device__ inline float cost_by_chunks(float L, float nt, float hv, float g) {
+  const float per_seq = fminf(0.13f * g, 11.0f + 0.081f * g);
+  return 20.0f + fmaxf(per_seq, 0.081f * nt * hv) + 0.5f * ceilf(L / 64.0f);
+}
+
+// First chunk of the second segment of a two-segment scan over nt chunks.
+__host__ __device__ inline int split_first(int nt) { return (nt + 1) / 2; }
+
+// Workgroups of a per-(chunk, v-head) launch over nt chunk slots: the pairs
+// (chunk, q/k head) rounded up to a multiple of the 8 XCDs, times the v-heads
+// per q/k head (the mapping is chunk_head_of in gdn_prefill.hip).
+__host__ __device__ inline long long chunk_head_grid(int nt, const Heads &H) {
+  return (static_cast<long long>(nt) * H.qk + 7) / 8 * 8 * H.ratio;
+}
+
+// Row tilings of the token-by-token kernel (gdn_recurrent.hip); the
+// sequential-kernel index kNumRecTilings names the 16-token block kernel.
+constexpr int kNumRecTilings = 10;
+
+// new_state tiles of a two-segment scan, per v-head (16 rows x 32 columns).
+constexpr int kStateTiles = (kDV / 16) * (kDK / 32);
+
+}  // namespace gdn

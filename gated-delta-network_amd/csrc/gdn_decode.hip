@@ -185,35 +185,10 @@ int decode_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v, const
                   float scale, gdn_bf16 *output, float *new_state, int batch, void *stream,
                   int variant, const Heads &H, const char *what) {
   clear_error();
-  if (batch < 0) return fail(GDN_ERR_INVALID, "%s: batch=%d < 0", what, batch);
-  if (!q || !k || !v || !A_log || !a || !dt_bias || !b || !output || !new_state)
-    return fail(GDN_ERR_INVALID, "%s: null pointer argument", what);
-  if (!(scale > 0.0f) || scale == __builtin_inff())
-    return fail(GDN_ERR_INVALID, "%s: scale must be finite and > 0", what);
-  if (!aligned(new_state, 16) || (state && !aligned(state, 16)))
-    return fail(GDN_ERR_INVALID, "%s: state/new_state must be 16-byte aligned", what);
-  if (!aligned(q, 8) || !aligned(k, 8))
-    return fail(GDN_ERR_INVALID, "%s: q/k must be 8-byte aligned", what);
+  if (int rc = check_decode_args(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
+                                 batch, 1, H, what))
+    return rc;
   if (batch == 0) return GDN_OK;
-  const size_t nb = static_cast<size_t>(batch);
-  const size_t nV = static_cast<size_t>(H.v), nQK = static_cast<size_t>(H.qk);
-  const size_t state_bytes = nb * nV * kDV * kDK * sizeof(float);
-  const size_t out_bytes = nb * nV * kDV * sizeof(uint16_t);
-  // new_state may be exactly state (in-place); no other overlap is allowed.
-  if (state != new_state && overlaps(state, state_bytes, new_state, state_bytes))
-    return fail(GDN_ERR_INVALID, "%s: new_state partially overlaps state", what);
-  const void *ins[] = {q, k, v, a, b, A_log, dt_bias, state};
-  const size_t in_bytes[] = {nb * nQK * kDK * 2, nb * nQK * kDK * 2, nb * nV * kDV * 2,
-                             nb * nV * 2,        nb * nV * 2,        nV * 4,
-                             nV * 4,             state ? state_bytes : 0};
-  for (int i = 0; i < 8; ++i) {
-    if (overlaps(output, out_bytes, ins[i], in_bytes[i]))
-      return fail(GDN_ERR_INVALID, "%s: output overlaps an input", what);
-    if (i < 7 && overlaps(new_state, state_bytes, ins[i], in_bytes[i]))
-      return fail(GDN_ERR_INVALID, "%s: new_state overlaps an input", what);
-  }
-  if (overlaps(output, out_bytes, new_state, state_bytes))
-    return fail(GDN_ERR_INVALID, "%s: output overlaps new_state", what);
 
   // The built-in tiling depends on the number of state rows, counted in
   // batch rows of the reference layout (8 v-heads).

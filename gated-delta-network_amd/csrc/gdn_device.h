@@ -4,19 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "gdn_common.h"
+
 namespace gdn {
-
-constexpr int kHQK = 4;    // q/k heads of the reference definitions
-constexpr int kHV = 8;     // their v heads; v-head h reads q/k head h / 2
-constexpr int kDK = 128;   // key head size
-constexpr int kDV = 128;   // value head size
-constexpr int kChunk = 64; // prefill chunk length
-
-// Head layout of a call: qk q/k heads, v v-heads, v a multiple of qk; v-head h
-// reads q/k head h / ratio (GVA without copies).  Head size is always 128.
-struct Heads {
-  int qk, v, ratio;
-};
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));

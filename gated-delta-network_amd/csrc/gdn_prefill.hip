@@ -63,58 +63,6 @@ constexpr int kStrideT = 72;   // bf16 [*][64]   tiles
 
 constexpr int kTElems = kChunk * kChunk * 2;  // T of one (chunk, head): hi + lo bf16
 
-// Workspace layout; every region starts on a 256-byte boundary.
-struct PrefillLayout {
-  int nt_max;  // upper bound on the chunk count from (T, N) alone
-  // The T form keeps T in the w region and (beta, beta e^G) in the u region.
-  size_t chunks, offsets, G, dcy, eg, w, u, kt, ht, vnt;
-  // Two-segment scan of one sequence (N == 1 only, else empty): the map's
-  // linear part per chunk of the second segment, the first segment's final
-  // state and the second segment's map (offset, linear part).
-  size_t htm, send, cend, mend, total;
-};
-
-// First chunk of the second segment of a two-segment scan over nt chunks.
-__host__ __device__ inline int split_first(int nt) { return (nt + 1) / 2; }
-
-static long long max_chunks(long long T, long long N) {
-  if (T <= 0 || N <= 0) return 0;
-  const long long bound = (T + N * (kChunk - 1)) / kChunk;
-  return bound < T ? bound : T;
-}
-
-static PrefillLayout prefill_layout(int T, int N, const Heads &H) {
-  PrefillLayout L{};
-  const long long nt = max_chunks(T, N);
-  L.nt_max = static_cast<int>(nt);
-  size_t off = 0;
-  auto take = [&](size_t bytes) {
-    const size_t o = off;
-    off = (off + bytes + 255) & ~static_cast<size_t>(255);
-    return o;
-  };
-  const size_t n = static_cast<size_t>(nt);
-  L.chunks = take(n * sizeof(int4));
-  L.offsets = take((static_cast<size_t>(N) + 3) * sizeof(int));  // + path and form flags
-  const size_t hv = static_cast<size_t>(H.v), hqk = static_cast<size_t>(H.qk);
-  L.G = take(n * hv * kChunk * 4);
-  L.dcy = take(n * hv * kChunk * 4);
-  L.eg = take(n * hv * 4);
-  L.w = take(n * hv * kChunk * kDK * 4);  // hi and lo bf16
-  L.u = take(n * hv * kChunk * kDV * 4);
-  L.kt = take(n * hqk * kDK * kChunk * 2);
-  L.ht = take(n * hv * kDV * kDK * 2);
-  L.vnt = take(n * hv * kDV * kChunk * 2);
-  const size_t n1 = N == 1 ? static_cast<size_t>(nt - split_first(static_cast<int>(nt))) : 0;
-  const size_t one = N == 1 ? 1 : 0;
-  L.htm = take(n1 * hv * kDV * kDK * 2);
-  L.send = take(one * hv * kDV * kDK * 4);
-  L.cend = take(one * hv * kDV * kDK * 4);
-  L.mend = take(one * hv * kDV * kDK * 4);
-  L.total = off;
-  return L;
-}
-
 // ---------------------------------------------------------------------------
 // 1. chunk table: chunks[c] = {sequence, first token, tokens (1..64), chunk
 // number within the sequence} for c < NT, {-1, 0, 0, 0} up to nt_max;
@@ -269,9 +217,6 @@ __device__ __forceinline__ int4 chunk_info(const int4 *chunks, int c, const OneS
 // v-heads of one (chunk, q/k head) pair -- the second and later ones find
 // that chunk's q/k rows in the XCD's L2.  Pairs are numbered P = 8 p + x in
 // chunk-major order.  False for ids past the last pair.
-__host__ __device__ inline long long chunk_head_grid(int nt, const Heads &H) {
-  return (static_cast<long long>(nt) * H.qk + 7) / 8 * 8 * H.ratio;
-}
 __device__ __forceinline__ bool chunk_head_of(int id, int nt, const Heads &H, int &c, int &h) {
   const int x = id & 7, sl = id >> 3;
   const int p = sl / H.ratio, r = sl - p * H.ratio;
@@ -1562,7 +1507,6 @@ void prefill_split_out_kernel(const uint16_t *__restrict__ q, const uint16_t *__
 // +31 of head h, new_state = S0 M + C in f32 FMAs, with S0's rows and M's
 // columns staged in LDS (24 KB of the output kernel's 27 KB).  Thread t owns
 // column 32 cb + (t & 31) of rows 16 rb + (t >> 5) and 16 rb + (t >> 5) + 8.
-constexpr int kStateTiles = (kDV / 16) * (kDK / 32);  // per head
 __device__ __forceinline__ void split_state_tile(char *smem, int f, const Heads &H,
                                                  const SplitScan &sp, float *new_state) {
   constexpr size_t kElems = static_cast<size_t>(kDV) * kDK;
@@ -1761,102 +1705,39 @@ __global__ __launch_bounds__(256) void prefill_zero_kernel(uint16_t *out, const 
   zero_uncovered_rows(out, cu, cu64, 0, T, hv, blockIdx.x, gridDim.x);
 }
 
-// Path choice between a sequential kernel and the chunk pipeline, from
-// sweeps of all three paths on MI355X.  A batch of at most kRecurrentMaxLen
-// tokens runs sequentially: token by token, or one sequence in blocks when
-// the cost models favour them (one sequence of 64 tokens: 16.1 us in blocks,
-// 20.1 us token by token, 20.7 us chunked).  Otherwise the sequential candidate is the
-// block kernel (gdn_block.hip) or the token-by-token kernel, whichever the
-// cost models (gdn_host.h) rate faster at the mean length, and the device
-// compares its cost model with the chunks' at the batch's longest sequence
-// (index kernel) -- unless the host already knows the chunks win: the
-// candidate's cost at the mean length (a lower bound on the longest) exceeds
-// the chunks' at the largest longest sequence (T) and chunk count (nt_max)
-// possible.
-constexpr int kRecurrentMaxLen = 96;
-
-// Two-segment scan of one sequence (state kernel, SplitScan): three groups of
-// 8 workgroups per v-head, one per CU, so it needs 24 H.v <= 256; the built-in
-// choice takes it from kSplitMinChunks chunks on (MI355X, graph replay: one
-// chain vs two segments 41.0 vs 44.9 us at 16 chunks, 54.2 vs 51.6 at 32,
-// 173.9 vs ~130 at 128, 308 vs 275 at 256).  Variants: 0 / -1 built in, 2
-// never (one chain), 3 always (one sequence of at least two chunks).
-constexpr int kSplitMinChunks = 32;
-
 static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                           const float *state, const float *A_log, const gdn_bf16 *a,
                           const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
                           int cu64, int N, int T, float scale, gdn_bf16 *output, float *new_state,
                           void *workspace, size_t ws_bytes, void *stream_ptr, int variant,
-                          int rec_max, int rec_variant, int hqk, int hv) {
+                          int rec_max, int rec_variant, int hqk, int hv, const char *what) {
   clear_error();
   Heads H;
-  if (int rc = make_heads(hqk, hv, "gdn_prefill_fwd", H)) return rc;
-  if (N < 0 || T < 0) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: num_seqs=%d, total_tokens=%d", N, T);
-  if (!cu_seqlens) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: null cu_seqlens");
-  if (!A_log || !dt_bias) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: null pointer argument");
-  if (T > 0 && (!q || !k || !v || !a || !b || !output))
-    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: null pointer argument");
-  if (N > 0 && !new_state) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: null new_state");
-  if (!(scale > 0.0f) || scale == __builtin_inff())
-    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: scale must be finite and > 0");
-  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16))
-    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: q/k/v must be 16-byte aligned");
-  if (!aligned(new_state, 16) || (state && !aligned(state, 16)))
-    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: state/new_state must be 16-byte aligned");
-  if (!aligned(output, 16)) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: output must be 16-byte aligned");
-  if (!aligned(cu_seqlens, cu64 ? 8 : 4))
-    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: cu_seqlens misaligned");
-  if (variant < -1 || variant > 3)
-    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown variant %d (0 WY form, 1 T form, 2 WY one "
-                "chain, 3 WY two segments)", variant);
-  if (rec_max < -2) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: recurrent_max_len %d < -2", rec_max);
-  if (rec_variant < -1 || rec_variant >= recurrent_num_variants())
-    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: unknown recurrent tiling %d", rec_variant);
+  if (int rc = make_heads(hqk, hv, what, H)) return rc;
+  PrefillLayout L;
+  if (int rc = check_prefill_args(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T,
+                                  scale, output, new_state, workspace, ws_bytes, variant, rec_max,
+                                  rec_variant, recurrent_num_variants(), H, what, &L))
+    return rc;
   if (N == 0 && T == 0) return GDN_OK;
-
-  // (a batch without sequences only zero-fills the output: no workspace needed)
-  PrefillLayout L = prefill_layout(T, N, H);
-  if (N == 0) {
-    workspace = nullptr;
-    L.total = 0;
-  } else if (!workspace || ws_bytes < L.total) {
-    return fail(GDN_ERR_WORKSPACE, "gdn_prefill_fwd: workspace of %zu bytes, %zu needed", ws_bytes, L.total);
-  }
-  if (!aligned(workspace, 256)) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: workspace must be 256-byte aligned");
-
-  const size_t nT = static_cast<size_t>(T), nN = static_cast<size_t>(N);
-  const size_t nV = static_cast<size_t>(H.v), nQK = static_cast<size_t>(H.qk);
-  const size_t state_bytes = nN * nV * kDV * kDK * 4;
-  const size_t out_bytes = nT * nV * kDV * 2;
-  const void *ins[] = {q, k, v, a, b, A_log, dt_bias, cu_seqlens, state};
-  const size_t in_bytes[] = {nT * nQK * kDK * 2, nT * nQK * kDK * 2, nT * nV * kDV * 2,
-                             nT * nV * 2,        nT * nV * 2,        nV * 4,
-                             nV * 4,             (nN + 1) * (cu64 ? 8 : 4),
-                             state ? state_bytes : 0};
-  for (int i = 0; i < 9; ++i) {
-    if (overlaps(output, out_bytes, ins[i], in_bytes[i]))
-      return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: output overlaps an input");
-    if (i < 8 && overlaps(new_state, state_bytes, ins[i], in_bytes[i]))
-      return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: new_state overlaps an input");
-    if (overlaps(workspace, L.total, ins[i], in_bytes[i]))
-      return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: workspace overlaps an input");
-  }
-  if (state != new_state && overlaps(state, state_bytes, new_state, state_bytes))
-    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: new_state partially overlaps state");
-  if (overlaps(output, out_bytes, new_state, state_bytes) ||
-      overlaps(workspace, L.total, output, out_bytes) ||
-      overlaps(workspace, L.total, new_state, state_bytes))
-    return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: outputs/workspace overlap");
-
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   if (N == 0) {  // no sequence: every output row is zero
-    const size_t units = nT * nV * (kDV / 8);
+    const size_t units = static_cast<size_t>(T) * H.v * (kDV / 8);
     const unsigned grid = static_cast<unsigned>(units / 256 + 1 < 1024 ? units / 256 + 1 : 1024);
     hipLaunchKernelGGL(prefill_zero_kernel, dim3(grid), dim3(256), 0, stream, output, cu_seqlens,
                        cu64, T, H.v);
-    return check_launch("gdn_prefill_fwd(zero)");
+    return check_launch(what);
   }
+  PrefillPlan P;
+  if (int rc = plan_prefill(T, N, H, L, variant, rec_max, rec_variant, recurrent_block_variant(),
+                            what, P))
+    return rc;
+  // The whole batch through one sequential kernel (token by token, or in
+  // 16-token blocks), decided on the host.
+  if (P.sequential)
+    return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
+                            nullptr, H, scale, output, new_state, stream, P.seq_variant, what);
+
   char *ws = static_cast<char *>(workspace);
   int4 *chunks = reinterpret_cast<int4 *>(ws + L.chunks);
   int *offsets = reinterpret_cast<int *>(ws + L.offsets);
@@ -1868,124 +1749,61 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   uint16_t *kt = reinterpret_cast<uint16_t *>(ws + L.kt);
   uint16_t *ht = reinterpret_cast<uint16_t *>(ws + L.ht);
   uint16_t *vnt = reinterpret_cast<uint16_t *>(ws + L.vnt);
-
-  // Path choice: the whole batch runs through one sequential kernel (one
-  // launch) or through the chunk pipeline.  Decided on the host when T and N
-  // settle it, else on the device by the index kernel, which then sets the
-  // path flag read by the sequential and state kernels (and leaves the chunk
-  // table empty).
-  //   rec_max >= 0 (explicit): sequential iff the longest sequence has at
-  //                            most rec_max tokens;
-  //   rec_max == -2:           always chunks;
-  //   rec_max == -1 (built in): token by token if T <= kRecurrentMaxLen;
-  //                            chunks for one longer sequence; else the cost
-  //                            models (see kRecurrentMaxLen).
-  // The sequential kernel is the recurrent tiling rec_variant (the block
-  // kernel when it names it; built in: the token-by-token tiling, or under
-  // the cost models the faster kind at the mean length).
-  const int block_var = recurrent_block_variant();
-  int seq_var = rec_variant;
-  int choose = 0;  // 0 chunks, 1 by rec_max, 2 token vs chunks, 3 blocks vs chunks
-  bool host_sequential = false;
-  if (rec_max >= 0) {
-    host_sequential = rec_max >= T;
-    choose = N > 1 ? 1 : 0;
-  } else if (rec_max == -1) {
-    host_sequential = T <= kRecurrentMaxLen;
-    if (host_sequential && N == 1 && seq_var < 0) {
-      // one short sequence: token by token or in blocks, by the cost models
-      const float fT = static_cast<float>(T), fhv = static_cast<float>(H.v);
-      if (cost_by_block(fT, fhv) < cost_by_token(fT, fT, fhv, fhv)) seq_var = block_var;
-    }
-    if (!host_sequential && N > 1) {
-      const float fT = static_cast<float>(T), fhv = static_cast<float>(H.v);
-      const float g = static_cast<float>(N) * fhv, mean = ceilf(fT / static_cast<float>(N));
-      const float by_token = cost_by_token(mean, fT, fhv, g), by_block = cost_by_block(mean, g);
-      if (seq_var < 0 && by_block < by_token) seq_var = block_var;
-      const bool blocks = seq_var == block_var;
-      const float seq_lo = blocks ? by_block : by_token;
-      if (seq_lo <= cost_by_chunks(fT, static_cast<float>(L.nt_max), fhv, g)) choose = blocks ? 3 : 2;
-    }
-  }
-  if (host_sequential)
-    return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
-                            nullptr, H, scale, output, new_state, stream, seq_var,
-                            "gdn_prefill_fwd");
-  // One sequence needs no chunk table: the kernels read its bounds
-  // [cu[0], cu[1]) themselves and compute its chunks.
-  const OneSeq one{(N == 1 && choose == 0) ? cu_seqlens : nullptr, cu64, T};
-  const bool single = one.cu != nullptr;
+  const OneSeq one{P.single ? cu_seqlens : nullptr, cu64, T};
   int rc = GDN_OK;
-  // Form of the per-chunk operands: `variant` when 0 (WY) or 1 (T); else the
-  // index kernel's rule (T iff at least 128 chunks and three times the
-  // longest sequence's), settled here when (T, N) alone exclude the T form --
-  // one or two sequences, fewer than 128 chunks, or fewer than three times
-  // the chunks of the mean length, a lower bound on the longest -- so that
-  // only one intra kernel is launched.
-  int form = variant >= 2 ? 0 : variant;
-  if (form < 0) {
-    const long long mean_chunks = ((static_cast<long long>(T) + N - 1) / N + kChunk - 1) / kChunk;
-    const bool t_possible = !single && N > 2 && L.nt_max >= 128 && L.nt_max >= 3 * mean_chunks;
-    form = t_possible ? -1 : 0;
-  }
-  if (!single) {
+  // Several sequences: the index kernel builds the chunk table and, when the
+  // plan leaves it to the device (P.choose != 0), sets the path flag read by
+  // the sequential and state kernels (the chunk table is then empty).
+  if (!P.single) {
     hipLaunchKernelGGL(prefill_index_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, cu64, N, T,
-                       L.nt_max, choose, rec_max, H.v, form, chunks, offsets);
-    if ((rc = check_launch("gdn_prefill_fwd(index)"))) return rc;
+                       L.nt_max, P.choose, rec_max, H.v, P.form, chunks, offsets);
+    if ((rc = check_launch(what))) return rc;
   }
-  if (choose != 0) {
+  if (P.choose != 0) {
     rc = recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
-                          offsets + N + 1, H, scale, output, new_state, stream, seq_var,
-                          "gdn_prefill_fwd");
+                          offsets + N + 1, H, scale, output, new_state, stream, P.seq_variant,
+                          what);
     if (rc) return rc;
   }
-  const long long grid_ll = chunk_head_grid(L.nt_max, H);
-  if (grid_ll > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many tokens");
-  const unsigned grid = static_cast<unsigned>(grid_ll);
-  if (L.nt_max > 0) {
-    const int *flag = form < 0 ? offsets + N + 2 : nullptr;
-    if (form != 1) {
-      hipLaunchKernelGGL(prefill_intra_wy_kernel, dim3(grid), dim3(256), 0, stream, k, v, A_log, a,
+  if (P.intra_grid > 0) {
+    const int *flag = P.form < 0 ? offsets + N + 2 : nullptr;
+    const dim3 grid(static_cast<unsigned>(P.intra_grid));
+    if (P.form != 1) {
+      hipLaunchKernelGGL(prefill_intra_wy_kernel, grid, dim3(256), 0, stream, k, v, A_log, a,
                          dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu, kt);
-      if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
+      if ((rc = check_launch(what))) return rc;
     }
-    if (form != 0) {
-      hipLaunchKernelGGL(prefill_intra_t_kernel, dim3(grid), dim3(256), 0, stream, k, A_log, a,
+    if (P.form != 0) {
+      hipLaunchKernelGGL(prefill_intra_t_kernel, grid, dim3(256), 0, stream, k, A_log, a,
                          dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu);
-      if ((rc = check_launch("gdn_prefill_fwd(intra)"))) return rc;
+      if ((rc = check_launch(what))) return rc;
     }
   }
-  SplitScan sp{0, nullptr, nullptr, nullptr, nullptr};
-  if (single && form == 0 && variant != 2 && L.nt_max >= 2 && 24 * H.v <= 256 &&
-      (variant == 3 || L.nt_max >= kSplitMinChunks)) {
-    sp.nt0 = split_first(L.nt_max);
+  SplitScan sp{P.split_nt0, nullptr, nullptr, nullptr, nullptr};
+  if (sp.nt0 > 0) {
     sp.htm = reinterpret_cast<uint16_t *>(ws + L.htm);
     sp.send = reinterpret_cast<float *>(ws + L.send);
     sp.cend = reinterpret_cast<float *>(ws + L.cend);
     sp.mend = reinterpret_cast<float *>(ws + L.mend);
   }
-  const long long blocks = static_cast<long long>(sp.nt0 > 0 ? 3 : N) * H.v * (kDV / 16);
-  if (blocks > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "gdn_prefill_fwd: too many sequences");
-  hipLaunchKernelGGL(prefill_state_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                     k, v, state, new_state, chunks, offsets, wsD, wsE, wsw, wsu, kt, ht, vnt, N,
-                     one, H, form, sp, cu_seqlens, cu64, T, output);
-  if ((rc = check_launch("gdn_prefill_fwd(state)"))) return rc;
-  if (sp.nt0 > 0) {
+  hipLaunchKernelGGL(prefill_state_kernel, dim3(static_cast<unsigned>(P.state_grid)), dim3(256), 0,
+                     stream, k, v, state, new_state, chunks, offsets, wsD, wsE, wsw, wsu, kt, ht,
+                     vnt, N, one, H, P.form, sp, cu_seqlens, cu64, T, output);
+  if ((rc = check_launch(what))) return rc;
+  if (P.split_grid > 0) {
     // new_state and the output of the second segment's chunks
-    const unsigned split_grid = static_cast<unsigned>((L.nt_max - sp.nt0) * H.v);
-    hipLaunchKernelGGL(prefill_split_out_kernel, dim3(split_grid), dim3(256), 0, stream, q, k, one,
-                       H, sp, wsG, wsw, wsu, ht, scale, output);
-    if ((rc = check_launch("gdn_prefill_fwd(split)"))) return rc;
+    hipLaunchKernelGGL(prefill_split_out_kernel, dim3(static_cast<unsigned>(P.split_grid)),
+                       dim3(256), 0, stream, q, k, one, H, sp, wsG, wsw, wsu, ht, scale, output);
+    if ((rc = check_launch(what))) return rc;
   }
-  if (L.nt_max > 0) {
+  if (P.out_grid > 0) {
     // with the two-segment scan, the output kernel covers the first segment
     // and new_state (extra workgroups first in its grid)
     const int out_chunks = sp.nt0 > 0 ? sp.nt0 : L.nt_max;
-    const long long out_grid = chunk_head_grid(out_chunks, H) + (sp.nt0 > 0 ? kStateTiles * H.v : 0);
-    hipLaunchKernelGGL(prefill_output_kernel, dim3(static_cast<unsigned>(out_grid)), dim3(256), 0,
-                       stream, q, k, chunks, one, out_chunks, H, wsG, ht, vnt, scale, output,
-                       sp, new_state);
-    if ((rc = check_launch("gdn_prefill_fwd(output)"))) return rc;
+    hipLaunchKernelGGL(prefill_output_kernel, dim3(static_cast<unsigned>(P.out_grid)), dim3(256), 0,
+                       stream, q, k, chunks, one, out_chunks, H, wsG, ht, vnt, scale, output, sp,
+                       new_state);
+    if ((rc = check_launch(what))) return rc;
   }
   return GDN_OK;
 }
@@ -2013,7 +1831,8 @@ extern "C" int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_b
                                size_t workspace_bytes, void *stream) {
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
                              num_seqs, total_tokens, scale, output, new_state, workspace,
-                             workspace_bytes, stream, -1, -1, -1, gdn::kHQK, gdn::kHV);
+                             workspace_bytes, stream, -1, -1, -1, gdn::kHQK, gdn::kHV,
+                             "gdn_prefill_fwd");
 }
 
 extern "C" int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
@@ -2025,7 +1844,8 @@ extern "C" int gdn_prefill_fwd_variant(const gdn_bf16 *q, const gdn_bf16 *k, con
                                        size_t workspace_bytes, void *stream, int variant) {
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
                              num_seqs, total_tokens, scale, output, new_state, workspace,
-                             workspace_bytes, stream, variant, -1, -1, gdn::kHQK, gdn::kHV);
+                             workspace_bytes, stream, variant, -1, -1, gdn::kHQK, gdn::kHV,
+                             "gdn_prefill_fwd_variant");
 }
 
 extern "C" int gdn_prefill_fwd_tuned(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
@@ -2039,7 +1859,7 @@ extern "C" int gdn_prefill_fwd_tuned(const gdn_bf16 *q, const gdn_bf16 *k, const
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
                              num_seqs, total_tokens, scale, output, new_state, workspace,
                              workspace_bytes, stream, state_tiling, recurrent_max_len,
-                             recurrent_tiling, gdn::kHQK, gdn::kHV);
+                             recurrent_tiling, gdn::kHQK, gdn::kHV, "gdn_prefill_fwd_tuned");
 }
 
 extern "C" int gdn_prefill_fwd_heads(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
@@ -2054,7 +1874,7 @@ extern "C" int gdn_prefill_fwd_heads(const gdn_bf16 *q, const gdn_bf16 *k, const
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
                              num_seqs, total_tokens, scale, output, new_state, workspace,
                              workspace_bytes, stream, state_tiling, recurrent_max_len,
-                             recurrent_tiling, num_qk_heads, num_v_heads);
+                             recurrent_tiling, num_qk_heads, num_v_heads, "gdn_prefill_fwd_heads");
 }
 
 // ---------------------------------------------------------------------------
@@ -2130,5 +1950,6 @@ extern "C" int gdn_prefill_fwd_noalloc(const gdn_bf16 *q, const gdn_bf16 *k, con
   if (int rc = gdn::device_scratch(stream, &ws)) return rc;
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
                              num_seqs, total_tokens, scale, output, new_state, ws,
-                             GDN_PREFILL_SCRATCH_BYTES, stream, -1, -1, -1, gdn::kHQK, gdn::kHV);
+                             GDN_PREFILL_SCRATCH_BYTES, stream, -1, -1, -1, gdn::kHQK, gdn::kHV,
+                             "gdn_prefill_fwd_noalloc");
 }

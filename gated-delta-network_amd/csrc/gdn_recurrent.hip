@@ -208,6 +208,7 @@ struct RecVariant {
 constexpr RecVariant kRecVariants[] = {
     {1, 1}, {2, 1}, {4, 1}, {1, 2}, {2, 2}, {4, 2}, {1, 4}, {4, 4}, {1, 8}, {1, 16}};
 constexpr int kNumRecVariants = sizeof(kRecVariants) / sizeof(kRecVariants[0]);
+static_assert(kNumRecVariants == kNumRecTilings, "the tiling count is shared with the host code");
 
 template <int W, int P>
 void launch_rec(long long groups, hipStream_t stream, const uint16_t *q, const uint16_t *k,
@@ -284,55 +285,20 @@ static int multi_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
   clear_error();
   Heads H;
   if (int rc = make_heads(hqk, hv, what, H)) return rc;
-  if (batch < 0 || tokens < 1)
-    return fail(GDN_ERR_INVALID, "%s: batch=%d, tokens=%d", what, batch, tokens);
-  if (!q || !k || !v || !A_log || !a || !dt_bias || !b || !output || !new_state)
-    return fail(GDN_ERR_INVALID, "%s: null pointer argument", what);
-  if (!(scale > 0.0f) || scale == __builtin_inff())
-    return fail(GDN_ERR_INVALID, "%s: scale must be finite and > 0", what);
-  if (!aligned(new_state, 16) || (state && !aligned(state, 16)))
-    return fail(GDN_ERR_INVALID, "%s: state/new_state must be 16-byte aligned", what);
-  if (!aligned(q, 8) || !aligned(k, 8))
-    return fail(GDN_ERR_INVALID, "%s: q/k must be 8-byte aligned", what);
-  if (variant < -1 || variant >= recurrent_num_variants())
-    return fail(GDN_ERR_INVALID, "%s: unknown variant %d", what, variant);
-  const long long total = static_cast<long long>(batch) * tokens;
-  if (total > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "%s: batch*tokens too large", what);
+  if (int rc = check_decode_args(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state,
+                                 batch, tokens, H, what))
+    return rc;
+  int kernel;
+  if (int rc = plan_multi(q, k, v, batch, tokens, H, variant, what, &kernel)) return rc;
   if (batch == 0) return GDN_OK;
-  const size_t nb = static_cast<size_t>(batch), nt = static_cast<size_t>(total);
-  const size_t nV = static_cast<size_t>(H.v), nQK = static_cast<size_t>(H.qk);
-  const size_t state_bytes = nb * nV * kDV * kDK * sizeof(float);
-  const size_t out_bytes = nt * nV * kDV * sizeof(uint16_t);
-  if (state != new_state && overlaps(state, state_bytes, new_state, state_bytes))
-    return fail(GDN_ERR_INVALID, "%s: new_state partially overlaps state", what);
-  const void *ins[] = {q, k, v, a, b, A_log, dt_bias, state};
-  const size_t in_bytes[] = {nt * nQK * kDK * 2, nt * nQK * kDK * 2, nt * nV * kDV * 2,
-                             nt * nV * 2,        nt * nV * 2,        nV * 4,
-                             nV * 4,             state ? state_bytes : 0};
-  for (int i = 0; i < 8; ++i) {
-    if (overlaps(output, out_bytes, ins[i], in_bytes[i]))
-      return fail(GDN_ERR_INVALID, "%s: output overlaps an input", what);
-    if (i < 7 && overlaps(new_state, state_bytes, ins[i], in_bytes[i]))
-      return fail(GDN_ERR_INVALID, "%s: new_state overlaps an input", what);
-  }
-  if (overlaps(output, out_bytes, new_state, state_bytes))
-    return fail(GDN_ERR_INVALID, "%s: output overlaps new_state", what);
-  // One token per row is the plain decode step, whose kernel is tuned for it;
-  // more go token by token or in 16-token blocks, whichever the cost models
-  // (gdn_host.h) rate faster (B = 64: 4 tokens 18.8 vs 19.5 us, 8 tokens
-  // 26.3 vs 19.9 us, 16 tokens 41.2 vs 20.6 us).
-  if (tokens == 1 && variant == -1)
+  const long long total = static_cast<long long>(batch) * tokens;
+  // one token per row: the plain decode step, whose kernel is tuned for it
+  if (kernel == kDecodeStep)
     return decode_launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
                          stream, -1, H, what);
-  if (variant == -1) {
-    const float L = static_cast<float>(tokens), fhv = static_cast<float>(H.v);
-    const float g = static_cast<float>(batch) * fhv;
-    if (cost_by_block(L, g) < cost_by_token(L, static_cast<float>(total), fhv, g))
-      variant = recurrent_block_variant();
-  }
   return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, nullptr, 0, batch,
                           static_cast<int>(total), tokens, nullptr, H, scale, output, new_state,
-                          static_cast<hipStream_t>(stream), variant, what);
+                          static_cast<hipStream_t>(stream), kernel, what);
 }
 
 }  // namespace gdn

@@ -59,6 +59,7 @@ SOLUTIONS_DIR = PKG_DIR.parent / "solutions"
 PACKAGE_FILES = (
     "gated-delta-network_amd/gdn_amd/*.py",
     "gated-delta-network_amd/csrc/*.hip",
+    "gated-delta-network_amd/csrc/*.cpp",
     "gated-delta-network_amd/csrc/*.h",
     "gated-delta-network_amd/csrc/Makefile",
     "include/gdn_amd.h",

@@ -47,7 +47,7 @@ def _decode_args(**over):
     return list(args.values())
 
 
-@pytest.mark.parametrize("over, needle", [
+DECODE_BAD = [
     (dict(q=None), "null"),
     (dict(output=None), "null"),
     (dict(batch=-1), "batch"),
@@ -58,7 +58,10 @@ def _decode_args(**over):
     (dict(q=(1 << 20) + 2), "aligned"),
     (dict(output=(3 << 20) + 256), "overlap"),
     (dict(state=(16 << 20) + 1024), "overlap"),
-])
+]
+
+
+@pytest.mark.parametrize("over, needle", DECODE_BAD)
 def test_decode_rejects_bad_arguments(over, needle):
     lib = _lib.load()
     rc = lib.gdn_decode_fwd(*_decode_args(**over))
@@ -108,7 +111,7 @@ def test_prefill_workspace_bytes():
     assert lib.gdn_prefill_workspace_bytes(8192, 4) > lib.gdn_prefill_workspace_bytes(8192, 2)
 
 
-@pytest.mark.parametrize("over, needle, code", [
+PREFILL_BAD = [
     (dict(cu=None), "cu_seqlens", _lib.GDN_ERR_INVALID),
     (dict(q=None), "null", _lib.GDN_ERR_INVALID),
     (dict(N=-1), "num_seqs", _lib.GDN_ERR_INVALID),
@@ -118,7 +121,12 @@ def test_prefill_workspace_bytes():
     (dict(ws=None), "workspace", _lib.GDN_ERR_WORKSPACE),
     (dict(output=(3 << 20) + 64), "overlap", _lib.GDN_ERR_INVALID),
     (dict(ws=(1 << 20)), "overlap", _lib.GDN_ERR_INVALID),
-])
+    (dict(output=(16 << 20) + 2), "aligned", _lib.GDN_ERR_INVALID),
+    (dict(cu=(8 << 20) + 4), "cu_seqlens", _lib.GDN_ERR_INVALID),
+]
+
+
+@pytest.mark.parametrize("over, needle, code", PREFILL_BAD)
 def test_prefill_rejects_bad_arguments(over, needle, code):
     lib = _lib.load()
     rc = lib.gdn_prefill_fwd(*_prefill_args(**over))
@@ -139,7 +147,7 @@ def _multi_args(**over):
     return list(args.values())
 
 
-@pytest.mark.parametrize("over, needle", [
+MULTI_BAD = [
     (dict(tokens=0), "tokens"),
     (dict(batch=-1), "batch"),
     (dict(v=None), "null"),
@@ -150,7 +158,14 @@ def _multi_args(**over):
     # output is [B*T, 8, 128] bf16 = 12 KiB: ending inside v
     (dict(output=(3 << 20) - 4096), "overlap"),
     (dict(state=(16 << 20) + 4096), "overlap"),
-])
+    (dict(v=(3 << 20) + 1), "2-byte"),
+    # the block kernel's 16-byte row loads
+    (dict(q=(1 << 20) + 8, variant=10), "block kernel"),
+    (dict(v=(3 << 20) + 8, variant=10), "block kernel"),
+]
+
+
+@pytest.mark.parametrize("over, needle", MULTI_BAD)
 def test_decode_multi_rejects_bad_arguments(over, needle):
     lib = _lib.load()
     rc = lib.gdn_decode_multi_fwd(*_multi_args(**over))
@@ -163,12 +178,15 @@ def test_decode_multi_zero_batch_is_a_no_op():
     assert lib.gdn_decode_multi_fwd(*_multi_args(batch=0)) == _lib.GDN_OK
 
 
-@pytest.mark.parametrize("tuning, needle", [
+TUNED_BAD = [
     ((-1, -3, -1), "recurrent_max_len"),
     ((-1, -1, 11), "recurrent tiling"),
     ((4, -1, -1), "variant"),
     ((-2, -1, -1), "variant"),
-])
+]
+
+
+@pytest.mark.parametrize("tuning, needle", TUNED_BAD)
 def test_prefill_tuned_rejects_bad_tuning(tuning, needle):
     lib = _lib.load()
     rc = lib.gdn_prefill_fwd_tuned(*_prefill_args(), *tuning)
