@@ -10,9 +10,13 @@ twice the 256 MB Infinity Cache) so no step reads a state that is still cached.
 Reported beside it: decode kernel time and achieved HBM bandwidth (the
 roofline of the dominant kernel, from HIP events around each launch on the
 launch stream), the decode batch sweep of configs[1], the prefill at 1x8192
-(ms and tokens/s) and at configs[2..4], and the CPU baseline (the reference's
-loop nest restated in numpy, oracle/gdn_oracle.py:decode_loop, single thread,
-on a bounded sample).
+(ms and tokens/s) and at configs[2..4] -- replaying one input set, and
+cache-honestly over rotating input/output/workspace sets larger than three
+Infinity Caches -- the reference's other published points (prefill of one
+sequence of 64..4096 tokens, decode at B = 128 and 512) beside its B200
+figures, and the CPU baseline (the reference's loops restated: in C with
+OpenMP on every usable host core and on one thread, and the decode loop nest
+in numpy on one thread; bounded samples).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep]
 """
@@ -35,6 +39,15 @@ HBM_PEAK_GBPS = 8000.0
 # Published B200 decode latency at B=64 (reference README.md:49): 0.023 ms/step.
 B200_DECODE_MS_B64 = 0.023
 ROTATE = 8
+# The reference's other published points on B200 (/root/reference paths):
+# prefill of one sequence, tensors reused (README.md:86-87 for 1x128,
+# README.md:102-107 otherwise) and in FlashInfer-Bench clone mode
+# (README.md:115-120); decode device time in µs (OPTIMIZATION_LOG.md:51-57).
+B200_PREFILL_REUSE_MS = {64: 0.191, 128: 0.268, 256: 0.192, 512: 0.190, 1024: 0.185,
+                         2048: 0.229, 4096: 0.420}
+B200_PREFILL_CLONE_MS = {64: 0.492, 256: 0.507, 512: 0.525, 1024: 0.546, 2048: 0.639,
+                         4096: 0.805}
+B200_DECODE_DEVICE_US = {1: 7.76, 8: 9.22, 32: 13.16, 128: 27.90, 512: 86.79}
 
 
 def log(msg):
@@ -177,6 +190,65 @@ def bench_prefill(lens, steps, warmup, dev, variant=-1, slow_decay_heads=None):
     return ms_eager, ms_graph
 
 
+def bench_prefill_rotated(lens, dev, min_bytes=768 << 20, steps=None):
+    """Cache-honest prefill time: `steps` calls captured in one HIP graph that
+    cycle over S distinct sets of inputs, outputs and workspace, S chosen so
+    that the sets together exceed `min_bytes` (three times the 256 MB Infinity
+    Cache), so no call finds its operands left in the MALL by the previous
+    call on the same set.  Returns (ms per call, S, bytes per set)."""
+    import torch
+    from gdn_amd import prefill
+    from oracle import gdn_oracle as O  # input recipe only
+
+    inp = O.make_prefill_inputs(lens, seed=2, with_state=len(lens) > 1)
+    base = _dev_inputs(inp, dev)
+    base["cu_seqlens"] = torch.from_numpy(inp["cu_seqlens"]).to(dev)
+    T, N = sum(lens), len(lens)
+    per_set = (sum(t.numel() * t.element_size() for t in base.values() if t is not None)
+               + T * 8 * 128 * 2 + N * 8 * 128 * 128 * 4 + prefill.workspace_bytes(T, N))
+    S = max(3, -(-min_bytes // per_set))
+    steps = steps or max(2 * S, 20)
+    sets = []
+    for _ in range(S):
+        c = {n: (None if t is None else t.clone()) for n, t in base.items()}
+        c["out"] = torch.empty((T, 8, 128), dtype=torch.bfloat16, device=dev)
+        c["ns"] = torch.empty((N, 8, 128, 128), dtype=torch.float32, device=dev)
+        c["ws"] = prefill.alloc_workspace(T, N, dev)
+        sets.append(c)
+
+    def step(i):
+        c = sets[i % S]
+        prefill.kernel(c["q"], c["k"], c["v"], c["state"], c["A_log"], c["a"], c["dt_bias"],
+                       c["b"], c["cu_seqlens"], inp["scale"], c["out"], c["ns"], workspace=c["ws"])
+
+    for i in range(S):
+        step(i)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        step(0)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            step(i)
+    graph.replay()
+    best = None
+    for _ in range(3):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record()
+        graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        best = ms if best is None else min(best, ms)
+    del graph, sets
+    torch.cuda.empty_cache()
+    return best, S, per_set
+
+
 def bench_prefill_clone(lens, reps, dev):
     """FlashInfer-Bench's clone mode (OPTIMIZATION_LOG.md:263-300): before each
     timed call every argument is cloned into fresh memory and the device is
@@ -266,37 +338,71 @@ def measured_traffic(path=os.path.join(ROOT, "profiles", "decode_b64_hbm_traffic
     return None
 
 
-def cpu_baseline_decode(B, seconds):
-    """The reference's decode loop nest restated in numpy (oracle decode_loop),
-    one thread, repeated until `seconds` of CPU time have passed."""
+def host_cores():
+    """The host CPUs this process may use: os.cpu_count(), the affinity mask,
+    and the OpenMP share the box grants (OMP_NUM_THREADS, when set)."""
+    aff = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    usable = min(aff, int(omp)) if omp.isdigit() and int(omp) > 0 else aff
+    return {"cpu_count": os.cpu_count(), "affinity": aff,
+            "omp_num_threads": int(omp) if omp.isdigit() else None, "used": usable}
+
+
+def _repeat(fn, seconds):
+    reps = 0
+    t = time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t
+        if el >= seconds:
+            return el / reps, reps
+
+
+def cpu_baseline_decode_loop(B, seconds):
+    """The reference's decode loop nest (gdn_decode_ref.py:63-80) restated in
+    numpy (oracle decode_loop), one thread, repeated for `seconds`; returns
+    (seconds per step, steps)."""
     from threadpoolctl import threadpool_limits
     from oracle import gdn_oracle as O
 
     inp = O.make_decode_inputs(B, seed=1)
-    reps = 0
     with threadpool_limits(limits=1):
-        t = time.perf_counter()
-        while True:
-            O.decode_loop(**inp)
-            reps += 1
-            el = time.perf_counter() - t
-            if el >= seconds:
-                break
-    return el / reps, reps
+        return _repeat(lambda: O.decode_loop(**inp), seconds)
 
 
-def cpu_baseline_prefill(lens):
-    """One prefill of `lens` through the sequential recurrence restated in C
-    (oracle/gdn_seq.c: the reference's per-token loop, f32, one OpenMP thread
-    per (sequence, v-head) pair); returns (seconds, threads used)."""
+def cpu_baseline_decode_c(B, threads, seconds):
+    """One decode step at batch B as B one-token sequences through the C
+    recurrence (oracle/gdn_seq.c, the reference's per-token loop in f32),
+    OpenMP over the B x 8 (row, v-head) pairs on `threads` threads, repeated
+    for `seconds`; returns (seconds per step, steps)."""
+    import numpy as np
+    from oracle import gdn_oracle as O
+
+    inp = O.make_decode_inputs(B, seed=1)
+    pre = dict(q=inp["q"][:, 0], k=inp["k"][:, 0], v=inp["v"][:, 0], state=inp["state"],
+               A_log=inp["A_log"], a=inp["a"][:, 0], dt_bias=inp["dt_bias"], b=inp["b"][:, 0],
+               cu_seqlens=np.arange(B + 1, dtype=np.int64), scale=inp["scale"])
+    O.set_c_threads(threads)
+    try:
+        return _repeat(lambda: O.prefill_seq_c(**pre), seconds)
+    finally:
+        O.set_c_threads(0)
+
+
+def cpu_baseline_prefill(lens, threads, seconds=0.0):
+    """Prefill of `lens` through the C recurrence (the reference's per-token
+    loop, f32), OpenMP over the (sequence, v-head) pairs on `threads` threads;
+    at least one call, repeated for `seconds`; returns (seconds per call,
+    calls)."""
     from oracle import gdn_oracle as O
 
     inp = O.make_prefill_inputs(lens, seed=2, with_state=len(lens) > 1)
-    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "64")),
-                  len(lens) * 8)
-    t = time.perf_counter()
-    O.prefill_seq_c(**inp)
-    return time.perf_counter() - t, threads
+    O.set_c_threads(threads)
+    try:
+        return _repeat(lambda: O.prefill_seq_c(**inp), seconds)
+    finally:
+        O.set_c_threads(0)
 
 
 def cpu_model():
@@ -400,6 +506,30 @@ def main():
     pre1k_clone = bench_prefill_clone([1024], 20, dev)
     log(f"prefill clone mode: 1x8192 {pre_clone:.3f} ms, 1x1024 {pre1k_clone:.3f} ms; "
         f"1x1024 graph {pre1k_ms:.3f} ms, eager {pre1k_eager:.3f} ms")
+    rotated = {}
+    for name, lens in (("1x8192", pre_lens), ("1x1024", [1024])):
+        ms, sets, per_set = bench_prefill_rotated(lens, dev)
+        rotated[name] = {"ms": round(ms, 4), "sets": sets, "bytes_per_set": per_set}
+    log(f"prefill over rotating input/output/workspace sets (> 768 MiB in all): {rotated}")
+
+    # The reference's other published points: prefill of one sequence of
+    # 64..4096 tokens (graph replay, eager calls with tensors reused, clone
+    # mode) and decode at B = 128 and 512 (graph replay, 8 rotating states).
+    ref_points = {"prefill": {}, "decode": {}}
+    for L in (64, 128, 256, 512, 1024, 2048, 4096):
+        pe, pg = bench_prefill([L], 20, 3, dev)
+        pc = bench_prefill_clone([L], 10, dev)
+        ref_points["prefill"][f"1x{L}"] = {
+            "graph_ms": round(pg, 4), "eager_ms": round(pe, 4), "clone_ms": round(pc, 4),
+            "b200_reuse_ms": B200_PREFILL_REUSE_MS.get(L),
+            "b200_clone_ms": B200_PREFILL_CLONE_MS.get(L)}
+    for b in (128, 512):
+        me, mg = bench_decode(b, 50, 5, dev)
+        ref_points["decode"][f"B{b}"] = {
+            "us": round(mg * 1e3, 3), "us_eager": round(me * 1e3, 3),
+            "GBps": round(O.decode_bytes(b) / (mg * 1e-3) / 1e9, 1),
+            "b200_device_us": B200_DECODE_DEVICE_US[b]}
+    log(f"reference points: {ref_points}")
 
     mtp = {}
     for T in (2, 4, 8, 16):
@@ -443,11 +573,21 @@ def main():
     cfg_detail["north_star_1x8192"] = detail(pre_lens, pre_ms)
     log(f"prefill configs (graph ms per call): {cfg_ms}")
 
-    cpu_s, reps = cpu_baseline_decode(B, args.cpu_seconds)
-    cpu_gbs = nbytes / cpu_s / 1e9
-    log(f"cpu baseline decode B={B}: {cpu_s * 1e3:.1f} ms/step over {reps} steps")
-    cpu_pre_s, cpu_pre_threads = cpu_baseline_prefill(pre_lens)
-    log(f"cpu baseline prefill 1x8192: {cpu_pre_s:.2f} s ({cpu_pre_threads} threads)")
+    # CPU baseline (the reference's loops restated; a reported baseline, not a
+    # target): about --cpu-seconds of CPU work in all.
+    hc = host_cores()
+    slice_s = args.cpu_seconds / 4
+    cpu_all_s, reps_all = cpu_baseline_decode_c(B, hc["used"], slice_s)
+    cpu_one_s, reps_one = cpu_baseline_decode_c(B, 1, slice_s)
+    cpu_loop_s, reps_loop = cpu_baseline_decode_loop(B, slice_s)
+    log(f"cpu baseline decode B={B}: C recurrence {cpu_all_s * 1e3:.1f} ms/step on "
+        f"{hc['used']} threads, {cpu_one_s * 1e3:.1f} ms/step on 1; numpy loop nest "
+        f"{cpu_loop_s * 1e3:.1f} ms/step ({hc})")
+    cpu_pre_all, _ = cpu_baseline_prefill(pre_lens, hc["used"], slice_s / 2)
+    cpu_pre_one, _ = cpu_baseline_prefill(pre_lens, 1)
+    cpu_pre4_all, _ = cpu_baseline_prefill([8192] * 4, hc["used"])
+    log(f"cpu baseline prefill 1x8192: {cpu_pre_all:.3f} s on {min(hc['used'], 8)} threads, "
+        f"{cpu_pre_one:.3f} s on 1; 4x8192 {cpu_pre4_all:.3f} s on {min(hc['used'], 32)}")
 
     b200_gbs = O.decode_bytes(64) / (B200_DECODE_MS_B64 * 1e-3) / 1e9
     line = {
@@ -476,6 +616,10 @@ def main():
         "prefill_ms_1x8192_clone": round(pre_clone, 4),
         "prefill_ms_1x1024": round(pre1k_ms, 4),
         "prefill_ms_1x1024_clone": round(pre1k_clone, 4),
+        "prefill_ms_1x8192_rotated": rotated["1x8192"]["ms"],
+        "prefill_ms_1x1024_rotated": rotated["1x1024"]["ms"],
+        "prefill_rotated_sets": rotated,
+        "reference_points": ref_points,
         "decode_sweep": sweep,
         "prefill_ms_configs": cfg_ms,
         "prefill_configs": cfg_detail,
@@ -491,15 +635,31 @@ def main():
                      "traffic": measured_traffic() if (B == 64 and args.variant == -1) else None,
                      "kernel": "gdn::decode_kernel",
                      "bytes_per_launch": nbytes},
-        "cpu_baseline": {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-                         "sample": f"{reps} decode steps at B={B} "
-                                   f"({cpu_s * 1e3:.1f} ms/step), oracle decode_loop (numpy), "
-                                   f"1 thread of {cpu_model()}"},
-        "cpu_baseline_prefill": {"value": round(T8 / cpu_pre_s, 1), "unit": "tokens/s",
-                                 "cores": cpu_pre_threads, "kind": "port",
-                                 "sample": f"one 1x8192 prefill in {cpu_pre_s:.2f} s, oracle "
-                                           f"gdn_seq.c (per-token loop, f32), OpenMP over the "
-                                           f"8 v-heads, {cpu_model()}"},
+        "cpu_baseline": {
+            "value": round(nbytes / cpu_all_s / 1e9, 4), "unit": "GB/s", "cores": hc["used"],
+            "kind": "port",
+            "sample": f"{reps_all} decode steps at B={B} ({cpu_all_s * 1e3:.2f} ms/step): the "
+                      f"reference's per-token loop in C (oracle/gdn_seq.c, f32), OpenMP over "
+                      f"the {B * 8} (row, v-head) pairs on {hc['used']} threads of {cpu_model()}",
+            "one_thread": {"value": round(nbytes / cpu_one_s / 1e9, 4), "unit": "GB/s",
+                           "ms_per_step": round(cpu_one_s * 1e3, 3), "steps": reps_one},
+            "numpy_loop_one_thread": {
+                "value": round(nbytes / cpu_loop_s / 1e9, 4), "unit": "GB/s",
+                "ms_per_step": round(cpu_loop_s * 1e3, 3), "steps": reps_loop,
+                "what": "oracle decode_loop: gdn_decode_ref.py:63-80's loop nest in numpy"},
+            "host_cores": hc, "cpu_model": cpu_model()},
+        "cpu_baseline_prefill": {
+            "value": round(T8 / cpu_pre_all, 1), "unit": "tokens/s", "cores": min(hc["used"], 8),
+            "kind": "port",
+            "sample": f"1x8192 prefill in {cpu_pre_all:.3f} s: the reference's per-token loop "
+                      f"in C (oracle/gdn_seq.c, f32), OpenMP over the 8 v-heads (the "
+                      f"parallelism one sequence has) of {cpu_model()}",
+            "one_thread": {"value": round(T8 / cpu_pre_one, 1), "unit": "tokens/s",
+                           "seconds": round(cpu_pre_one, 3)},
+            "configs4_4x8192_all_cores": {"value": round(4 * 8192 / cpu_pre4_all, 1),
+                                          "unit": "tokens/s", "cores": min(hc["used"], 32),
+                                          "seconds": round(cpu_pre4_all, 3)},
+            "host_cores": hc, "cpu_model": cpu_model()},
     }
     print(json.dumps(line), flush=True)
 

@@ -504,8 +504,16 @@ def _clib():
                                                ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                                P, P, ctypes.c_int]
         lib.gdn_oracle_prefill_seq.restype = ctypes.c_int
+        lib.gdn_oracle_set_threads.argtypes = [ctypes.c_int]
+        lib.gdn_oracle_set_threads.restype = ctypes.c_int
         _CLIB = lib
     return _CLIB
+
+
+def set_c_threads(n: int) -> int:
+    """OpenMP threads of prefill_seq_c's (sequence, v-head) loop for later
+    calls from this thread (n <= 0: every processor); returns the count."""
+    return int(_clib().gdn_oracle_set_threads(int(n)))
 
 
 def prefill_seq_c(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale,

@@ -22,6 +22,7 @@
  *             reference/gdn_prefill_ref.py:61-62)
  * use_f64 != 0 evaluates the recurrence in double precision instead.
  */
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -92,6 +93,13 @@ static void run_head_f64(const float *q, const float *k, const float *v, const f
   for (int vv = 0; vv < DV; ++vv)
     for (int kk = 0; kk < DK; ++kk) s_out[vv * DK + kk] = (float)S[kk * DV + vv];
   free(S);
+}
+
+/* Threads of the (sequence, v-head) loop below for later calls from this
+ * thread; n <= 0 restores every processor.  Returns the count in effect. */
+int gdn_oracle_set_threads(int n) {
+  omp_set_num_threads(n > 0 ? n : omp_get_num_procs());
+  return omp_get_max_threads();
 }
 
 int gdn_oracle_prefill_seq(const float *q, const float *k, const float *v, const float *g,
