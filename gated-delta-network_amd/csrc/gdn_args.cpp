@@ -240,6 +240,7 @@ int plan_prefill(int T, int N, const Heads &H, const PrefillLayout &L, int varia
   const long long grid = chunk_head_grid(L.nt_max, H);
   if (grid > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "%s: too many tokens", what);
   P.intra_grid = L.nt_max > 0 ? grid : 0;
+  P.intra_split = P.form != 1 && 2 * P.intra_grid <= static_cast<long long>(kNumCus) * kIntraSplitPerCu;
   if (P.single && P.form == 0 && variant != 2 && L.nt_max >= 2 && 24 * H.v <= 256 &&
       (variant == 3 || L.nt_max >= kSplitMinChunks))
     P.split_nt0 = split_first(L.nt_max);

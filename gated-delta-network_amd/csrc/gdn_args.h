@@ -110,6 +110,13 @@ constexpr int kRecurrentMaxLen = 96;
 // never (one chain), 3 always (one sequence of at least two chunks).
 constexpr int kSplitMinChunks = 32;
 
+// Compute units of the target (MI355X: 256).  The WY intra kernel runs each
+// (chunk, v-head) as two workgroups (its w and u halves) while that leaves
+// at most kIntraSplitPerCu workgroups per CU: a batch too small to fill the
+// CUs then halves its per-chunk latency instead of idling CUs.
+constexpr int kNumCus = 256;
+constexpr int kIntraSplitPerCu = 2;
+
 // What a prefill call launches, decided from (T, N), the head layout and the
 // tuning arguments alone (cu_seqlens is never read on the host).
 struct PrefillPlan {
@@ -120,6 +127,7 @@ struct PrefillPlan {
   bool single;      // one sequence without a chunk table (bounds read on the device)
   int form;         // per-chunk operands: 0 WY, 1 T, -1 the index kernel's rule
   int split_nt0;    // two-segment scan: first chunk of the second segment; 0 none
+  bool intra_split; // WY intra kernel as two workgroups per (chunk, v-head)
   // launch grids (workgroups); 0 = not launched
   long long intra_grid, state_grid, split_grid, out_grid;
 };

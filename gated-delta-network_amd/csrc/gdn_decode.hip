@@ -168,14 +168,18 @@ constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 constexpr int kNontemporalFlag = 16;
 
 // Built-in tiling per batch size, from the MI355X sweep of every tiling at
-// B = 1..64 (HIP-graph replay timing): small batches want many small
-// workgroups, large ones one wave streaming 64 rows (32 KiB in flight per
-// wave); non-temporal state accesses win at every size.
+// B = 1..512 (HIP-graph replay timing, 8 rotating states): small batches want
+// many small workgroups, B = 33..128 one wave streaming 64 rows (32 KiB in
+// flight per wave), and beyond that -- many waves resident per CU for the
+// whole launch -- one wave of 8 rows (B = 512: 87.3 us against 93.1 us with
+// 64 rows and 90.4 us for a plain copy of the same bytes); non-temporal
+// state accesses win at every size.
 int default_variant(int batch) {
-  if (batch <= 4) return 3 + kNontemporalFlag;   // 16 rows, 256 threads
-  if (batch <= 8) return 2 + kNontemporalFlag;   // 32 rows, 256 threads
-  if (batch <= 32) return 5 + kNontemporalFlag;  // 32 rows,  64 threads
-  return 9 + kNontemporalFlag;                   // 64 rows,  64 threads
+  if (batch <= 4) return 3 + kNontemporalFlag;    // 16 rows, 256 threads
+  if (batch <= 8) return 2 + kNontemporalFlag;    // 32 rows, 256 threads
+  if (batch <= 32) return 5 + kNontemporalFlag;   // 32 rows,  64 threads
+  if (batch <= 128) return 9 + kNontemporalFlag;  // 64 rows,  64 threads
+  return 7 + kNontemporalFlag;                    //  8 rows,  64 threads
 }
 
 }  // namespace

@@ -85,11 +85,19 @@ __device__ __forceinline__ int load_cu(const void *cu, int is64, int i, int T) {
 // its share with 16-byte stores (out is 16-byte aligned; a token row is
 // hv * 256 bytes).  A batch spanning [0, T), the usual case, costs two uniform
 // loads and a compare.
-__device__ __forceinline__ void zero_uncovered_rows(uint16_t *out, const void *cu, int cu64, int N,
-                                                    int T, int hv, unsigned wg, unsigned nwg) {
+// (covered_rows loads the bounds, zero_rows_outside fills: a kernel that
+// must not wait for the loads at its end issues them at its start.)
+struct CoveredRows {
+  int lo, hi;
+};
+__device__ __forceinline__ CoveredRows covered_rows(const void *cu, int cu64, int N, int T) {
   const int lo = load_cu(cu, cu64, 0, T);
-  int hi = load_cu(cu, cu64, N, T);
-  hi = hi < lo ? lo : hi;
+  const int hi = load_cu(cu, cu64, N, T);
+  return CoveredRows{lo, hi < lo ? lo : hi};
+}
+__device__ __forceinline__ void zero_rows_outside(uint16_t *out, CoveredRows r, int T, int hv,
+                                                  unsigned wg, unsigned nwg) {
+  const int lo = r.lo, hi = r.hi;
   if (lo == 0 && hi == T) return;
   const size_t per_row = static_cast<size_t>(hv) * (kDV / 8);  // 16-byte units per token row
   const size_t head = static_cast<size_t>(lo) * per_row;
@@ -99,6 +107,10 @@ __device__ __forceinline__ void zero_uncovered_rows(uint16_t *out, const void *c
     const size_t u = i < head ? i : i - head + static_cast<size_t>(hi) * per_row;
     *reinterpret_cast<uint4 *>(out + u * 8) = make_uint4(0u, 0u, 0u, 0u);
   }
+}
+__device__ __forceinline__ void zero_uncovered_rows(uint16_t *out, const void *cu, int cu64, int N,
+                                                    int T, int hv, unsigned wg, unsigned nwg) {
+  zero_rows_outside(out, covered_rows(cu, cu64, N, T), T, hv, wg, nwg);
 }
 
 // A batch of one sequence runs without a chunk table: its tokens are

@@ -227,57 +227,102 @@ __device__ __forceinline__ bool chunk_head_of(int id, int nt, const Heads &H, in
   return true;
 }
 
-// Transposed [*][64] bf16 tiles in LDS (rows of 128 bytes, no padding) store
-// each row's eight 8-token blocks in XOR-swizzled order (block b of row n at
-// slot b ^ ((n >> 3) & 7)), so the 16-byte transposed writes of eight
-// consecutive rows hit different banks.
-constexpr int kStrideTT = 64;
-__device__ __forceinline__ int tsw(int row, int token) {
-  return row * kStrideTT + ((((token >> 3) ^ (row >> 3)) & 7) << 3) + (token & 7);
-}
-
-// WY form of the intra kernel (per chunk c, v-head h; LDS from smem, 52 KB):
+// WY form of the intra kernel, per chunk c and v-head h (30 KB of LDS):
 //   * wave 0: gating, chunk-local cumsum G, decay factors.
-//   * every thread: one 8x8 block of K or V -> row-major K and transposed
-//     K^T / V^T in LDS (8x8 transposes in registers, 16-byte LDS writes).
-//   * A = strictly-lower(beta_i exp(G_i - G_j) K K^T) on MFMA.
-//   * the four 16x16 diagonal blocks of (I + A) inverted by forward
-//     substitution (wave w, block w).
-//   * u = (I + A)^-1 (beta V) and w = (I + A)^-1 (beta exp(G) K) by blocked
-//     forward substitution: wave w owns 64 right-hand-side columns (waves 0-1
-//     u, 2-3 w) and walks the four 16-row block rows,
+//   * K rows -> LDS row-major (V rows wait in registers).
+//   * A = strictly-lower(beta_i exp(G_i - G_j) K K^T) on MFMA, stored as its
+//     ten lower 16x16 blocks; K^T fragments for the state kernel.
+//   * the four diagonal blocks of (I + A) inverted by forward substitution
+//     (wave w, block w), in place of the diagonal blocks of A.
+//   * w = (I + A)^-1 (beta exp(G) K) and then u = (I + A)^-1 (beta V) by
+//     blocked forward substitution: wave w owns 32 right-hand-side columns
+//     and walks the four 16-row block rows,
 //       Y_i = D_i (X_i - sum_{j<i} A_ij Y_j),
-//     on split-bf16 MFMAs with every Y_j kept in registers.
+//     on split-bf16 MFMAs with every Y_j kept in registers; the X_i operands
+//     (4 consecutive tokens of one feature) come straight from the row-major
+//     tile through gfx950's transposing LDS read, so no transposed copy of K
+//     or V is kept.  w is turned into A-operand fragments through the K
+//     tile's space once the w-solve is done; V then takes that space.
+// PART: 0 = w then u in one workgroup; 1 = w only; 2 = u only (a chunk's two
+// halves in two workgroups, for batches too small to fill the CUs).
 // Outputs go to the workspace in the exact fragment order the state kernel
 // reads: u as MFMA result tiles, w as hi/lo A-operand fragments, K^T as
 // A-operand fragments.
-constexpr int kIntraWyLds = kChunk * kStrideK * 2 + kDK * kStrideTT * 2 + kChunk * 68 * 4 + 3 * kChunk * 4;
+constexpr int kABlk = 16 * 20;  // one 16x16 f32 block of A, rows padded to 20
+constexpr int kIntraWyLds = kChunk * kStrideK * 2 + 10 * kABlk * 4 + 3 * kChunk * 4;
+// Block (ib, jb), jb <= ib, of the compact lower-triangular A.
+__device__ __forceinline__ int ablk(int ib, int jb) { return (ib * (ib + 1) / 2 + jb) * kABlk; }
+
+// The B operand of a 16x16x16 product contracting over tokens: rows
+// r0..r0+3 (tokens) of column c0 + (lane & 15) of a row-major bf16 tile,
+// gathered by one transposing read (16-lane group g passes its own r0, c0).
+__device__ __forceinline__ u32x2 tile_col4(const uint16_t *tile, int r0, int c0, int r16) {
+  return ds_read_tr16(&tile[(r0 + (r16 >> 2)) * kStrideK + c0 + 4 * (r16 & 3)]);
+}
+
+// Blocked forward substitution (I + A) Y = diag(scl) X for the 32 columns
+// col0.. of this wave; X row-major in sX ([64][kStrideK] bf16).
+__device__ __forceinline__ void wy_solve(const uint16_t *sX, const float *scl, const float *sA,
+                                         int col0, int g, int r16, f32x4 (&Y)[4][2]) {
+  u32x2 Yh[4][2], Yl[4][2];  // hi/lo splits of Y (B operands)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // Z = X_i - sum_{j<i} A_ij Y_j
+    const f32x4 s4 = *reinterpret_cast<const f32x4 *>(&scl[16 * i + 4 * g]);
+    f32x4 Z[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const u32x2 x2 = tile_col4(sX, 16 * i + 4 * g, col0 + 16 * nt, r16);
+      Z[nt] = f32x4{s4[0] * __uint_as_float(x2[0] << 16),
+                    s4[1] * __uint_as_float(x2[0] & 0xffff0000u),
+                    s4[2] * __uint_as_float(x2[1] << 16),
+                    s4[3] * __uint_as_float(x2[1] & 0xffff0000u)};
+    }
+#pragma unroll
+    for (int j = 0; j < i; ++j) {
+      const f32x4 la = *reinterpret_cast<const f32x4 *>(&sA[ablk(i, j) + r16 * 20 + 4 * g]);
+      u32x2 lh, ll;
+      split4(-la, lh, ll);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) Z[nt] = mfma16_x3(lh, ll, Yh[j][nt], Yl[j][nt], Z[nt]);
+    }
+    // Y_i = D_i Z
+    const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&sA[ablk(i, i) + r16 * 20 + 4 * g]);
+    u32x2 dh, dl;
+    split4(d4, dh, dl);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      u32x2 zh, zl;
+      split4(Z[nt], zh, zl);
+      Y[i][nt] = mfma16_x3(dh, dl, zh, zl, f32x4{0.f, 0.f, 0.f, 0.f});
+      split4(Y[i][nt], Yh[i][nt], Yl[i][nt]);
+    }
+  }
+}
+
+template <int PART>
 __device__ __forceinline__ void wy_intra(
     char *smem, int c, int h, int start, int len, const uint16_t *__restrict__ k,
     const uint16_t *__restrict__ v, const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b, const Heads &H,
     float *__restrict__ ws_G, float *__restrict__ ws_dcy, float *__restrict__ ws_eg,
     uint16_t *__restrict__ ws_w, float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr bool kW = PART != 2, kU = PART != 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4, kg = g * 8;
   const int hq = h / H.ratio;
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
 
-  constexpr int kStrideA4 = 68;  // f32 stride of the 64x64 A tile (16-byte rows)
-  // 52 KB of LDS, so three workgroups share a CU:
-  //   sKV: K row-major until A is built, then V^T, then (wave 2) w scratch;
-  //   sA:  strictly lower blocks of A; the unused upper blocks hold the four
-  //        16x16 diagonal inverses (D_w at block kDiagBlock[w]); at the end
-  //        (wave 3) w scratch.
-  uint16_t *const sKV = reinterpret_cast<uint16_t *>(smem);                  // [64][136]
-  uint16_t *const sKt = sKV + kChunk * kStrideK;                              // [128][64]
-  float *const sA = reinterpret_cast<float *>(sKt + kDK * kStrideTT);         // [64][68]
-  float *const sBeta = sA + kChunk * kStrideA4, *const sBG = sBeta + kChunk, *const sG = sBG + kChunk;
-  uint16_t *const sK = sKV, *const sVt = sKV;
-  static_assert(kDV * kStrideTT <= kChunk * kStrideK, "V^T must fit in the K tile");
-  // D_w lives at row block w, column block dcol(w): (0,1), (1,2), (2,3), (0,2).
-  auto dcol = [](int w) { return w == 3 ? 2 : w + 1; };
-  auto drow = [](int w) { return w == 3 ? 0 : w; };
+  //   sX:  K row-major; after the w-solve f32 scratch for w's fragments; then
+  //        V row-major for the u-solve.
+  //   sA:  the ten lower 16x16 blocks of A; the diagonal ones become D_w.
+  uint16_t *const sX = reinterpret_cast<uint16_t *>(smem);                   // [64][136]
+  float *const sA = reinterpret_cast<float *>(sX + kChunk * kStrideK);        // 10 blocks
+  float *const sBeta = sA + 10 * kABlk, *const sBG = sBeta + kChunk, *const sG = sBG + kChunk;
+  float *const scr = reinterpret_cast<float *>(sX);                           // [64][68]
+  constexpr int kStrideS = 68;
+  static_assert(kChunk * kStrideS * 4 <= kChunk * kStrideK * 2, "w scratch must fit the tile");
 
   // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding tokens
   // get g = 0 and beta = 0, so G stays at G_last past the end of the chunk.
@@ -293,91 +338,102 @@ __device__ __forceinline__ void wy_intra(
     sG[lane] = G;
     sBeta[lane] = be;
     sBG[lane] = be * expf(G);
-    const float G_last = __shfl(G, 63);
-    ws_G[ch_head * kChunk + lane] = G;
-    ws_dcy[ch_head * kChunk + lane] = expf(G_last - G);
-    if (lane == 0) ws_eg[ch_head] = expf(G_last);
+    if (kW) {  // (the u-only half leaves these to the w half)
+      const float G_last = __shfl(G, 63);
+      ws_G[ch_head * kChunk + lane] = G;
+      ws_dcy[ch_head * kChunk + lane] = expf(G_last - G);
+      if (lane == 0) ws_eg[ch_head] = expf(G_last);
+    }
   }
 
-  // One 8x8 block of K (threads 0..127) or V (128..255) per thread, loaded
-  // now; K goes to LDS (row-major and transposed) at once, V's transpose waits
-  // in registers until A is built (it reuses the K tile's space).
-  const bool isK = __builtin_amdgcn_readfirstlane(wave) < 2;  // wave-uniform (SGPR)
-  const int blk = tid & 127, rb = blk >> 4, cb = blk & 15;
-  // (rows past the chunk read zero through the descriptor's range)
-  u32x4 rows[8];
+  // K rows -> LDS; V rows into registers (rows past the chunk read zero
+  // through the descriptors' range).  Thread t moves 16 bytes of rows
+  // (t + 256 i) / 16.
+  u32x4 vrows[4];
   {
-    const int nh = isK ? H.qk : H.v;
-    const uint16_t *src = isK ? k + (static_cast<size_t>(start) * H.qk + hq) * kDK
-                              : v + (static_cast<size_t>(start) * H.v + h) * kDV;
-    const uint32_t rstride = static_cast<uint32_t>(nh) * (kDK * 2);
-    const auto rs = buf_rsrc(src, static_cast<uint32_t>(len) * rstride);
+    const uint32_t kstride = static_cast<uint32_t>(H.qk) * (kDK * 2);
+    const auto rk = buf_rsrc(k + (static_cast<size_t>(start) * H.qk + hq) * kDK,
+                             static_cast<uint32_t>(len) * kstride);
+    u32x4 krows[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      rows[i] = buf_load16(rs, static_cast<uint32_t>(rb * 8 + i) * rstride + cb * 16);
-  }
-  // Column j of the block = 8 tokens of feature cb*8 + j, into transposed LDS.
-  auto transpose_into = [&](uint16_t *dstT, bool kt_frags) {
-    uint16_t *ktf = ws_kt + (static_cast<size_t>(c) * H.qk + hq) * (kDK * kChunk);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      u32x4 col;
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const uint32_t x0 = rows[2 * p][j >> 1], x1 = rows[2 * p + 1][j >> 1];
-        col[p] = (j & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
-      }
-      const int n = cb * 8 + j;
-      *reinterpret_cast<u32x4 *>(&dstT[tsw(n, rb * 8)]) = col;
-      // K^T as A-operand fragments of the state kernel: (mt, kk, lane) =
-      // (n / 16, rb / 4, (rb % 4) * 16 + n % 16), 8 tokens each.
-      if (kt_frags)
-        *reinterpret_cast<u32x4 *>(
-            ktf + ((((n >> 4) * 2 + (rb >> 2)) * 64) + (rb & 3) * 16 + (n & 15)) * 8) = col;
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      krows[i] = buf_load16(rk, static_cast<uint32_t>(idx >> 4) * kstride + (idx & 15) * 16);
     }
-  };
-  if (isK) {
+    if (kU) {
+      const uint32_t vstride = static_cast<uint32_t>(H.v) * (kDV * 2);
+      const auto rv = buf_rsrc(v + (static_cast<size_t>(start) * H.v + h) * kDV,
+                               static_cast<uint32_t>(len) * vstride);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<u32x4 *>(&sK[(rb * 8 + i) * kStrideK + cb * 8]) = rows[i];
-    transpose_into(sKt, h % H.ratio == 0);  // one v-head per q/k head writes K^T
+      for (int i = 0; i < 4; ++i) {
+        const int idx = tid + 256 * i;
+        vrows[i] = buf_load16(rv, static_cast<uint32_t>(idx >> 4) * vstride + (idx & 15) * 16);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      *reinterpret_cast<u32x4 *>(&sX[(idx >> 4) * kStrideK + (idx & 15) * 8]) = krows[i];
+    }
   }
   __syncthreads();
 
   // A = strictly-lower(beta_i exp(G_i - G_j) K K^T): its ten lower 16x16
   // tiles dealt three, three, two and two to the waves.  G_i - G_j <= 0 for
   // every kept entry (g <= 0); the clamp keeps the others finite.
-  {
-    const int wv = __builtin_amdgcn_readfirstlane(wave);
-    for (int t = wv; t < 10; t += 4) {
-      // t = 0..9 -> (mb, nb) = (3,3) (3,2) (3,1) (3,0) (2,2) (2,1) (2,0) (1,1) (1,0) (0,0)
-      const int mb = t < 4 ? 3 : t < 7 ? 2 : t < 9 ? 1 : 0;
-      const int nb = t < 4 ? 3 - t : t < 7 ? 6 - t : t < 9 ? 8 - t : 0;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int t = wave; t < 10; t += 4) {
+    // t = 0..9 -> (mb, nb) = (3,3) (3,2) (3,1) (3,0) (2,2) (2,1) (2,0) (1,1) (1,0) (0,0)
+    const int mb = t < 4 ? 3 : t < 7 ? 2 : t < 9 ? 1 : 0;
+    const int nb = t < 4 ? 3 - t : t < 7 ? 6 - t : t < 9 ? 8 - t : 0;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const u32x4 af = *reinterpret_cast<const u32x4 *>(&sK[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
-        const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[(16 * nb + r16) * kStrideK + 32 * kk + kg]);
-        acc = mfma_bf16(af, bf, acc);
-      }
-      const float Gj = sG[16 * nb + r16];
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 af = *reinterpret_cast<const u32x4 *>(&sX[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
+      const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sX[(16 * nb + r16) * kStrideK + 32 * kk + kg]);
+      acc = mfma_bf16(af, bf, acc);
+    }
+    const float Gj = sG[16 * nb + r16];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * mb + 4 * g + r, j = 16 * nb + r16;
-        const float e = sBeta[i] * expf(fminf(sG[i] - Gj, 0.f)) * acc[r];
-        sA[i * kStrideA4 + j] = (i > j && i < len) ? e : 0.f;
-      }
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * mb + 4 * g + r, j = 16 * nb + r16;
+      const float e = sBeta[i] * expf(fminf(sG[i] - Gj, 0.f)) * acc[r];
+      sA[ablk(mb, nb) + (4 * g + r) * 20 + r16] = (i > j && i < len) ? e : 0.f;
     }
   }
-  __syncthreads();  // K row-major is dead: its space takes V^T
+  // K^T as A-operand fragments of the state kernel (one v-head per q/k head
+  // writes them): fragment (mt, kk), lane (g, r16) = the 8 tokens 32 kk +
+  // 8 g .. of feature 16 mt + r16; wave w writes fragments 4 w .. 4 w + 3.
+  if (kW && h % H.ratio == 0) {
+    uint16_t *ktf = ws_kt + (static_cast<size_t>(c) * H.qk + hq) * (kDK * kChunk);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const int fi = 4 * wave + f, mt = fi >> 1, kk = fi & 1;
+      u32x4 x;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const u32x2 y = tile_col4(sX, 32 * kk + kg + 4 * hh, 16 * mt, r16);
+        x[2 * hh] = y[0];
+        x[2 * hh + 1] = y[1];
+      }
+      *reinterpret_cast<u32x4 *>(ktf + (fi * 64 + lane) * 8) = x;
+    }
+  }
+  __syncthreads();
 
-  if (!isK) transpose_into(sVt, false);
-
-  // Diagonal blocks D_w = (I + A_ww)^-1: wave w, lane j < 16 solves column j,
-  // column-oriented (each solved x_m is applied to all later rows at once, so
-  // the serial chain is one FMA per row).
+  // Diagonal blocks D_w = (I + A_ww)^-1 in place of A_ww: wave w, lane j < 16
+  // solves column j, column-oriented (each solved x_m is applied to all later
+  // rows at once, so the serial chain is one FMA per row).  Every read of
+  // A_ww precedes the writes in the wave's program order.
+  if (kU && !kW) {
+    // the u-only half: K is dead once A is built, V takes its place
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      *reinterpret_cast<u32x4 *>(&sX[(idx >> 4) * kStrideK + (idx & 15) * 8]) = vrows[i];
+    }
+  }
   if (lane < 16) {
-    const int base = 16 * wave;
+    float *Aw = sA + ablk(wave, wave);
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = i == lane ? 1.f : 0.f;
@@ -385,95 +441,69 @@ __device__ __forceinline__ void wy_intra(
     for (int m = 0; m < 15; ++m) {
       const float xm = x[m];
 #pragma unroll
-      for (int i = m + 1; i < 16; ++i) x[i] -= sA[(base + i) * kStrideA4 + base + m] * xm;
+      for (int i = m + 1; i < 16; ++i) x[i] -= Aw[i * 20 + m] * xm;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      sA[(16 * drow(wave) + i) * kStrideA4 + 16 * dcol(wave) + lane] = x[i];
+    for (int i = 0; i < 16; ++i) Aw[i * 20 + lane] = x[i];
   }
   __syncthreads();
 
-  // Blocked forward substitution over 64 right-hand-side columns per wave.
-  {
-    const bool isU = wave < 2;
-    const int col0 = (wave & 1) * 64;            // first V (or K) column of this wave
-    const uint16_t *Xt = isU ? sVt : sKt;         // X^T rows = features
-    const float *scl = isU ? sBeta : sBG;
-    f32x4 Y[4][4];                                // [block row][column tile]
-    u32x2 Yh[4][4], Yl[4][4];                     // their hi/lo splits (B operands)
+  const int col0 = 32 * wave;
+  if (kW) {
+    f32x4 Y[4][2];
+    wy_solve(sX, sBG, sA, col0, g, r16, Y);
+    __syncthreads();  // K is dead: its space is the w scratch
+    // w -> hi/lo A-operand fragments [mb][kk][lane][hi 8 | lo 8] (row
+    // 16 mb + r16, features 32 kk + 8 g ..), in two passes of 64 features
+    // through the f32 scratch: waves 2p, 2p + 1 fill it, then each wave
+    // converts two of the pass's eight fragments.
+    uint16_t *wf = ws_w + ch_head * (kChunk * kDK * 2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // Z = X_i - sum_{j<i} A_ij Y_j
-      const f32x4 s4 = *reinterpret_cast<const f32x4 *>(&scl[16 * i + 4 * g]);
-      f32x4 Z[4];
+    for (int pass = 0; pass < 2; ++pass) {
+      if ((wave >> 1) == pass) {
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const int n = col0 + 16 * nt + r16;
-        const u32x2 x2 = *reinterpret_cast<const u32x2 *>(&Xt[tsw(n, 16 * i + 4 * g)]);
-        Z[nt] = f32x4{s4[0] * __uint_as_float(x2[0] << 16),
-                      s4[1] * __uint_as_float(x2[0] & 0xffff0000u),
-                      s4[2] * __uint_as_float(x2[1] << 16),
-                      s4[3] * __uint_as_float(x2[1] & 0xffff0000u)};
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              scr[(16 * i + 4 * g + r) * kStrideS + (col0 & 63) + 16 * nt + r16] = Y[i][nt][r];
       }
+      __syncthreads();
 #pragma unroll
-      for (int j = 0; j < i; ++j) {
-        const f32x4 la = *reinterpret_cast<const f32x4 *>(&sA[(16 * i + r16) * kStrideA4 + 16 * j + 4 * g]);
-        u32x2 lh, ll;
-        split4(-la, lh, ll);
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) Z[nt] = mfma16_x3(lh, ll, Yh[j][nt], Yl[j][nt], Z[nt]);
+      for (int f = 0; f < 2; ++f) {
+        const int fi = 2 * wave + f, mb = fi >> 1, kk2 = fi & 1;
+        const float *row = &scr[(16 * mb + r16) * kStrideS + 32 * kk2 + kg];
+        const f32x4 x0 = *reinterpret_cast<const f32x4 *>(row);
+        const f32x4 x1 = *reinterpret_cast<const f32x4 *>(row + 4);
+        const float x8[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        u32x4 hi, lo;
+        split8(x8, hi, lo);
+        uint16_t *dst = wf + ((mb * 4 + 2 * pass + kk2) * 64 + lane) * 16;
+        *reinterpret_cast<u32x4 *>(dst) = hi;
+        *reinterpret_cast<u32x4 *>(dst + 8) = lo;
       }
-      // Y_i = D_i Z
-      const f32x4 d4 = *reinterpret_cast<const f32x4 *>(
-          &sA[(16 * drow(i) + r16) * kStrideA4 + 16 * dcol(i) + 4 * g]);
-      u32x2 dh, dl;
-      split4(d4, dh, dl);
+      __syncthreads();
+    }
+    if (kU) {
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        u32x2 zh, zl;
-        split4(Z[nt], zh, zl);
-        Y[i][nt] = mfma16_x3(dh, dl, zh, zl, f32x4{0.f, 0.f, 0.f, 0.f});
-        split4(Y[i][nt], Yh[i][nt], Yl[i][nt]);
+      for (int i = 0; i < 4; ++i) {
+        const int idx = tid + 256 * i;
+        *reinterpret_cast<u32x4 *>(&sX[(idx >> 4) * kStrideK + (idx & 15) * 8]) = vrows[i];
       }
+      __syncthreads();
     }
-
-    if (isU) {
-      // u tiles in MFMA result order: [chunk][head][row tile][col tile][lane][4]
-      float *ut = ws_u + ch_head * (kChunk * kDV);
+  }
+  if (kU) {
+    f32x4 Y[4][2];
+    wy_solve(sX, sBeta, sA, col0, g, r16, Y);
+    // u tiles in MFMA result order: [chunk][head][row tile][col tile][lane][4]
+    float *ut = ws_u + ch_head * (kChunk * kDV);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          *reinterpret_cast<f32x4 *>(ut + ((i * 8 + (col0 >> 4) + nt) * 64 + lane) * 4) = Y[i][nt];
-    }
-    __syncthreads();  // sKV and sA are free from here on: w transpose scratch
-
-    if (!isU) {
-      // w: through LDS to A-operand fragments (row 16*mb + r16, 8 consecutive
-      // k), split hi/lo: [chunk][head][mb][kk][lane][hi 8 | lo 8].
-      float *scr = (wave == 2) ? reinterpret_cast<float *>(sKV) : sA;  // [64][68]
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) scr[(16 * i + 4 * g + r) * kStrideA4 + 16 * nt + r16] = Y[i][nt][r];
-      uint16_t *wf = ws_w + ch_head * (kChunk * kDK * 2);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int kk2 = 0; kk2 < 2; ++kk2) {
-          const f32x4 x0 = *reinterpret_cast<const f32x4 *>(&scr[(16 * mb + r16) * kStrideA4 + 32 * kk2 + kg]);
-          const f32x4 x1 = *reinterpret_cast<const f32x4 *>(&scr[(16 * mb + r16) * kStrideA4 + 32 * kk2 + kg + 4]);
-          const float x8[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-          u32x4 hi, lo;
-          split8(x8, hi, lo);
-          const int kk = 2 * (wave - 2) + kk2;
-          uint16_t *dst = wf + ((mb * 4 + kk) * 64 + lane) * 16;
-          *reinterpret_cast<u32x4 *>(dst) = hi;
-          *reinterpret_cast<u32x4 *>(dst + 8) = lo;
-        }
-    }
+      for (int nt = 0; nt < 2; ++nt)
+        *reinterpret_cast<f32x4 *>(ut + ((i * 8 + 2 * wave + nt) * 64 + lane) * 4) = Y[i][nt];
   }
 }
 
@@ -669,10 +699,14 @@ __device__ __forceinline__ void t_intra(
 // ---------------------------------------------------------------------------
 // 2. intra-chunk: per (chunk c, v-head h) = chunk_head_of(blockIdx.x), one
 // kernel per form, each with its own LDS size (the T form's 35 KB lets four
-// workgroups share a CU, the WY form's 52 KB three).  When the form is left
+// workgroups share a CU, the WY form's 30 KB five).  When the form is left
 // to the device (form_flag != nullptr) both are launched and each returns at
 // once unless *form_flag names its form.
 // ---------------------------------------------------------------------------
+// SPLIT: two workgroups per (chunk, v-head), the w half and the u half;
+// workgroup id 16 s + 8 p + x (x = XCD) is half p of the pair 8 s + x, so
+// both halves of a chunk run on the same XCD and share its K rows in L2.
+template <bool SPLIT>
 __global__ __launch_bounds__(256) void prefill_intra_wy_kernel(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
@@ -683,12 +717,21 @@ __global__ __launch_bounds__(256) void prefill_intra_wy_kernel(
     uint16_t *__restrict__ ws_kt) {
   __shared__ __align__(16) char smem[kIntraWyLds];
   if (form_flag != nullptr && *form_flag != 0) return;
+  const int id = static_cast<int>(blockIdx.x);
+  const int pair = SPLIT ? (((id >> 4) << 3) | (id & 7)) : id;
   int c, h;
-  if (!chunk_head_of(blockIdx.x, nt_max, H, c, h)) return;
+  if (!chunk_head_of(pair, nt_max, H, c, h)) return;
   const int4 ch = chunk_info(chunks, c, one);
   if (ch.x < 0) return;
-  wy_intra(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u,
-           ws_kt);
+  if (!SPLIT)
+    wy_intra<0>(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w,
+                ws_u, ws_kt);
+  else if ((id >> 3) & 1)
+    wy_intra<2>(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w,
+                ws_u, ws_kt);
+  else
+    wy_intra<1>(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w,
+                ws_u, ws_kt);
 }
 
 __global__ __launch_bounds__(256) void prefill_intra_t_kernel(
@@ -769,7 +812,7 @@ __device__ __forceinline__ void load_wy_frag(WyFrag &f, int c, int h, const Head
 constexpr int kStateWyLds = 2 * 16 * kStrideK * 2 + 2 * 16 * kStrideT * 2;
 template <bool MAP>
 __device__ __forceinline__ void wy_state(
-    char *smem, int c0, int nch, int h, int v0, int wave, int lane, size_t sbase,
+    char *smem, int c0, int nch, int npre, int h, int v0, int wave, int lane, size_t sbase,
     const float *state, float *new_state, const float *ws_dcy, const float *ws_eg,
     const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt, uint16_t *ws_ht,
     uint16_t *ws_vnt, const Heads &H, int ht_c0) {
@@ -789,7 +832,7 @@ __device__ __forceinline__ void wy_state(
     if constexpr (MAP) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) S[mi][r] = vc == kr + r ? 1.f : 0.f;
-    } else if (state != nullptr && nch > 0) {
+    } else if (state != nullptr) {
       S[mi] = *reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + kr);
     } else {
       S[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -877,11 +920,13 @@ __device__ __forceinline__ void wy_state(
   // with the same loads pending from both of its predecessors and the
   // compiler waits for exactly the set in use (an exit after each step made it
   // merge those paths and wait for nearly every prefetch).  The last 0-2
-  // chunks run after the loop.  Prefetches past the last chunk re-read it,
-  // so every iteration issues the same loads.  (A fourth set measured slower:
-  // the extra registers push accumulators into AGPRs.)
-  if (nch > 0) {
-    auto chunk_at = [&](int i) { return c0 + (i < nch ? i : nch - 1); };
+  // chunks run after the loop.  Prefetches are clamped to npre chunks, a
+  // bound known at launch (for one sequence, from T), so the first ones go
+  // out before the chunk count arrives from memory; past the last chunk they
+  // re-read a chunk slot of the workspace and are never used.  (A fourth set
+  // measured slower: the extra registers push accumulators into AGPRs.)
+  if (npre > 0) {
+    auto chunk_at = [&](int i) { return c0 + (i < npre ? i : npre - 1); };
     WyFrag fa, fb, fc;
 #define GDN_LOAD(F, I) \
     load_wy_frag<!MAP>(F, chunk_at(I), h, H, vw, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt)
@@ -906,7 +951,8 @@ __device__ __forceinline__ void wy_state(
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
     const int kr = 16 * (2 * wave + mi) + q4, vc = vw + r16;
-    *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + kr) = S[mi];
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + kr) = (MAP || nch > 0) ? S[mi] : z;
   }
 }
 
@@ -1193,8 +1239,8 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
     const uint16_t *k, const uint16_t *v, const float *state, float *new_state,
     const int4 *chunks, const int *offsets, const float *ws_dcy, const float *ws_eg,
     const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt, uint16_t *ws_ht,
-    uint16_t *ws_vnt, int N, OneSeq one, Heads H, int form, SplitScan sp, const void *cu,
-    int cu64, int T, uint16_t *out) {
+    uint16_t *ws_vnt, int N, int nt_max, OneSeq one, Heads H, int form, SplitScan sp,
+    const void *cu, int cu64, int T, uint16_t *out) {
   __shared__ __align__(16) char smem[kStateWyLds > kStateTLds ? kStateWyLds : kStateTLds];
   constexpr int NVB = kDV / 16;
   const int h = blockIdx.x % H.v;
@@ -1203,17 +1249,22 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in SGPRs
 
-  // This workgroup's chunks: c0 .. c0 + nch - 1; the sequence's tokens [bos, eos).
-  int c0 = 0, nch = 0, bos = 0, eos = 0;
+  // This workgroup's chunks: c0 .. c0 + nch - 1 (prefetches clamped to npre
+  // chunks, known at launch for one sequence); the tokens [bos, eos).
+  int c0 = 0, nch = 0, npre = 0, bos = 0, eos = 0;
   size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;  // [V][K]
+  // (the bounds of the rows this batch covers are loaded now, used at the end)
+  const CoveredRows rows = covered_rows(cu, cu64, N, T);
   if (one.cu != nullptr) {
     one_seq_bounds(one, bos, eos);
     nch = (eos - bos + kChunk - 1) / kChunk;
+    npre = nt_max;
   } else {
     if (offsets[N + 1]) return;  // the sequential kernel owns the batch
     if (form < 0) form = offsets[N + 2];
     c0 = offsets[s];
     nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
+    npre = nch;
     if (form == 1 && nch > 0) {  // the T form's token range
       const int4 first = chunks[c0], last = chunks[c0 + nch - 1];
       bos = first.y;
@@ -1223,26 +1274,31 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
   if (sp.nt0 > 0) {  // two-segment scan of one sequence (WY form)
     sbase = static_cast<size_t>(h) * kDV * kDK;
     if (s == 2) {
-      wy_state<true>(smem, sp.nt0, nch - sp.nt0, h, vb * 16, wave, lane, sbase, nullptr, sp.mend,
-                     ws_dcy, ws_eg, ws_w, ws_u, ws_kt, sp.htm, ws_vnt, H, sp.nt0);
+      wy_state<true>(smem, sp.nt0, nch - sp.nt0, nt_max - sp.nt0, h, vb * 16, wave, lane, sbase,
+                     nullptr, sp.mend, ws_dcy, ws_eg, ws_w, ws_u, ws_kt, sp.htm, ws_vnt, H, sp.nt0);
+      form = -2;
     } else if (s == 0) {
-      wy_state<false>(smem, 0, nch < sp.nt0 ? nch : sp.nt0, h, vb * 16, wave, lane, sbase, state,
-                      sp.send, ws_dcy, ws_eg, ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0);
+      nch = nch < sp.nt0 ? nch : sp.nt0;
+      npre = sp.nt0;
+      new_state = sp.send;
     } else {
-      wy_state<false>(smem, sp.nt0, nch - sp.nt0, h, vb * 16, wave, lane, sbase, nullptr, sp.cend,
-                      ws_dcy, ws_eg, ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0);
+      c0 = sp.nt0;
+      nch -= sp.nt0;
+      npre = nt_max - sp.nt0;
+      state = nullptr;
+      new_state = sp.cend;
     }
-  } else if (form == 1) {
+  }
+  if (form == 1) {
     // the T form reads K and V itself: the sequence's tokens [bos, eos)
     t_state(smem, c0, nch, bos, eos, h, vb * 16, wave, lane, sbase, k, v, state, new_state, ws_dcy,
             ws_eg, ws_w, ws_u, ws_ht, ws_vnt, H);
-  } else {
-    wy_state<false>(smem, c0, nch, h, vb * 16, wave, lane, sbase, state, new_state, ws_dcy, ws_eg,
-                    ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0);
+  } else if (form != -2) {
+    wy_state<false>(smem, c0, nch, npre, h, vb * 16, wave, lane, sbase, state, new_state, ws_dcy,
+                    ws_eg, ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0);
   }
-  // The chunk pipeline owns the batch: rows outside every sequence get zeros
-  // (after the chain, so that the common case's check costs the chain nothing).
-  zero_uncovered_rows(out, cu, cu64, N, T, H.v, blockIdx.x, gridDim.x);
+  // The chunk pipeline owns the batch: rows outside every sequence get zeros.
+  zero_rows_outside(out, rows, T, H.v, blockIdx.x, gridDim.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1769,8 +1825,14 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     const int *flag = P.form < 0 ? offsets + N + 2 : nullptr;
     const dim3 grid(static_cast<unsigned>(P.intra_grid));
     if (P.form != 1) {
-      hipLaunchKernelGGL(prefill_intra_wy_kernel, grid, dim3(256), 0, stream, k, v, A_log, a,
-                         dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu, kt);
+      if (P.intra_split)
+        hipLaunchKernelGGL(prefill_intra_wy_kernel<true>, dim3(2 * grid.x), dim3(256), 0, stream, k,
+                           v, A_log, a, dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE,
+                           wsw, wsu, kt);
+      else
+        hipLaunchKernelGGL(prefill_intra_wy_kernel<false>, grid, dim3(256), 0, stream, k, v, A_log,
+                           a, dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu,
+                           kt);
       if ((rc = check_launch(what))) return rc;
     }
     if (P.form != 0) {
@@ -1788,7 +1850,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   }
   hipLaunchKernelGGL(prefill_state_kernel, dim3(static_cast<unsigned>(P.state_grid)), dim3(256), 0,
                      stream, k, v, state, new_state, chunks, offsets, wsD, wsE, wsw, wsu, kt, ht,
-                     vnt, N, one, H, P.form, sp, cu_seqlens, cu64, T, output);
+                     vnt, N, L.nt_max, one, H, P.form, sp, cu_seqlens, cu64, T, output);
   if ((rc = check_launch(what))) return rc;
   if (P.split_grid > 0) {
     // new_state and the output of the second segment's chunks

@@ -169,13 +169,16 @@ def test_plan_sweep(driver):
     for c, got in zip(cases, out):
         f = [int(x) for x in got.split()]
         plans[c] = dict(rc=f[0], sequential=f[1], seq_variant=f[2], choose=f[3], single=f[4],
-                        form=f[5], nt0=f[6], intra=f[7], state=f[8], split=f[9], out=f[10])
+                        form=f[5], nt0=f[6], intra=f[7], state=f[8], split=f[9], out=f[10],
+                        intra_split=f[11])
     base = (-1, -1, -1)
     p = plans[(96, 1, 4, 8) + base]
     assert p["sequential"] == 1
     p = plans[(8192, 1, 4, 8) + base]
     assert (p["single"], p["form"], p["nt0"], p["state"], p["split"]) == (1, 0, 64, 192, 512)
     assert p["out"] == 64 * 4 // 8 * 8 * 2 + 32 * 8  # chunk-head pairs + new_state tiles
+    assert p["intra_split"] == 0  # 1024 chunk-head pairs fill the CUs
+    assert plans[(1000, 1, 4, 8) + base]["intra_split"] == 1  # 128 pairs: two halves each
     p = plans[(8192, 1, 4, 8, 2, -1, -1)]
     assert p["nt0"] == 0 and p["state"] == 64
     p = plans[(32768, 2, 4, 8) + base]
