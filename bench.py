@@ -76,6 +76,7 @@ ONLY_WORKLOADS = {
     "prefill_4x8192": ("prefill", [8192] * 4),
     "prefill_1x1024": ("prefill", [1024]),
     "prefill_64x16": ("prefill", [16] * 64),
+    "prefill_256x1": ("prefill", [1] * 256),
     "prefill_64x256": ("prefill", [256] * 64),
     "prefill_configs3": ("prefill", [6, 49, 294, 1800, 2040, 61]),
     "prefill_8x2048": ("prefill", [2048] * 8),

@@ -240,13 +240,21 @@ int plan_prefill(int T, int N, const Heads &H, const PrefillLayout &L, int varia
   const long long grid = chunk_head_grid(L.nt_max, H);
   if (grid > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "%s: too many tokens", what);
   P.intra_grid = L.nt_max > 0 ? grid : 0;
-  P.intra_split = P.form != 1 && 2 * P.intra_grid <= static_cast<long long>(kNumCus) * kIntraSplitPerCu;
+  P.intra_split = P.form == 0 && 2 * P.intra_grid <= static_cast<long long>(kNumCus) * kIntraSplitPerCu;
+  if (P.intra_split) P.intra_grid *= 2;
+  P.loop = P.choose != 0;
+  auto cap = [&P](long long units, int per_cu) {
+    const long long most = static_cast<long long>(kNumCus) * per_cu;
+    return P.loop && units > most ? most : units;
+  };
+
   if (P.single && P.form == 0 && variant != 2 && L.nt_max >= 2 && 24 * H.v <= 256 &&
       (variant == 3 || L.nt_max >= kSplitMinChunks))
     P.split_nt0 = split_first(L.nt_max);
   const bool split = P.split_nt0 > 0;
-  P.state_grid = static_cast<long long>(split ? 3 : N) * H.v * (kDV / 16);
-  if (P.state_grid > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "%s: too many sequences", what);
+  const long long state_units = static_cast<long long>(split ? 3 : N) * H.v * (kDV / 16);
+  if (state_units > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "%s: too many sequences", what);
+  P.state_grid = cap(state_units, kStatePerCu);
   P.split_grid = split ? static_cast<long long>(L.nt_max - P.split_nt0) * H.v : 0;
   P.out_grid = L.nt_max > 0 ? chunk_head_grid(split ? P.split_nt0 : L.nt_max, H) +
                                   (split ? kStateTiles * H.v : 0)

@@ -116,6 +116,12 @@ constexpr int kSplitMinChunks = 32;
 // CUs then halves its per-chunk latency instead of idling CUs.
 constexpr int kNumCus = 256;
 constexpr int kIntraSplitPerCu = 2;
+// Workgroups the state kernel keeps resident per CU (its VGPRs): when the
+// device makes the path choice, its grid is capped at this many per CU and
+// it loops over the rest of its units (a multiple of 8, so a unit keeps its
+// XCD), so that a batch handed to a sequential kernel does not dispatch a
+// full grid (N x 64 workgroups) of idle ones.
+constexpr int kStatePerCu = 2;
 
 // What a prefill call launches, decided from (T, N), the head layout and the
 // tuning arguments alone (cu_seqlens is never read on the host).
@@ -128,7 +134,10 @@ struct PrefillPlan {
   int form;         // per-chunk operands: 0 WY, 1 T, -1 the index kernel's rule
   int split_nt0;    // two-segment scan: first chunk of the second segment; 0 none
   bool intra_split; // WY intra kernel as two workgroups per (chunk, v-head)
-  // launch grids (workgroups); 0 = not launched
+  bool loop;        // the state kernel loops over its units in a capped grid
+                    // (when the device makes the path choice, choose != 0)
+  // launch grids (workgroups, capped at the resident ones; the kernels loop
+  // over the remaining units); 0 = not launched
   long long intra_grid, state_grid, split_grid, out_grid;
 };
 

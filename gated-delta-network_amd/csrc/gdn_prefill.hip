@@ -697,27 +697,28 @@ __device__ __forceinline__ void t_intra(
 
 
 // ---------------------------------------------------------------------------
-// 2. intra-chunk: per (chunk c, v-head h) = chunk_head_of(blockIdx.x), one
-// kernel per form, each with its own LDS size (the T form's 35 KB lets four
-// workgroups share a CU, the WY form's 30 KB five).  When the form is left
-// to the device (form_flag != nullptr) both are launched and each returns at
-// once unless *form_flag names its form.
+// 2. intra-chunk: per (chunk c, v-head h) = chunk_head_of(unit), one kernel
+// instantiated per form with its own LDS size (WY 31 KB: four to five
+// workgroups per CU; T 35 KB: four), and once for a form the device picks
+// (FORM -1: the index kernel's flag chooses the path per launch; the union
+// of both, 35 KB and 104 VGPRs, still fits four per CU), so a device-decided
+// batch pays one intra launch, not two.
+//
+// One unit per workgroup: looping over units raised register pressure (the
+// WY intra kernel would drop to three workgroups per CU, the output kernel
+// would spill); only the state kernel loops (see there).
 // ---------------------------------------------------------------------------
 // SPLIT: two workgroups per (chunk, v-head), the w half and the u half;
 // workgroup id 16 s + 8 p + x (x = XCD) is half p of the pair 8 s + x, so
 // both halves of a chunk run on the same XCD and share its K rows in L2.
 template <bool SPLIT>
-__global__ __launch_bounds__(256) void prefill_intra_wy_kernel(
-    const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+__device__ __forceinline__ void intra_wy_unit(
+    char *smem, int id, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
-    const int4 *__restrict__ chunks, OneSeq one, int nt_max, Heads H,
-    const int *__restrict__ form_flag, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
-    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u,
-    uint16_t *__restrict__ ws_kt) {
-  __shared__ __align__(16) char smem[kIntraWyLds];
-  if (form_flag != nullptr && *form_flag != 0) return;
-  const int id = static_cast<int>(blockIdx.x);
+    const int4 *__restrict__ chunks, const OneSeq &one, int nt_max, const Heads &H,
+    float *__restrict__ ws_G, float *__restrict__ ws_dcy, float *__restrict__ ws_eg,
+    uint16_t *__restrict__ ws_w, float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
   const int pair = SPLIT ? (((id >> 4) << 3) | (id & 7)) : id;
   int c, h;
   if (!chunk_head_of(pair, nt_max, H, c, h)) return;
@@ -734,20 +735,31 @@ __global__ __launch_bounds__(256) void prefill_intra_wy_kernel(
                 ws_u, ws_kt);
 }
 
-__global__ __launch_bounds__(256) void prefill_intra_t_kernel(
-    const uint16_t *__restrict__ k, const float *__restrict__ A_log,
-    const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
-    const uint16_t *__restrict__ b, const int4 *__restrict__ chunks, OneSeq one, int nt_max,
-    Heads H, const int *__restrict__ form_flag, float *__restrict__ ws_G,
-    float *__restrict__ ws_dcy, float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w,
-    float *__restrict__ ws_u) {
-  __shared__ __align__(16) char smem[kIntraTLds];
-  if (form_flag != nullptr && *form_flag != 1) return;
-  int c, h;
-  if (!chunk_head_of(blockIdx.x, nt_max, H, c, h)) return;
-  const int4 ch = chunk_info(chunks, c, one);
-  if (ch.x < 0) return;
-  t_intra(smem, c, h, ch.y, ch.z, k, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u);
+template <int FORM, bool SPLIT>
+__global__ __launch_bounds__(256) void prefill_intra_kernel(
+    const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+    const float *__restrict__ A_log, const uint16_t *__restrict__ a,
+    const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
+    const int4 *__restrict__ chunks, OneSeq one, int nt_max, Heads H,
+    const int *__restrict__ form_flag, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
+    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u,
+    uint16_t *__restrict__ ws_kt) {
+  static_assert(!(SPLIT && FORM != 0), "only the WY form splits into halves");
+  constexpr int kLds = FORM == 0 ? kIntraWyLds
+                       : FORM == 1 ? kIntraTLds
+                                   : (kIntraWyLds > kIntraTLds ? kIntraWyLds : kIntraTLds);
+  __shared__ __align__(16) char smem[kLds];
+  const int form = FORM >= 0 ? FORM : *form_flag;
+  if (form == 1) {
+    int c, h;
+    if (!chunk_head_of(blockIdx.x, nt_max, H, c, h)) return;
+    const int4 ch = chunk_info(chunks, c, one);
+    if (ch.x < 0) return;
+    t_intra(smem, c, h, ch.y, ch.z, k, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u);
+  } else {
+    intra_wy_unit<SPLIT>(smem, blockIdx.x, k, v, A_log, a, dt_bias, b, chunks, one, nt_max, H,
+                         ws_G, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1207,10 +1219,10 @@ __device__ __forceinline__ void t_state(
 
 
 // ---------------------------------------------------------------------------
-// 3. state recurrence: per (sequence s, v-head h, 16 columns of V),
-// blockIdx.x = h + H.v * (vb + 8 s): with 8 v-heads every workgroup of one
-// head lands on the same XCD (workgroups are dealt round-robin over the 8
-// XCDs), so the per-head operands stream through one L2.  The state tile
+// 3. state recurrence: per (sequence s, v-head h, 16 columns of V), unit
+// h + H.v * (vb + 8 s): with 8 v-heads every unit of one head lands on the
+// same XCD (workgroups are dealt round-robin over the 8 XCDs, and the grid is
+// a multiple of 8), so the per-head operands stream through one L2.  The state tile
 // S[:, v0:v0+16] ([K=128] x [16], f32) lives in MFMA accumulators.  The form
 // is `form` (0 WY, 1 T) or, when form < 0, the index kernel's flag.
 //
@@ -1235,33 +1247,30 @@ struct SplitScan {
   float *send, *cend, *mend;  // [H.v][128][128] f32 each
 };
 
-__global__ __launch_bounds__(256) void prefill_state_kernel(
-    const uint16_t *k, const uint16_t *v, const float *state, float *new_state,
-    const int4 *chunks, const int *offsets, const float *ws_dcy, const float *ws_eg,
-    const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt, uint16_t *ws_ht,
-    uint16_t *ws_vnt, int N, int nt_max, OneSeq one, Heads H, int form, SplitScan sp,
-    const void *cu, int cu64, int T, uint16_t *out) {
-  __shared__ __align__(16) char smem[kStateWyLds > kStateTLds ? kStateWyLds : kStateTLds];
+// One unit of the state kernel: sequence s, v-head h, V-block vb (unit =
+// h + H.v (vb + 8 s)); `form` as settled for the batch (0 WY, 1 T).
+__device__ __forceinline__ void state_unit(
+    char *smem, int unit, const uint16_t *k, const uint16_t *v, const float *state,
+    float *new_state, const int4 *chunks, const int *offsets, const float *ws_dcy,
+    const float *ws_eg, const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt,
+    uint16_t *ws_ht, uint16_t *ws_vnt, int nt_max, const OneSeq &one, const Heads &H, int form,
+    const SplitScan &sp) {
   constexpr int NVB = kDV / 16;
-  const int h = blockIdx.x % H.v;
-  const int rest = blockIdx.x / H.v;
+  const int h = unit % H.v;
+  const int rest = unit / H.v;
   const int vb = rest % NVB, s = rest / NVB;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in SGPRs
 
-  // This workgroup's chunks: c0 .. c0 + nch - 1 (prefetches clamped to npre
+  // This unit's chunks: c0 .. c0 + nch - 1 (prefetches clamped to npre
   // chunks, known at launch for one sequence); the tokens [bos, eos).
   int c0 = 0, nch = 0, npre = 0, bos = 0, eos = 0;
   size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;  // [V][K]
-  // (the bounds of the rows this batch covers are loaded now, used at the end)
-  const CoveredRows rows = covered_rows(cu, cu64, N, T);
   if (one.cu != nullptr) {
     one_seq_bounds(one, bos, eos);
     nch = (eos - bos + kChunk - 1) / kChunk;
     npre = nt_max;
   } else {
-    if (offsets[N + 1]) return;  // the sequential kernel owns the batch
-    if (form < 0) form = offsets[N + 2];
     c0 = offsets[s];
     nch = offsets[s + 1] - c0 > 0 ? offsets[s + 1] - c0 : 0;
     npre = nch;
@@ -1276,8 +1285,9 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
     if (s == 2) {
       wy_state<true>(smem, sp.nt0, nch - sp.nt0, nt_max - sp.nt0, h, vb * 16, wave, lane, sbase,
                      nullptr, sp.mend, ws_dcy, ws_eg, ws_w, ws_u, ws_kt, sp.htm, ws_vnt, H, sp.nt0);
-      form = -2;
-    } else if (s == 0) {
+      return;
+    }
+    if (s == 0) {
       nch = nch < sp.nt0 ? nch : sp.nt0;
       npre = sp.nt0;
       new_state = sp.send;
@@ -1293,9 +1303,36 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
     // the T form reads K and V itself: the sequence's tokens [bos, eos)
     t_state(smem, c0, nch, bos, eos, h, vb * 16, wave, lane, sbase, k, v, state, new_state, ws_dcy,
             ws_eg, ws_w, ws_u, ws_ht, ws_vnt, H);
-  } else if (form != -2) {
+  } else {
     wy_state<false>(smem, c0, nch, npre, h, vb * 16, wave, lane, sbase, state, new_state, ws_dcy,
                     ws_eg, ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0);
+  }
+}
+
+template <bool LOOP>
+__global__ __launch_bounds__(256) void prefill_state_kernel(
+    const uint16_t *k, const uint16_t *v, const float *state, float *new_state,
+    const int4 *chunks, const int *offsets, const float *ws_dcy, const float *ws_eg,
+    const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt, uint16_t *ws_ht,
+    uint16_t *ws_vnt, int N, int nt_max, OneSeq one, Heads H, int form, SplitScan sp,
+    const void *cu, int cu64, int T, uint16_t *out) {
+  __shared__ __align__(16) char smem[kStateWyLds > kStateTLds ? kStateWyLds : kStateTLds];
+  // (the bounds of the rows this batch covers are loaded now, used at the end)
+  const CoveredRows rows = covered_rows(cu, cu64, N, T);
+  if (one.cu == nullptr) {
+    if (offsets[N + 1]) return;  // the sequential kernel owns the batch
+    if (form < 0) form = offsets[N + 2];
+  }
+  const int units = (sp.nt0 > 0 ? 3 : N) * H.v * (kDV / 16);
+  if (!LOOP) {
+    state_unit(smem, blockIdx.x, k, v, state, new_state, chunks, offsets, ws_dcy, ws_eg, ws_w,
+               ws_u, ws_kt, ws_ht, ws_vnt, nt_max, one, H, form, sp);
+  } else {
+    for (int unit = blockIdx.x; unit < units; unit += gridDim.x) {
+      state_unit(smem, unit, k, v, state, new_state, chunks, offsets, ws_dcy, ws_eg, ws_w, ws_u,
+                 ws_kt, ws_ht, ws_vnt, nt_max, one, H, form, sp);
+      __syncthreads();  // the next unit reuses the LDS tiles
+    }
   }
   // The chunk pipeline owns the batch: rows outside every sequence get zeros.
   zero_rows_outside(out, rows, T, H.v, blockIdx.x, gridDim.x);
@@ -1608,27 +1645,25 @@ __device__ __forceinline__ void split_state_tile(char *smem, int f, const Heads 
 //   P  = mask_{j<=i} exp(G_i - G_j) Q K^T      (waves split the rows)
 //   O  = exp(G_i) Q S_c + P v_new              (waves split the columns)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
-void prefill_output_kernel(
-    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
-    const int4 *__restrict__ chunks, OneSeq one, int nt_max, Heads H,
+constexpr int kOutputLds = kChunk * kStrideK * 2 + kChunk * kStrideT * 2 + kChunk * 4;
+__device__ __forceinline__ void output_unit(
+    char *osmem, int id, const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
+    const int4 *__restrict__ chunks, const OneSeq &one, int nt_max, const Heads &H,
     const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
-    uint16_t *__restrict__ out, SplitScan sp, float *__restrict__ new_state) {
-  // 27 KB of LDS and at most 128 VGPRs: four workgroups per CU.
-  __shared__ __align__(16) char osmem[kChunk * kStrideK * 2 + kChunk * kStrideT * 2 + kChunk * 4];
+    uint16_t *__restrict__ out, const SplitScan &sp, float *__restrict__ new_state) {
   uint16_t *const sQ = reinterpret_cast<uint16_t *>(osmem);  // [64][kStrideK]
   uint16_t *const sP = sQ + kChunk * kStrideK;                // [64][kStrideT]
   float *const sG = reinterpret_cast<float *>(sP + kChunk * kStrideT);
-  static_assert(16 * kDK * 4 + kDK * 32 * 4 <= sizeof(osmem), "new_state tile must fit");
+  static_assert(16 * kDK * 4 + kDK * 32 * 4 <= kOutputLds, "new_state tile must fit");
   // After a two-segment scan the first kStateTiles H.v workgroups compute
   // new_state.
   const int nfix = sp.nt0 > 0 ? kStateTiles * H.v : 0;
-  if (static_cast<int>(blockIdx.x) < nfix) {
-    split_state_tile(osmem, blockIdx.x, H, sp, new_state);
+  if (id < nfix) {
+    split_state_tile(osmem, id, H, sp, new_state);
     return;
   }
   int c, h;
-  if (!chunk_head_of(blockIdx.x - nfix, nt_max, H, c, h)) return;
+  if (!chunk_head_of(id - nfix, nt_max, H, c, h)) return;
   const int4 ch = chunk_info(chunks, c, one);
   if (ch.x < 0) return;
   const int start = ch.y, len = ch.z;
@@ -1755,6 +1790,18 @@ void prefill_output_kernel(
   }
 }
 
+// 27 KB of LDS and at most 128 VGPRs: four workgroups per CU.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+void prefill_output_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
+    const int4 *__restrict__ chunks, OneSeq one, int nt_max, Heads H,
+    const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
+    uint16_t *__restrict__ out, SplitScan sp, float *__restrict__ new_state) {
+  __shared__ __align__(16) char osmem[kOutputLds];
+  output_unit(osmem, blockIdx.x, q, k, chunks, one, nt_max, H, ws_G, ws_ht, ws_vnt, scale, out, sp,
+              new_state);
+}
+
 // The output of a batch without sequences (N == 0): every row is zero.
 __global__ __launch_bounds__(256) void prefill_zero_kernel(uint16_t *out, const void *cu, int cu64,
                                                            int T, int hv) {
@@ -1822,24 +1869,15 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     if (rc) return rc;
   }
   if (P.intra_grid > 0) {
-    const int *flag = P.form < 0 ? offsets + N + 2 : nullptr;
-    const dim3 grid(static_cast<unsigned>(P.intra_grid));
-    if (P.form != 1) {
-      if (P.intra_split)
-        hipLaunchKernelGGL(prefill_intra_wy_kernel<true>, dim3(2 * grid.x), dim3(256), 0, stream, k,
-                           v, A_log, a, dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE,
-                           wsw, wsu, kt);
-      else
-        hipLaunchKernelGGL(prefill_intra_wy_kernel<false>, grid, dim3(256), 0, stream, k, v, A_log,
-                           a, dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu,
-                           kt);
-      if ((rc = check_launch(what))) return rc;
-    }
-    if (P.form != 0) {
-      hipLaunchKernelGGL(prefill_intra_t_kernel, grid, dim3(256), 0, stream, k, A_log, a,
-                         dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE, wsw, wsu);
-      if ((rc = check_launch(what))) return rc;
-    }
+    const int *flag = offsets + N + 2;  // read only when the device picks the form
+    auto intra = P.intra_split ? prefill_intra_kernel<0, true>
+                 : P.form == 0 ? prefill_intra_kernel<0, false>
+                 : P.form == 1 ? prefill_intra_kernel<1, false>
+                               : prefill_intra_kernel<-1, false>;
+    hipLaunchKernelGGL(intra, dim3(static_cast<unsigned>(P.intra_grid)), dim3(256), 0, stream, k,
+                       v, A_log, a, dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE, wsw,
+                       wsu, kt);
+    if ((rc = check_launch(what))) return rc;
   }
   SplitScan sp{P.split_nt0, nullptr, nullptr, nullptr, nullptr};
   if (sp.nt0 > 0) {
@@ -1848,7 +1886,8 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     sp.cend = reinterpret_cast<float *>(ws + L.cend);
     sp.mend = reinterpret_cast<float *>(ws + L.mend);
   }
-  hipLaunchKernelGGL(prefill_state_kernel, dim3(static_cast<unsigned>(P.state_grid)), dim3(256), 0,
+  hipLaunchKernelGGL(P.loop ? prefill_state_kernel<true> : prefill_state_kernel<false>,
+                     dim3(static_cast<unsigned>(P.state_grid)), dim3(256), 0,
                      stream, k, v, state, new_state, chunks, offsets, wsD, wsE, wsw, wsu, kt, ht,
                      vnt, N, L.nt_max, one, H, P.form, sp, cu_seqlens, cu64, T, output);
   if ((rc = check_launch(what))) return rc;

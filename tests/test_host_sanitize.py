@@ -170,7 +170,7 @@ def test_plan_sweep(driver):
         f = [int(x) for x in got.split()]
         plans[c] = dict(rc=f[0], sequential=f[1], seq_variant=f[2], choose=f[3], single=f[4],
                         form=f[5], nt0=f[6], intra=f[7], state=f[8], split=f[9], out=f[10],
-                        intra_split=f[11])
+                        intra_split=f[11], loop=f[12])
     base = (-1, -1, -1)
     p = plans[(96, 1, 4, 8) + base]
     assert p["sequential"] == 1
@@ -189,4 +189,10 @@ def test_plan_sweep(driver):
     assert plans[(INT_MAX, INT_MAX, 4, 8) + base]["rc"] == _lib.GDN_ERR_INVALID  # grid too large
     for c, p in plans.items():
         if p["rc"] == 0 and not p["sequential"]:
-            assert 0 < p["state"] <= INT_MAX and 0 <= p["intra"] <= INT_MAX, c
+            # multiples of 8 so that a unit keeps its XCD; when the device
+            # makes the path choice, the state grid is capped at the
+            # resident workgroups (2 per CU of 256)
+            assert p["state"] % 8 == 0 and p["intra"] % 8 == 0 and p["out"] % 8 == 0, c
+            assert p["loop"] == (p["choose"] != 0), c
+            if p["loop"]:
+                assert p["state"] <= 512, c
