@@ -508,7 +508,7 @@ __device__ __forceinline__ void wy_intra(
 }
 
 
-// T form of the intra kernel (per chunk c, v-head h; LDS from smem, 35 KB):
+// T form of the intra kernel (per chunk c, v-head h; LDS from smem, 30 KB):
 //   * wave 0: gating, chunk-local cumsum G, the per-token vectors.
 //   * A = strictly-lower(beta_i exp(G_i - G_j) K K^T) on MFMA (K exact bf16).
 //   * T = (I + A)^-1: the four 16x16 diagonal blocks D_i by forward
@@ -519,7 +519,7 @@ __device__ __forceinline__ void wy_intra(
 // T goes to the workspace (w region) as split A-operand fragments of the
 // state kernel, which applies it to the state-dependent right-hand side
 // itself; (beta, beta e^G) go to the u region.
-constexpr int kIntraTLds = kChunk * kStrideK * 2 + kChunk * 68 * 4 + 2 * kChunk * 4;
+constexpr int kIntraTLds = kChunk * kStrideK * 2 + 10 * kABlk * 4 + 2 * kChunk * 4;
 __device__ __forceinline__ void t_intra(
     char *smem, int c, int h, int start, int len, const uint16_t *__restrict__ k,
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
@@ -531,19 +531,16 @@ __device__ __forceinline__ void t_intra(
   const int hq = h / H.ratio;
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
 
-  constexpr int kStrideA4 = 68;  // f32 stride of the 64x64 tiles (16-byte rows)
+  constexpr int kStrideA4 = 68;  // f32 stride of the T scratch (16-byte rows)
   //   sK: K row-major until A is built, then T (f32 [64][68]) for the
   //       fragment transposition.
-  //   sA: strictly lower blocks of A; the unused upper blocks hold the four
-  //       16x16 diagonal inverses (D_w at block (drow(w), dcol(w))).
+  //   sA: the ten lower 16x16 blocks of A (as the WY kernel's); the
+  //       diagonal ones become the inverses D_w.
   uint16_t *const sK = reinterpret_cast<uint16_t *>(smem);                   // [64][136]
-  float *const sA = reinterpret_cast<float *>(sK + kChunk * kStrideK);        // [64][68]
-  float *const sBeta = sA + kChunk * kStrideA4, *const sG = sBeta + kChunk;
+  float *const sA = reinterpret_cast<float *>(sK + kChunk * kStrideK);        // 10 blocks
+  float *const sBeta = sA + 10 * kABlk, *const sG = sBeta + kChunk;
   static_assert(kChunk * kStrideA4 * 4 <= kChunk * kStrideK * 2, "T must fit in the K tile");
   float *const sT = reinterpret_cast<float *>(sK);
-  // D_w lives at row block w, column block dcol(w): (0,1), (1,2), (2,3), (0,2).
-  auto dcol = [](int w) { return w == 3 ? 2 : w + 1; };
-  auto drow = [](int w) { return w == 3 ? 0 : w; };
 
   // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding tokens
   // get g = 0 and beta = 0, so G stays at G_last past the end of the chunk.
@@ -608,17 +605,18 @@ __device__ __forceinline__ void t_intra(
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * mb + 4 * g + r, j = 16 * nb + r16;
         const float e = sBeta[i] * expf(fminf(sG[i] - Gj, 0.f)) * acc[r];
-        sA[i * kStrideA4 + j] = (i > j && i < len) ? e : 0.f;
+        sA[ablk(mb, nb) + (4 * g + r) * 20 + r16] = (i > j && i < len) ? e : 0.f;
       }
     }
   }
   __syncthreads();
 
-  // Diagonal blocks D_w = (I + A_ww)^-1: wave w, lane j < 16 solves column j,
-  // column-oriented (each solved x_m is applied to all later rows at once, so
-  // the serial chain is one FMA per row).
+  // Diagonal blocks D_w = (I + A_ww)^-1 in place of A_ww: wave w, lane j < 16
+  // solves column j, column-oriented (each solved x_m is applied to all
+  // later rows at once, so the serial chain is one FMA per row); every read
+  // of A_ww precedes the wave's writes.
   if (lane < 16) {
-    const int base = 16 * wave;
+    float *Aw = sA + ablk(wave, wave);
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = i == lane ? 1.f : 0.f;
@@ -626,11 +624,10 @@ __device__ __forceinline__ void t_intra(
     for (int m = 0; m < 15; ++m) {
       const float xm = x[m];
 #pragma unroll
-      for (int i = m + 1; i < 16; ++i) x[i] -= sA[(base + i) * kStrideA4 + base + m] * xm;
+      for (int i = m + 1; i < 16; ++i) x[i] -= Aw[i * 20 + m] * xm;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      sA[(16 * drow(wave) + i) * kStrideA4 + 16 * dcol(wave) + lane] = x[i];
+    for (int i = 0; i < 16; ++i) Aw[i * 20 + lane] = x[i];
   }
   __syncthreads();
 
@@ -647,8 +644,8 @@ __device__ __forceinline__ void t_intra(
         Tc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         Th[i] = Tl[i] = u32x2{0u, 0u};
       } else if (i == j) {  // T_jj = D_j
-        const float *d = &sA[(16 * drow(i) + 4 * g) * kStrideA4 + 16 * dcol(i) + r16];
-        Tc[i] = f32x4{d[0], d[kStrideA4], d[2 * kStrideA4], d[3 * kStrideA4]};
+        const float *d = &sA[ablk(i, i) + (4 * g) * 20 + r16];
+        Tc[i] = f32x4{d[0], d[20], d[40], d[60]};
         split4(Tc[i], Th[i], Tl[i]);
       } else {
         // Z = -sum_{j<=m<i} A_im T_mj, then T_ij = D_i Z
@@ -656,13 +653,12 @@ __device__ __forceinline__ void t_intra(
 #pragma unroll
         for (int m = 0; m < i; ++m) {
           if (m < j) continue;
-          const f32x4 la = *reinterpret_cast<const f32x4 *>(&sA[(16 * i + r16) * kStrideA4 + 16 * m + 4 * g]);
+          const f32x4 la = *reinterpret_cast<const f32x4 *>(&sA[ablk(i, m) + r16 * 20 + 4 * g]);
           u32x2 lh, ll;
           split4(-la, lh, ll);
           Z = mfma16_x3(lh, ll, Th[m], Tl[m], Z);
         }
-        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(
-            &sA[(16 * drow(i) + r16) * kStrideA4 + 16 * dcol(i) + 4 * g]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&sA[ablk(i, i) + r16 * 20 + 4 * g]);
         u32x2 dh, dl, zh, zl;
         split4(d4, dh, dl);
         split4(Z, zh, zl);
@@ -736,7 +732,7 @@ __device__ __forceinline__ void intra_wy_unit(
 }
 
 template <int FORM, bool SPLIT>
-__global__ __launch_bounds__(256) void prefill_intra_kernel(
+__device__ __forceinline__ void intra_body(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
@@ -760,6 +756,33 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
     intra_wy_unit<SPLIT>(smem, blockIdx.x, k, v, A_log, a, dt_bias, b, chunks, one, nt_max, H,
                          ws_G, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
   }
+}
+
+template <int FORM, bool SPLIT>
+__global__ __launch_bounds__(256) void prefill_intra_kernel(
+    const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+    const float *__restrict__ A_log, const uint16_t *__restrict__ a,
+    const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
+    const int4 *__restrict__ chunks, OneSeq one, int nt_max, Heads H,
+    const int *__restrict__ form_flag, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
+    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u,
+    uint16_t *__restrict__ ws_kt) {
+  intra_body<FORM, SPLIT>(k, v, A_log, a, dt_bias, b, chunks, one, nt_max, H, form_flag, ws_G,
+                          ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
+}
+// the form left to the device: held to five workgroups per CU, as each form
+// alone (the union of both paths needs a few more registers than either)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5)))
+void prefill_intra_either_kernel(
+    const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+    const float *__restrict__ A_log, const uint16_t *__restrict__ a,
+    const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
+    const int4 *__restrict__ chunks, OneSeq one, int nt_max, Heads H,
+    const int *__restrict__ form_flag, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
+    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u,
+    uint16_t *__restrict__ ws_kt) {
+  intra_body<-1, false>(k, v, A_log, a, dt_bias, b, chunks, one, nt_max, H, form_flag, ws_G,
+                        ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
 }
 
 // ---------------------------------------------------------------------------
@@ -1873,7 +1896,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     auto intra = P.intra_split ? prefill_intra_kernel<0, true>
                  : P.form == 0 ? prefill_intra_kernel<0, false>
                  : P.form == 1 ? prefill_intra_kernel<1, false>
-                               : prefill_intra_kernel<-1, false>;
+                               : prefill_intra_either_kernel;
     hipLaunchKernelGGL(intra, dim3(static_cast<unsigned>(P.intra_grid)), dim3(256), 0, stream, k,
                        v, A_log, a, dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE, wsw,
                        wsu, kt);
