@@ -1362,35 +1362,34 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// 3b. two-segment scan: the combination, and the output of the second
-// segment's chunks (one launch after the state kernel).  With S0 = sp.send
-// (the state at chunk nt0) and, for a chunk c >= nt0, M_c = sp.htm (the
-// linear part of the map over chunks nt0..c-1, bf16 [j][k]) and C_c = ht (its
-// offset, bf16 [v][k]), the chunk-start state is S_c = S0 M_c + C_c.
-//
+// 3b. two-segment scan: the output of the second segment's chunks (one launch
+// after the state kernel).  With S0 = sp.send (the state at chunk nt0) and,
+// for a chunk c >= nt0, M_c = sp.htm (the linear part of the map over chunks
+// nt0..c-1, bf16 [j][k]) and C_c = ht (its offset, bf16 [v][k]), the
+// chunk-start state is S_c = S0 M_c + C_c, and the second chain left
+// v_off = u - w C_c^T in vnt.  The output
+//   o = scale (E Q S_c^T + P v_new),  v_new = u - w S_c^T
+// (E = diag exp(G_i), P = mask_{j<=i} exp(G_i - G_j) q_i . k_j) is linear in
+// S_c, so it splits into the output of the offset chain and a correction
+// that never forms S_c:
+//   o = scale (E Q C_c^T + P v_off + R S0^T),  R = (E Q - P w) M_c^T
+//                                                = E (Q M_c^T) - P (w M_c^T).
 // Each workgroup produces the output of one chunk c >= nt0 and v-head h
 // (c = nt0 + id / H.v, h = id % H.v, so a head's workgroups share an XCD and
-// read S0 from its L2); wave w owns the columns v = 32 w .. 32 w + 31:
-//   S_c   = S0 M_c + C_c      S0 split into bf16 hi + lo, M_c bf16, in f32
-//   v_new = u - w S_c         w and S_c split: three products
-//   P     = mask_{j<=i}(exp(G_i - G_j) q_i . k_j)
-//   o     = scale (exp(G_i) q_i S_c + P v_new)
-// The state and v_new never leave the registers: a 16x16 result tile of
-// S_c^T (4 consecutive k per lane) and of v_new (4 consecutive tokens) is
-// the B operand of a 16x16x16 MFMA as it stands.  Up to the bf16 rounding of
-// M_c and C_c (a relative 2^-9 of S0 M_c and C_c, the order of the bf16 state
-// the output kernel uses) this is what the output kernel computes from the
-// single chain's ht and v_new.  new_state = S0 M + C (M = sp.mend, C =
+// read S0 from its L2).  Wave w owns the output columns v and the columns j
+// of R in 32 w .. 32 w + 31.  Operands in bf16 as in the output kernel (w and
+// S0 rounded once); results in f32.  new_state = S0 M + C (M = sp.mend, C =
 // sp.cend) is computed by extra workgroups of the output kernel's launch
 // (split_state_tile), which runs beside this one's in the same round.
 // ---------------------------------------------------------------------------
-constexpr int kSplitOutLds = 2 * kChunk * kStrideK * 2 + kDV * kStrideK * 2 + kChunk * kStrideT * 2 + kChunk * 4;
+constexpr int kSplitOutLds = 2 * kChunk * kStrideK * 2 + kChunk * kDK * 2 + kChunk * kStrideT * 2 + kChunk * 4;
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_split_out_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
                               OneSeq one, Heads H, SplitScan sp,
                               const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_w,
-                              const float *__restrict__ ws_u, const uint16_t *__restrict__ ws_ht,
-                              float scale, uint16_t *__restrict__ out) {
+                              const uint16_t *__restrict__ ws_ht,
+                              const uint16_t *__restrict__ ws_vnt, float scale,
+                              uint16_t *__restrict__ out) {
   __shared__ __align__(16) uint16_t smem[kSplitOutLds / 2];
   constexpr size_t kElems = static_cast<size_t>(kDV) * kDK;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1405,62 +1404,59 @@ void prefill_split_out_kernel(const uint16_t *__restrict__ q, const uint16_t *__
   const int hq = h / H.ratio;
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
   const int r16 = lane & 15, g = lane >> 4, kg = 8 * g, q4 = 4 * g;
-  uint16_t *const sQ = smem;                      // [64][kStrideK]; at the end o
-  uint16_t *const sK = sQ + kChunk * kStrideK;    // [64][kStrideK]
-  uint16_t *const sM = sK + kChunk * kStrideK;    // [128][kStrideK] M_c; then w's fragments
-  uint16_t *const sP = sM + kDV * kStrideK;       // [64][kStrideT]
+  uint16_t *const sQ = smem;                    // [64][kStrideK]: Q, then R, then o
+  uint16_t *const sK = sQ + kChunk * kStrideK;  // [64][kStrideK]
+  uint16_t *const sW = sK + kChunk * kStrideK;  // w's hi fragments [jb][kk][lane][8]
+  uint16_t *const sP = sW + kChunk * kDK;       // [64][kStrideT]
   float *const sG = reinterpret_cast<float *>(sP + kChunk * kStrideT);
   const float *const S0 = sp.send + static_cast<size_t>(h) * kElems;
   const uint16_t *const Mc = sp.htm + (static_cast<size_t>(c - sp.nt0) * H.v + h) * kElems;
   const uint16_t *const Cc = ws_ht + ch_head * kElems;
+  const uint16_t *const Vo = ws_vnt + ch_head * (kDV * kChunk);
+  const uint16_t *const wsrc = ws_w + ch_head * (kWBytes / 2);
 
-  // --- loads: q, K rows (zero past the chunk through the descriptors'
-  // range), M_c rows, G -> LDS; C_c at this lane's result positions of S_c^T
-  // (k = 16 mi + q4 .. +3, v = 32 wave + 16 vi + r16) and this wave's S0 rows.
+  // --- Every global load is issued here, so that one memory latency covers
+  // them all: Q and K rows (rows past the chunk read zero through the
+  // descriptors' range), G and the hi halves of w's stored fragments
+  // [jb][kk][lane][hi 8 | lo 8] (A operands of w M^T, all 64 rows) -> LDS;
+  // the S0 rows of this wave's columns n = 32 wave + 16 nt + r16 (B operands
+  // of R S0^T) into registers.
+  const uint32_t rstride = static_cast<uint32_t>(H.qk) * (kDK * 2);
+  const size_t qk0 = (static_cast<size_t>(start) * H.qk + hq) * kDK;
   {
-    const uint32_t rstride = static_cast<uint32_t>(H.qk) * (kDK * 2);
-    const size_t qk0 = (static_cast<size_t>(start) * H.qk + hq) * kDK;
     const auto rq = buf_rsrc(q + qk0, static_cast<uint32_t>(len) * rstride);
     const auto rk = buf_rsrc(k + qk0, static_cast<uint32_t>(len) * rstride);
-    u32x4 qv[4], kv[4], mrow[8];
+    u32x4 qv[4], kv[4], wv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int idx = tid + 256 * i;
       const uint32_t off = static_cast<uint32_t>(idx >> 4) * rstride + (idx & 15) * 16;
       qv[i] = buf_load16(rq, off);
       kv[i] = buf_load16(rk, off);
+      wv[i] = *reinterpret_cast<const u32x4 *>(wsrc + idx * 16);
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      mrow[i] = *reinterpret_cast<const u32x4 *>(Mc + (tid / 16 + 16 * i) * kDK + 8 * (tid % 16));
     if (tid < kChunk) sG[tid] = ws_G[ch_head * kChunk + tid];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int idx = tid + 256 * i;
       *reinterpret_cast<u32x4 *>(&sQ[(idx >> 4) * kStrideK + (idx & 15) * 8]) = qv[i];
       *reinterpret_cast<u32x4 *>(&sK[(idx >> 4) * kStrideK + (idx & 15) * 8]) = kv[i];
+      *reinterpret_cast<u32x4 *>(&sW[idx * 8]) = wv[i];
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<u32x4 *>(&sM[(tid / 16 + 16 * i) * kStrideK + 8 * (tid % 16)]) = mrow[i];
   }
-  u32x2 cc[2][8];
   f32x4 s0r[2][4][2];
 #pragma unroll
-  for (int vi = 0; vi < 2; ++vi) {
-    const int v = 32 * wave + 16 * vi + r16;
-#pragma unroll
-    for (int mi = 0; mi < 8; ++mi)
-      cc[vi][mi] = *reinterpret_cast<const u32x2 *>(Cc + v * kDK + 16 * mi + q4);
+  for (int nt = 0; nt < 2; ++nt) {
+    const int n = 32 * wave + 16 * nt + r16;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      s0r[vi][kk][0] = *reinterpret_cast<const f32x4 *>(S0 + v * kDK + 32 * kk + kg);
-      s0r[vi][kk][1] = *reinterpret_cast<const f32x4 *>(S0 + v * kDK + 32 * kk + kg + 4);
+      s0r[nt][kk][0] = *reinterpret_cast<const f32x4 *>(S0 + n * kDK + 32 * kk + kg);
+      s0r[nt][kk][1] = *reinterpret_cast<const f32x4 *>(S0 + n * kDK + 32 * kk + kg + 4);
     }
   }
   __syncthreads();
 
-  // --- P rows 16 wave .. +15 (as the output kernel).
+  // --- P rows 16 wave .. +15 -> LDS (as the output kernel).
   {
     const int mb = wave;
 #pragma unroll
@@ -1482,133 +1478,133 @@ void prefill_split_out_kernel(const uint16_t *__restrict__ q, const uint16_t *__
       }
     }
   }
-
-  // --- S_c^T[k][v] = sum_j M_c[j][k] S0[v][j] + C_c: A = M_c^T rows k
-  // (transposed LDS reads), B = S0 rows split; kept as split K=16 B operands.
-  u32x2 Sh[8][2], Sl[8][2];
+  // S0 as bf16 B operands; then the B operands of this wave's columns: C_c
+  // rows (E Q C^T), M_c rows (Q M^T, w M^T) and v_off rows (P v_off), loaded
+  // before the barrier so that their latency overlaps it.
+  u32x4 sb[2][4];
 #pragma unroll
-  for (int vi = 0; vi < 2; ++vi) {
-    u32x4 bh[4], bl[4];
+  for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const f32x4 x0 = s0r[vi][kk][0], x1 = s0r[vi][kk][1];
-      const float xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-      split8(xs, bh[kk], bl[kk]);
+      const f32x4 x0 = s0r[nt][kk][0], x1 = s0r[nt][kk][1];
+      sb[nt][kk] = u32x4{pk_bf16(x0[0], x0[1]), pk_bf16(x0[2], x0[3]), pk_bf16(x1[0], x1[1]),
+                         pk_bf16(x1[2], x1[3])};
+    }
+  u32x4 cb[2][4], mb4[2][4], vb[2][2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int n = 32 * wave + 16 * nt + r16;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      cb[nt][kk] = *reinterpret_cast<const u32x4 *>(Cc + n * kDK + 32 * kk + kg);
+      mb4[nt][kk] = *reinterpret_cast<const u32x4 *>(Mc + n * kDK + 32 * kk + kg);
     }
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi) {
-      u32x4 am[4];
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const u32x2 x = ds_read_tr16(&sM[(32 * kk + kg + 4 * hh + (r16 >> 2)) * kStrideK +
-                                           16 * mi + 4 * (r16 & 3)]);
-          am[kk][2 * hh] = x[0];
-          am[kk][2 * hh + 1] = x[1];
-        }
-      f32x4 a = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        a = mfma_bf16(am[kk], bh[kk], a);
-        a = mfma_bf16(am[kk], bl[kk], a);
-      }
-      const f32x4 sc = {a[0] + __uint_as_float(cc[vi][mi][0] << 16),
-                        a[1] + __uint_as_float(cc[vi][mi][0] & 0xffff0000u),
-                        a[2] + __uint_as_float(cc[vi][mi][1] << 16),
-                        a[3] + __uint_as_float(cc[vi][mi][1] & 0xffff0000u)};
-      split4(sc, Sh[mi][vi], Sl[mi][vi]);
-    }
+    for (int kk = 0; kk < 2; ++kk) vb[nt][kk] = *reinterpret_cast<const u32x4 *>(Vo + n * kChunk + 32 * kk + kg);
   }
-  // w's fragments (32 KB, the state kernel's A-operand order) into M_c's space.
-  u32x4 wraw[8];
-  {
-    const uint16_t *wsrc = ws_w + ch_head * (kWBytes / 2);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) wraw[i] = *reinterpret_cast<const u32x4 *>(wsrc + (tid + 256 * i) * 8);
-  }
-  __syncthreads();  // every wave is done with M_c and P is complete
-#pragma unroll
-  for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4 *>(&sM[(tid + 256 * i) * 8]) = wraw[i];
-  f32x4 uf[4][2];
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-    for (int vi = 0; vi < 2; ++vi)
-      uf[tb][vi] = *reinterpret_cast<const f32x4 *>(
-          ws_u + ch_head * (kChunk * kDV) + ((tb * 8 + 2 * wave + vi) * 64 + lane) * 4);
   __syncthreads();
 
-  // --- v_new[t][v] = u - sum_k w[t][k] S_c[v][k] for all 64 tokens t (tiles
-  // tb) and this wave's columns; K=16 A fragments of w (4 consecutive k) are
-  // halves of the stored K=32 fragments: (tb, mi, lane) reads record
-  // (tb, mi / 2, lane 16 (2 (mi & 1) + (g >> 1)) + r16), elements 4 (g & 1)..+3.
-  u32x2 vb[4][2];  // v_new as bf16 B operands of P v_new
+  // --- O = E Q C^T + P v_off, then Y = E Q M^T (rows: all 64 tokens; two
+  // passes over the Q tile keep fewer operands live).
+  f32x4 O[4][2], Y[4][2];
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    f32x4 P0[2], P1[2], P2[2];
+  for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
-    for (int vi = 0; vi < 2; ++vi) P0[vi] = P1[vi] = P2[vi] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < 2; ++nt) O[mb][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi) {
-      const int rec = (tb * 4 + (mi >> 1)) * 64 + 16 * (2 * (mi & 1) + (g >> 1)) + r16;
-      const u32x2 wh = *reinterpret_cast<const u32x2 *>(&sM[rec * 16 + 4 * (g & 1)]);
-      const u32x2 wl = *reinterpret_cast<const u32x2 *>(&sM[rec * 16 + 8 + 4 * (g & 1)]);
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 qa = *reinterpret_cast<const u32x4 *>(&sQ[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
 #pragma unroll
-      for (int vi = 0; vi < 2; ++vi) {
-        P0[vi] = mfma16_bf16(wh, Sh[mi][vi], P0[vi]);
-        P1[vi] = mfma16_bf16(wh, Sl[mi][vi], P1[vi]);
-        P2[vi] = mfma16_bf16(wl, Sh[mi][vi], P2[vi]);
-      }
+      for (int nt = 0; nt < 2; ++nt) O[mb][nt] = mfma_bf16(qa, cb[nt][kk], O[mb][nt]);
     }
 #pragma unroll
-    for (int vi = 0; vi < 2; ++vi) {
-      float vn[4];
+    for (int r = 0; r < 4; ++r) {
+      const float e = expf(sG[16 * mb + q4 + r]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) vn[r] = uf[tb][vi][r] - ((P0[vi][r] + P1[vi][r]) + P2[vi][r]);
-      vb[tb][vi] = u32x2{pk_bf16(vn[0], vn[1]), pk_bf16(vn[2], vn[3])};
+      for (int nt = 0; nt < 2; ++nt) O[mb][nt][r] *= e;
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const u32x4 pa = *reinterpret_cast<const u32x4 *>(&sP[(16 * mb + r16) * kStrideT + 32 * kk + kg]);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) O[mb][nt] = mfma_bf16(pa, vb[nt][kk], O[mb][nt]);
+    }
+  }
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) Y[mb][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 qa = *reinterpret_cast<const u32x4 *>(&sQ[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) Y[mb][nt] = mfma_bf16(qa, mb4[nt][kk], Y[mb][nt]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float e = expf(sG[16 * mb + q4 + r]);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) Y[mb][nt][r] *= e;
     }
   }
 
-  // --- O = exp(G_t) q S_c^T + P v_new for all 64 tokens, this wave's columns.
-  f32x4 O[4][2];
+  // --- Z = w M^T (rows: all 64 tokens j; A = the hi halves of w's stored
+  // fragments [jb][kk][lane][hi 8 | lo 8]), then R = Y - P Z: Z's 16x16
+  // result tiles (4 consecutive j per lane) are the B operands of 16x16x16
+  // MFMAs as they stand.
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
+  for (int jb = 0; jb < 4; ++jb) {
+    f32x4 Z[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int vi = 0; vi < 2; ++vi) O[tb][vi] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 wa = *reinterpret_cast<const u32x4 *>(&sW[((jb * 4 + kk) * 64 + lane) * 8]);
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi) {
-      const u32x2 qa = *reinterpret_cast<const u32x2 *>(&sQ[(16 * tb + r16) * kStrideK + 16 * mi + q4]);
+      for (int nt = 0; nt < 2; ++nt) Z[nt] = mfma_bf16(wa, mb4[nt][kk], Z[nt]);
+    }
 #pragma unroll
-      for (int vi = 0; vi < 2; ++vi) {
-        O[tb][vi] = mfma16_bf16(qa, Sh[mi][vi], O[tb][vi]);
-        O[tb][vi] = mfma16_bf16(qa, Sl[mi][vi], O[tb][vi]);
+    for (int nt = 0; nt < 2; ++nt) {
+      const u32x2 zb = {pk_bf16(Z[nt][0], Z[nt][1]), pk_bf16(Z[nt][2], Z[nt][3])};
+      // rows i of blocks mb >= jb see the columns j of block jb
+#pragma unroll
+      for (int mb = jb; mb < 4; ++mb) {
+        const u32x2 pa = *reinterpret_cast<const u32x2 *>(&sP[(16 * mb + r16) * kStrideT + 16 * jb + q4]);
+        f32x4 pz = mfma16_bf16(pa, zb, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Y[mb][nt][r] -= pz[r];
       }
     }
-    float eg[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) eg[r] = expf(sG[16 * tb + q4 + r]);
-#pragma unroll
-    for (int vi = 0; vi < 2; ++vi)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) O[tb][vi][r] *= eg[r];
-#pragma unroll
-    for (int jt = 0; jt <= tb; ++jt) {
-      const u32x2 pa = *reinterpret_cast<const u32x2 *>(&sP[(16 * tb + r16) * kStrideT + 16 * jt + q4]);
-#pragma unroll
-      for (int vi = 0; vi < 2; ++vi) O[tb][vi] = mfma16_bf16(pa, vb[jt][vi], O[tb][vi]);
-    }
   }
-  __syncthreads();  // every wave is done with the Q tile: o takes its place
+  __syncthreads();  // every wave is done with the Q tile: R takes its place
 
-  uint16_t *sO = sQ;  // [64][kStrideK]
+  uint16_t *const sR = sQ;  // [64][kStrideK]: R[i][j]
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb)
+  for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-    for (int vi = 0; vi < 2; ++vi)
+    for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        sO[(16 * tb + q4 + r) * kStrideK + 32 * wave + 16 * vi + r16] = f32_to_bf16(scale * O[tb][vi][r]);
+        sR[(16 * mb + q4 + r) * kStrideK + 32 * wave + 16 * nt + r16] = f32_to_bf16(Y[mb][nt][r]);
+  __syncthreads();
+
+  // --- O += R S0^T.
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 ra = *reinterpret_cast<const u32x4 *>(&sR[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) O[mb][nt] = mfma_bf16(ra, sb[nt][kk], O[mb][nt]);
+    }
+  __syncthreads();  // every wave is done with R: o takes its place
+
+  uint16_t *const sO = sQ;  // [64][kStrideK]
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sO[(16 * mb + q4 + r) * kStrideK + 32 * wave + 16 * nt + r16] = f32_to_bf16(scale * O[mb][nt][r]);
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -1917,7 +1913,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   if (P.split_grid > 0) {
     // new_state and the output of the second segment's chunks
     hipLaunchKernelGGL(prefill_split_out_kernel, dim3(static_cast<unsigned>(P.split_grid)),
-                       dim3(256), 0, stream, q, k, one, H, sp, wsG, wsw, wsu, ht, scale, output);
+                       dim3(256), 0, stream, q, k, one, H, sp, wsG, wsw, ht, vnt, scale, output);
     if ((rc = check_launch(what))) return rc;
   }
   if (P.out_grid > 0) {
