@@ -217,7 +217,13 @@ int plan_prefill(int T, int N, const Heads &H, const PrefillLayout &L, int varia
       if (P.seq_variant < 0 && by_block < by_token) P.seq_variant = block_variant;
       const bool blocks = P.seq_variant == block_variant;
       const float seq_lo = blocks ? by_block : by_token;
-      if (seq_lo <= cost_by_chunks(fT, static_cast<float>(L.nt_max), fhv, g)) P.choose = blocks ? 3 : 2;
+      // The sequential path's best case against the chunks is N equal
+      // sequences of the mean length (its cost grows with the longest
+      // sequence ~10x faster than the chunks'): the device gets the choice
+      // only if the sequential path wins there by more than the choice costs.
+      const float fN = static_cast<float>(N);
+      const float chunks_eq = cost_by_chunks(mean, fN * ceilf(mean / kChunk), fhv, fN);
+      if (seq_lo + kDeviceChoiceCost < chunks_eq) P.choose = blocks ? 3 : 2;
     }
   }
   if (P.sequential) return GDN_OK;
@@ -226,15 +232,16 @@ int plan_prefill(int T, int N, const Heads &H, const PrefillLayout &L, int varia
   // [cu[0], cu[1]) themselves and compute its chunks.
   P.single = N == 1 && P.choose == 0;
   // Form of the per-chunk operands: `variant` when 0 (WY) or 1 (T); else the
-  // index kernel's rule (T iff at least 128 chunks and three times the
-  // longest sequence's), settled here when (T, N) alone exclude the T form --
-  // one or two sequences, fewer than 128 chunks, or fewer than three times
-  // the chunks of the mean length, a lower bound on the longest -- so that
-  // only one intra kernel is launched.
+  // index kernel's rule (t_form_wins), settled here when (T, N) alone exclude
+  // the T form -- the rule fails at the largest chunk count possible (nt_max)
+  // and the chunks of the mean length, a lower bound on the longest
+  // sequence's (the rule only turns true as chunks grow or the longest
+  // shrinks) -- so that only one intra kernel is launched.
   P.form = variant >= 2 ? 0 : variant;
   if (P.form < 0) {
     const long long mean_chunks = ((static_cast<long long>(T) + N - 1) / N + kChunk - 1) / kChunk;
-    const bool t_possible = !P.single && N > 2 && L.nt_max >= 128 && L.nt_max >= 3 * mean_chunks;
+    const bool t_possible =
+        !P.single && t_form_wins(static_cast<float>(L.nt_max), static_cast<float>(mean_chunks));
     P.form = t_possible ? -1 : 0;
   }
   const long long grid = chunk_head_grid(L.nt_max, H);

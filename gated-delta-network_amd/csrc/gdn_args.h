@@ -96,10 +96,10 @@ int check_prefill_args(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v, 
 // candidate is the block kernel (gdn_block.hip) or the token-by-token kernel,
 // whichever the cost models rate faster at the mean length, and the device
 // compares its cost model with the chunks' at the batch's longest sequence
-// (index kernel) -- unless the host already knows the chunks win: the
-// candidate's cost at the mean length (a lower bound on the longest) exceeds
-// the chunks' at the largest longest sequence (T) and chunk count (nt_max)
-// possible.
+// and chunk count (index kernel) -- unless the host already knows the chunks
+// win: at N equal sequences of the mean length, the candidate's best case,
+// it does not beat the chunks by more than a device-side choice costs
+// (kDeviceChoiceCost).
 constexpr int kRecurrentMaxLen = 96;
 
 // Two-segment scan of one sequence (state kernel, SplitScan): three groups of

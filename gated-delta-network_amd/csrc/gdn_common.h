@@ -23,7 +23,7 @@ struct Heads {
 };
 
 // Path cost models in microseconds, fitted to graph-replay sweeps of each
-// path on MI355X (sequence count N = 1..256 of equal lengths L = 8..256,
+// path on MI355X (sequence count N = 1..256 of equal lengths L = 8..16384,
 // multi-token decode B = 1..128 with 4..16 tokens).  L = longest sequence,
 // T = tokens, nt = chunks of 64, g = N * hv (sequence, v-head) groups.
 // Token by token (recurrent kernel): the serial token chain plus VALU work
@@ -40,12 +40,43 @@ __host__ __device__ inline float cost_by_block(float L, float g) {
   const float per_block = g <= 128.0f ? 2.8f : g <= 256.0f ? 3.5f : 4.7f;
   return 4.5f + 0.015f * g + 0.008f * fmaxf(g - 256.0f, 0.0f) + rounds * blocks * per_block;
 }
-// Chunks: fixed launches, per-sequence work up to ~40 sequences and the
-// per-chunk throughput beyond, plus the serial chunk chain of the longest.
-__host__ __device__ inline float cost_by_chunks(float L, float nt, float hv, float g) {
-  const float per_seq = fminf(0.13f * g, 11.0f + 0.081f * g);
-  return 20.0f + fmaxf(per_seq, 0.081f * nt * hv) + 0.5f * ceilf(L / 64.0f);
+// Operand form of the chunks (WY or T) for a batch of nt chunks whose
+// longest sequence has lc chunks, from graph-replay sweeps of both forms on
+// MI355X (N = 1..64 equal sequences of 128..16384 tokens; 0.3 % above the
+// faster form over the sweep): the T form from 192 chunks on when the batch
+// holds more than three times the longest sequence's chunks, or from 384 on
+// with at least twice (the WY form's workspace, ~1 MB per chunk, then no
+// longer stays in the memory-side cache); else the WY form, and always for
+// one sequence (nt == lc).
+__host__ __device__ inline bool t_form_wins(float nt, float lc) {
+  return nt >= 192.0f && (nt > 3.0f * lc || (nt >= 384.0f && nt >= 2.0f * lc));
 }
+// Chunks in one form (t: T, else WY) for N > 1 sequences, fitted to the same
+// sweeps (rms 4-5 %): fixed launches, the intra and output kernels' work per
+// chunk and v-head, and the state recurrence -- the longest sequence's chain
+// of lc steps, or the batch's nt * hv * 8 unit-steps over the 512 resident
+// state workgroups, whichever is longer; a step takes longer once some CU
+// holds two state workgroups (more than 256 units of N * hv * 8).
+__host__ __device__ inline float cost_by_chunks_form(float L, float nt, float hv, float N, bool t) {
+  const float lc = ceilf(L / 64.0f), units = N * hv * 8.0f;
+  const float steps = fmaxf(lc, nt * hv / 64.0f);
+  if (t) return 10.6f + 0.039f * nt * hv + (units <= 256.0f ? 1.09f : 1.85f) * steps;
+  return 24.6f + 0.033f * nt * hv + (units <= 256.0f ? 0.81f : 1.80f) * steps;
+}
+// Chunks in the form t_form_wins picks.
+__host__ __device__ inline float cost_by_chunks(float L, float nt, float hv, float N) {
+  return cost_by_chunks_form(L, nt, hv, N, t_form_wins(nt, ceilf(L / 64.0f)));
+}
+
+// What a path choice made on the device costs (graph replay, MI355X): the
+// index kernel and the chunk kernels returning at once when the sequential
+// path wins (~9 us over the sequential kernel alone), the sequential kernel
+// returning at once when the chunks win (~5 us).  The device prefers the
+// sequential path only by more than the difference of the two; the host
+// leaves the choice to the device only when the sequential path can win by
+// more than the whole.
+constexpr float kDeviceChoiceCost = 9.0f;
+constexpr float kSeqChoiceMargin = 4.0f;
 
 // First chunk of the second segment of a two-segment scan over nt chunks.
 __host__ __device__ inline int split_first(int nt) { return (nt + 1) / 2; }

@@ -38,9 +38,10 @@
 //            e^G K S): a third exchange per step, but a quarter of the
 //            intra kernel's HBM traffic and fewer bytes per step -- best
 //            when many sequences keep every CU and the memory system busy.
-// Rule (index kernel, from sweeps of both on MI355X): the T form when the
-// batch has at least 128 chunks and at least three times the chunks of its
-// longest sequence.  One sequence always takes the WY form.
+// Rule (index kernel, t_form_wins in gdn_common.h, from sweeps of both on
+// MI355X): the T form from 192 chunks on when the batch holds more than three
+// times the chunks of its longest sequence, or from 384 on with at least
+// twice.  One sequence always takes the WY form.
 //
 // Precision.  The state recurrence must hold 1e-3 of max|S| after 128-512
 // chunks.  Rounding any operand of w S or K^T v_new (or u, w themselves) to
@@ -130,7 +131,9 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
     const float g = static_cast<float>(N) * fhv;
     const float by_seq = choose == 2 ? cost_by_token(L, static_cast<float>(T), fhv, g)
                                      : cost_by_block(L, g);
-    sequential = by_seq <= cost_by_chunks(L, static_cast<float>(s_chunks), fhv, g);
+    const float fnt = static_cast<float>(s_chunks);
+    const bool t = form == 1 || (form != 0 && t_form_wins(fnt, ceilf(L / kChunk)));
+    sequential = by_seq + kSeqChoiceMargin <= cost_by_chunks_form(L, fnt, fhv, static_cast<float>(N), t);
   }
   if (tid == 0) offsets[N + 1] = sequential ? 1 : 0;
   long long carry = 0;
@@ -189,7 +192,9 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
   const int nt = static_cast<int>(carry < nt_max ? carry : nt_max);
   if (tid == 0) {
     offsets[N] = nt;
-    offsets[N + 2] = (form == 0 || form == 1) ? form : (nt >= 128 && nt >= 3 * s_most_chunks ? 1 : 0);
+    offsets[N + 2] = (form == 0 || form == 1)
+                         ? form
+                         : (t_form_wins(static_cast<float>(nt), static_cast<float>(s_most_chunks)) ? 1 : 0);
   }
   for (int c = nt + tid; c < nt_max; c += 1024) chunks[c] = make_int4(-1, 0, 0, 0);
 }

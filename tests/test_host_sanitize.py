@@ -182,7 +182,9 @@ def test_plan_sweep(driver):
     p = plans[(8192, 1, 4, 8, 2, -1, -1)]
     assert p["nt0"] == 0 and p["state"] == 64
     p = plans[(32768, 2, 4, 8) + base]
-    assert (p["single"], p["form"], p["choose"]) == (0, 0, 0)
+    assert (p["single"], p["form"], p["choose"]) == (0, -1, 0)  # two 16384s: the T form
+    p = plans[(8192, 2, 4, 8) + base]
+    assert (p["single"], p["form"], p["choose"]) == (0, 0, 0)  # at most 129 chunks: WY
     p = plans[(32768, 64, 4, 8) + base]
     assert p["form"] == -1  # T form possible: left to the index kernel
     assert plans[(INT_MAX, 1, 4, 8) + base]["rc"] == _lib.GDN_OK  # 2^25 chunks still launch

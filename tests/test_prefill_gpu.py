@@ -161,11 +161,12 @@ FORMS = {"wy": 0, "t": 1}
 
 def form_rule(lens):
     """Restatement of the built-in form choice of gdn_prefill.hip (index
-    kernel): the T form for a batch of several sequences with at least 128
-    chunks and at least three times the chunks of the longest one."""
+    kernel, t_form_wins in gdn_common.h): the T form from 192 chunks on for a
+    batch holding more than three times the chunks of its longest sequence,
+    or from 384 on with at least twice."""
     chunks = [-(-L // 64) for L in lens]
     nt, longest = sum(chunks), max(chunks)
-    return 1 if len(lens) > 1 and nt >= 128 and nt >= 3 * longest else 0
+    return 1 if nt >= 192 and (nt > 3 * longest or (nt >= 384 and nt >= 2 * longest)) else 0
 
 
 @pytest.mark.parametrize("form", list(FORMS))
@@ -186,7 +187,8 @@ def test_prefill_forms_reference_and_edge_cases(cuda_device, form):
 
 
 @pytest.mark.parametrize("lens", [[512] * 16, [1024] * 8, [2048] * 4, [4096] * 2, [8192, 1024, 512, 100],
-                                  [6, 49, 294, 1800, 2040, 61], [64] * 130])
+                                  [6, 49, 294, 1800, 2040, 61], [64] * 130, [512] * 32, [2048] * 8,
+                                  [4096, 4096, 4096], [64] * 200, [8192, 64, 4096]])
 def test_prefill_built_in_form_choice(cuda_device, lens):
     # The built-in choice is bit-identical to the form the rule names, and
     # the flag the index kernel leaves in the workspace is that form.

@@ -119,8 +119,20 @@ def _cost_by_block(L, g):
             + math.ceil(g / 512) * math.ceil(L / 16) * per_block)
 
 
-def _cost_by_chunks(L, nt, hv, g):
-    return 20 + max(min(0.13 * g, 11 + 0.081 * g), 0.081 * nt * hv) + 0.5 * math.ceil(L / 64)
+def _t_form_wins(nt, lc):
+    return nt >= 192 and (nt > 3 * lc or (nt >= 384 and nt >= 2 * lc))
+
+
+def _cost_by_chunks_form(L, nt, hv, N, t):
+    lc, units = math.ceil(L / 64), N * hv * 8
+    steps = max(lc, nt * hv / 64)
+    if t:
+        return 10.6 + 0.039 * nt * hv + (1.09 if units <= 256 else 1.85) * steps
+    return 24.6 + 0.033 * nt * hv + (0.81 if units <= 256 else 1.80) * steps
+
+
+def _cost_by_chunks(L, nt, hv, N):
+    return _cost_by_chunks_form(L, nt, hv, N, _t_form_wins(nt, math.ceil(L / 64)))
 
 
 def _expected_path(lens, hv=8):
@@ -136,11 +148,11 @@ def _expected_path(lens, hv=8):
     g, mean = N * hv, math.ceil(T / N)
     by_token, by_block = _cost_by_token(mean, T, hv, g), _cost_by_block(mean, g)
     kind = "block" if by_block < by_token else "token"
-    if min(by_token, by_block) > _cost_by_chunks(T, O.max_chunks(T, N), hv, g):
-        return "chunks"
+    if min(by_token, by_block) + 9 >= _cost_by_chunks(mean, N * math.ceil(mean / 64), hv, N):
+        return "chunks"  # decided on the host
     nt = sum(math.ceil(n / 64) for n in lens)
     seq = _cost_by_block(L, g) if kind == "block" else _cost_by_token(L, T, hv, g)
-    return kind if seq <= _cost_by_chunks(L, nt, hv, g) else "chunks"
+    return kind if seq + 4 <= _cost_by_chunks(L, nt, hv, N) else "chunks"
 
 
 def _expected_multi_kind(B, T, hv=8):
@@ -163,8 +175,9 @@ def _lens_1500():
     return lens
 
 
-# Batches the host leaves to the device (T > 96, N > 1), with the path the
-# cost models pick: token by token, 16-token blocks or chunks.
+# Batches of T > 96 tokens in N > 1 sequences (the host settles the clear
+# cases, the device the rest), with the path the cost models pick: token by
+# token, 16-token blocks or chunks.
 DEVICE_CHOICE = {
     "256x1": ([1] * 256, "token"),
     "64x16": ([16] * 64, "block"),
