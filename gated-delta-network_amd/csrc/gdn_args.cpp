@@ -250,6 +250,8 @@ int plan_prefill(int T, int N, const Heads &H, const PrefillLayout &L, int varia
   P.intra_split = P.form == 0 && 2 * P.intra_grid <= static_cast<long long>(kNumCus) * kIntraSplitPerCu;
   if (P.intra_split) P.intra_grid *= 2;
   P.loop = P.choose != 0;
+  P.self_index = !P.single && N <= kSelfIndexMax && P.intra_grid > 0 &&
+                 P.intra_grid <= kSelfIndexMaxGrid;
   auto cap = [&P](long long units, int per_cu) {
     const long long most = static_cast<long long>(kNumCus) * per_cu;
     return P.loop && units > most ? most : units;

@@ -136,6 +136,9 @@ struct PrefillPlan {
   bool intra_split; // WY intra kernel as two workgroups per (chunk, v-head)
   bool loop;        // the state kernel loops over its units in a capped grid
                     // (when the device makes the path choice, choose != 0)
+  bool self_index;  // no index launch: the intra kernel builds the chunk table
+                    // (2..kSelfIndexMax sequences, an intra grid of 1..
+                    // kSelfIndexMaxGrid workgroups), launched first
   // launch grids (workgroups, capped at the resident ones; the kernels loop
   // over the remaining units); 0 = not launched
   long long intra_grid, state_grid, split_grid, out_grid;

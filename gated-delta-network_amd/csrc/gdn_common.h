@@ -78,6 +78,16 @@ __host__ __device__ inline float cost_by_chunks(float L, float nt, float hv, flo
 constexpr float kDeviceChoiceCost = 9.0f;
 constexpr float kSeqChoiceMargin = 4.0f;
 
+// Batches of at most kSelfIndexMax sequences whose intra launch is at most
+// kSelfIndexMaxGrid workgroups (two rounds at five per CU) are indexed by
+// the intra kernel itself (one sequence per thread of its 256), without the
+// index launch (~4.7 us): each of its workgroups then scans cu_seqlens
+// before its chunk, ~2 us per round of workgroups (8x2048, 2104 workgroups:
+// 144.1 -> 139.5 us per call; 4x8192, 4128: intra 37.1 -> 44.9 us for 4.9 us
+// of index kernel saved, so it keeps the index kernel).
+constexpr int kSelfIndexMax = 256;
+constexpr long long kSelfIndexMaxGrid = 2560;
+
 // First chunk of the second segment of a two-segment scan over nt chunks.
 __host__ __device__ inline int split_first(int nt) { return (nt + 1) / 2; }
 

@@ -101,6 +101,23 @@ __device__ __forceinline__ void block_sum_into(int x, int *dst) {
   if ((threadIdx.x & 63) == 0) atomicAdd(dst, x);
 }
 
+// The path the device picks (choose != 0, set on the host): sequential (true)
+// or chunks, from the batch's longest sequence and chunk count (the form the
+// chunks would take: `form` 0 / 1 as set, else t_form_wins).
+__device__ __forceinline__ bool device_picks_sequential(int choose, int rec_max, int longest,
+                                                        int chunks, int N, int T, int hv,
+                                                        int form) {
+  if (choose == 1) return longest <= rec_max;
+  if (choose < 2) return false;
+  const float L = static_cast<float>(longest), fhv = static_cast<float>(hv);
+  const float g = static_cast<float>(N) * fhv;
+  const float by_seq = choose == 2 ? cost_by_token(L, static_cast<float>(T), fhv, g)
+                                   : cost_by_block(L, g);
+  const float fnt = static_cast<float>(chunks);
+  const bool t = form == 1 || (form != 0 && t_form_wins(fnt, ceilf(L / kChunk)));
+  return by_seq + kSeqChoiceMargin <= cost_by_chunks_form(L, fnt, fhv, static_cast<float>(N), t);
+}
+
 __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int cu64, int N, int T,
                                                               int nt_max, int choose, int rec_max,
                                                               int hv, int form, int4 *chunks,
@@ -123,18 +140,8 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
     block_sum_into(nch, &s_chunks);
   }
   __syncthreads();
-  bool sequential = false;
-  if (choose == 1) {
-    sequential = s_longest <= rec_max;
-  } else if (choose >= 2) {
-    const float L = static_cast<float>(s_longest), fhv = static_cast<float>(hv);
-    const float g = static_cast<float>(N) * fhv;
-    const float by_seq = choose == 2 ? cost_by_token(L, static_cast<float>(T), fhv, g)
-                                     : cost_by_block(L, g);
-    const float fnt = static_cast<float>(s_chunks);
-    const bool t = form == 1 || (form != 0 && t_form_wins(fnt, ceilf(L / kChunk)));
-    sequential = by_seq + kSeqChoiceMargin <= cost_by_chunks_form(L, fnt, fhv, static_cast<float>(N), t);
-  }
+  const bool sequential =
+      device_picks_sequential(choose, rec_max, s_longest, s_chunks, N, T, hv, form);
   if (tid == 0) offsets[N + 1] = sequential ? 1 : 0;
   long long carry = 0;
   int most_chunks = 0;
@@ -213,6 +220,100 @@ __device__ __forceinline__ int4 chunk_info(const int4 *chunks, int c, const OneS
   const int4 e = chunks[c];
   return make_int4(__builtin_amdgcn_readfirstlane(e.x), __builtin_amdgcn_readfirstlane(e.y),
                    __builtin_amdgcn_readfirstlane(e.z), __builtin_amdgcn_readfirstlane(e.w));
+}
+
+// ---------------------------------------------------------------------------
+// 1b. the chunk table built inside the intra kernel (several sequences, at
+// most kSelfIndexMax, and an intra grid of at most kSelfIndexMaxGrid
+// workgroups; gdn_common.h): each workgroup scans cu_seqlens itself -- one
+// sequence per thread, a prefix sum of the chunk counts in LDS -- and finds
+// its own chunk by binary search; workgroup 0 writes offsets, the chunk
+// count and the flags, and the workgroup of v-head 0 of each chunk slot its
+// chunk-table entry, for the state and output kernels.  A batch then needs no
+// index launch (~4.7 us): the intra kernel is the first launch, the path the
+// device picks included (the sequential kernel runs after it and reads the
+// flag).  Same results as the index kernel, entry by entry.
+// ---------------------------------------------------------------------------
+struct SelfIndex {
+  const void *cu;  // nullptr: the index kernel built the table
+  int cu64, N, T, choose, rec_max, form;
+  int4 *chunks;
+  int *offsets;
+};
+constexpr int kSelfIndexLds = 3 * kSelfIndexMax * 4 + 16 * 4;
+
+struct SelfIndexed {
+  int nt, form;
+};
+
+__device__ __forceinline__ SelfIndexed self_index(char *smem, const SelfIndex &si, int nt_max,
+                                                  int hv) {
+  int *const s_incl = reinterpret_cast<int *>(smem);
+  int *const s_bos = s_incl + kSelfIndexMax;
+  int *const s_eos = s_bos + kSelfIndexMax;
+  int *const s_red = s_eos + kSelfIndexMax;  // longest, most chunks, wave totals [4..7]
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int N = si.N, T = si.T;
+  int n = 0, len = 0;
+  if (tid < 2) s_red[tid] = 0;
+  if (tid < N) {
+    const int bos = load_cu(si.cu, si.cu64, tid, T);
+    int eos = load_cu(si.cu, si.cu64, tid + 1, T);
+    eos = eos < bos ? bos : eos;
+    len = eos - bos;
+    n = (len + kChunk - 1) / kChunk;
+    s_bos[tid] = bos;
+    s_eos[tid] = eos;
+  }
+  int incl = n;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63) s_red[4 + wv] = incl;
+  __syncthreads();
+  for (int w = 0; w < wv; ++w) incl += s_red[4 + w];
+  s_incl[tid] = incl;
+  block_max_into(len, &s_red[0]);
+  block_max_into(n, &s_red[1]);
+  __syncthreads();
+  const int total = s_incl[N - 1];
+  const bool sequential = device_picks_sequential(si.choose, si.rec_max, s_red[0], total, N, T,
+                                                  hv, si.form);
+  const int nt = sequential ? 0 : (total < nt_max ? total : nt_max);
+  const int form = (si.form == 0 || si.form == 1)
+                       ? si.form
+                       : (t_form_wins(static_cast<float>(nt), static_cast<float>(s_red[1])) ? 1 : 0);
+  if (blockIdx.x == 0) {
+    if (tid < N) {
+      const int first = sequential ? 0 : s_incl[tid] - n;
+      si.offsets[tid] = first < nt_max ? first : nt_max;
+    }
+    if (tid == 0) {
+      si.offsets[N] = nt;
+      si.offsets[N + 1] = sequential ? 1 : 0;
+      si.offsets[N + 2] = form;
+    }
+  }
+  return SelfIndexed{nt, form};
+}
+
+// Entry c of the chunk table from the self index's LDS arrays.
+__device__ __forceinline__ int4 self_chunk(const char *smem, int N, int c, int nt) {
+  if (c >= nt) return make_int4(-1, 0, 0, 0);
+  const int *const s_incl = reinterpret_cast<const int *>(smem);
+  const int *const s_bos = s_incl + kSelfIndexMax;
+  const int *const s_eos = s_bos + kSelfIndexMax;
+  int lo = 0, hi = N - 1;  // first sequence with s_incl > c
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (s_incl[mid] > c) hi = mid; else lo = mid + 1;
+  }
+  const int local = c - (lo == 0 ? 0 : s_incl[lo - 1]);
+  const int start = s_bos[lo] + local * kChunk;
+  const int len = s_eos[lo] - start < kChunk ? s_eos[lo] - start : kChunk;
+  return make_int4(lo, start, len, local);
 }
 
 // Workgroup id -> (chunk c, v-head h) for the per-(chunk, head) kernels, so
@@ -714,21 +815,16 @@ __device__ __forceinline__ void t_intra(
 // both halves of a chunk run on the same XCD and share its K rows in L2.
 template <bool SPLIT>
 __device__ __forceinline__ void intra_wy_unit(
-    char *smem, int id, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
-    const float *__restrict__ A_log, const uint16_t *__restrict__ a,
-    const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
-    const int4 *__restrict__ chunks, const OneSeq &one, int nt_max, const Heads &H,
-    float *__restrict__ ws_G, float *__restrict__ ws_dcy, float *__restrict__ ws_eg,
-    uint16_t *__restrict__ ws_w, float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
-  const int pair = SPLIT ? (((id >> 4) << 3) | (id & 7)) : id;
-  int c, h;
-  if (!chunk_head_of(pair, nt_max, H, c, h)) return;
-  const int4 ch = chunk_info(chunks, c, one);
-  if (ch.x < 0) return;
+    char *smem, int c, int h, int4 ch, int half, const uint16_t *__restrict__ k,
+    const uint16_t *__restrict__ v, const float *__restrict__ A_log,
+    const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
+    const uint16_t *__restrict__ b, const Heads &H, float *__restrict__ ws_G,
+    float *__restrict__ ws_dcy, float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w,
+    float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
   if (!SPLIT)
     wy_intra<0>(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w,
                 ws_u, ws_kt);
-  else if ((id >> 3) & 1)
+  else if (half)
     wy_intra<2>(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w,
                 ws_u, ws_kt);
   else
@@ -742,25 +838,43 @@ __device__ __forceinline__ void intra_body(
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
     const int4 *__restrict__ chunks, OneSeq one, int nt_max, Heads H,
-    const int *__restrict__ form_flag, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
-    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u,
-    uint16_t *__restrict__ ws_kt) {
+    const int *__restrict__ form_flag, const SelfIndex &si, float *__restrict__ ws_G,
+    float *__restrict__ ws_dcy, float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w,
+    float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
   static_assert(!(SPLIT && FORM != 0), "only the WY form splits into halves");
-  constexpr int kLds = FORM == 0 ? kIntraWyLds
-                       : FORM == 1 ? kIntraTLds
-                                   : (kIntraWyLds > kIntraTLds ? kIntraWyLds : kIntraTLds);
+  constexpr int kLds0 = FORM == 0 ? kIntraWyLds
+                        : FORM == 1 ? kIntraTLds
+                                    : (kIntraWyLds > kIntraTLds ? kIntraWyLds : kIntraTLds);
+  constexpr int kLds = kLds0 > kSelfIndexLds ? kLds0 : kSelfIndexLds;
   __shared__ __align__(16) char smem[kLds];
-  const int form = FORM >= 0 ? FORM : *form_flag;
-  if (form == 1) {
-    int c, h;
-    if (!chunk_head_of(blockIdx.x, nt_max, H, c, h)) return;
-    const int4 ch = chunk_info(chunks, c, one);
-    if (ch.x < 0) return;
-    t_intra(smem, c, h, ch.y, ch.z, k, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u);
+  // This workgroup's (chunk, v-head) -- and, split, its half: workgroup id
+  // 16 s + 8 p + x is half p of the pair 8 s + x (the same for both forms).
+  const int id = blockIdx.x;
+  const int pair = SPLIT ? (((id >> 4) << 3) | (id & 7)) : id;
+  const int half = SPLIT ? (id >> 3) & 1 : 0;
+  int c = 0, h = 0;
+  const bool unit = chunk_head_of(pair, nt_max, H, c, h);
+  int form = FORM;
+  int4 ch;
+  if (si.cu != nullptr) {
+    if (!unit && id != 0) return;
+    const SelfIndexed x = self_index(smem, si, nt_max, H.v);
+    if (FORM < 0) form = x.form;
+    ch = self_chunk(smem, si.N, c, x.nt);
+    if (unit && h == 0 && half == 0) si.chunks[c] = ch;
+    __syncthreads();  // the LDS arrays are dead: the unit's tiles take their place
+    if (!unit) return;
   } else {
-    intra_wy_unit<SPLIT>(smem, blockIdx.x, k, v, A_log, a, dt_bias, b, chunks, one, nt_max, H,
-                         ws_G, ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
+    if (!unit) return;
+    if (FORM < 0) form = *form_flag;
+    ch = chunk_info(chunks, c, one);
   }
+  if (ch.x < 0) return;
+  if (form == 1)
+    t_intra(smem, c, h, ch.y, ch.z, k, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u);
+  else
+    intra_wy_unit<SPLIT>(smem, c, h, ch, half, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg,
+                         ws_w, ws_u, ws_kt);
 }
 
 template <int FORM, bool SPLIT>
@@ -769,10 +883,10 @@ __global__ __launch_bounds__(256) void prefill_intra_kernel(
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
     const int4 *__restrict__ chunks, OneSeq one, int nt_max, Heads H,
-    const int *__restrict__ form_flag, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
-    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u,
-    uint16_t *__restrict__ ws_kt) {
-  intra_body<FORM, SPLIT>(k, v, A_log, a, dt_bias, b, chunks, one, nt_max, H, form_flag, ws_G,
+    const int *__restrict__ form_flag, SelfIndex si, float *__restrict__ ws_G,
+    float *__restrict__ ws_dcy, float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w,
+    float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
+  intra_body<FORM, SPLIT>(k, v, A_log, a, dt_bias, b, chunks, one, nt_max, H, form_flag, si, ws_G,
                           ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
 }
 // the form left to the device: held to five workgroups per CU, as each form
@@ -783,10 +897,10 @@ void prefill_intra_either_kernel(
     const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
     const int4 *__restrict__ chunks, OneSeq one, int nt_max, Heads H,
-    const int *__restrict__ form_flag, float *__restrict__ ws_G, float *__restrict__ ws_dcy,
-    float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w, float *__restrict__ ws_u,
-    uint16_t *__restrict__ ws_kt) {
-  intra_body<-1, false>(k, v, A_log, a, dt_bias, b, chunks, one, nt_max, H, form_flag, ws_G,
+    const int *__restrict__ form_flag, SelfIndex si, float *__restrict__ ws_G,
+    float *__restrict__ ws_dcy, float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w,
+    float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
+  intra_body<-1, false>(k, v, A_log, a, dt_bias, b, chunks, one, nt_max, H, form_flag, si, ws_G,
                         ws_dcy, ws_eg, ws_w, ws_u, ws_kt);
 }
 
@@ -1880,28 +1994,37 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   int rc = GDN_OK;
   // Several sequences: the index kernel builds the chunk table and, when the
   // plan leaves it to the device (P.choose != 0), sets the path flag read by
-  // the sequential and state kernels (the chunk table is then empty).
-  if (!P.single) {
+  // the sequential and state kernels (the chunk table is then empty) -- or,
+  // for at most kSelfIndexMax sequences, the intra kernel does it itself
+  // (P.self_index), launched first.
+  if (!P.single && !P.self_index) {
     hipLaunchKernelGGL(prefill_index_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, cu64, N, T,
                        L.nt_max, P.choose, rec_max, H.v, P.form, chunks, offsets);
     if ((rc = check_launch(what))) return rc;
   }
-  if (P.choose != 0) {
-    rc = recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
-                          offsets + N + 1, H, scale, output, new_state, stream, P.seq_variant,
-                          what);
-    if (rc) return rc;
+  auto sequential_kernel = [&]() {
+    return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
+                            offsets + N + 1, H, scale, output, new_state, stream, P.seq_variant,
+                            what);
+  };
+  if (P.choose != 0 && !P.self_index) {
+    if ((rc = sequential_kernel())) return rc;
   }
   if (P.intra_grid > 0) {
     const int *flag = offsets + N + 2;  // read only when the device picks the form
+    const SelfIndex si{P.self_index ? cu_seqlens : nullptr, cu64, N, T, P.choose, rec_max, P.form,
+                       chunks, offsets};
     auto intra = P.intra_split ? prefill_intra_kernel<0, true>
                  : P.form == 0 ? prefill_intra_kernel<0, false>
                  : P.form == 1 ? prefill_intra_kernel<1, false>
                                : prefill_intra_either_kernel;
     hipLaunchKernelGGL(intra, dim3(static_cast<unsigned>(P.intra_grid)), dim3(256), 0, stream, k,
-                       v, A_log, a, dt_bias, b, chunks, one, L.nt_max, H, flag, wsG, wsD, wsE, wsw,
-                       wsu, kt);
+                       v, A_log, a, dt_bias, b, chunks, one, L.nt_max, H, flag, si, wsG, wsD, wsE,
+                       wsw, wsu, kt);
     if ((rc = check_launch(what))) return rc;
+  }
+  if (P.choose != 0 && P.self_index) {
+    if ((rc = sequential_kernel())) return rc;
   }
   SplitScan sp{P.split_nt0, nullptr, nullptr, nullptr, nullptr};
   if (sp.nt0 > 0) {

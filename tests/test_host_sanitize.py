@@ -170,7 +170,7 @@ def test_plan_sweep(driver):
         f = [int(x) for x in got.split()]
         plans[c] = dict(rc=f[0], sequential=f[1], seq_variant=f[2], choose=f[3], single=f[4],
                         form=f[5], nt0=f[6], intra=f[7], state=f[8], split=f[9], out=f[10],
-                        intra_split=f[11], loop=f[12])
+                        intra_split=f[11], loop=f[12], self_index=f[13])
     base = (-1, -1, -1)
     p = plans[(96, 1, 4, 8) + base]
     assert p["sequential"] == 1
@@ -198,3 +198,6 @@ def test_plan_sweep(driver):
             assert p["loop"] == (p["choose"] != 0), c
             if p["loop"]:
                 assert p["state"] <= 512, c
+            # batches of 2..256 sequences and at most 2560 intra workgroups
+            # index themselves in the intra kernel
+            assert p["self_index"] == (1 < c[1] <= 256 and 0 < p["intra"] <= 2560), c
