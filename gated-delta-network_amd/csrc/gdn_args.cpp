@@ -113,6 +113,7 @@ PrefillLayout prefill_layout(int T, int N, const Heads &H) {
   const size_t nN = N > 0 ? static_cast<size_t>(N) : 0;
   L.chunks = take(n * 16);                // int4 per chunk
   L.offsets = take((nN + 3) * sizeof(int));  // + path and form flags
+  L.status = take(nN * sizeof(int));         // contract bits per sequence
   const size_t hv = static_cast<size_t>(H.v), hqk = static_cast<size_t>(H.qk);
   L.G = take(n * hv * kChunk * 4);
   L.dcy = take(n * hv * kChunk * 4);

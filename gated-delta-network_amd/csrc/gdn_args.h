@@ -64,7 +64,9 @@ int plan_multi(const void *q, const void *k, const void *v, int batch, int token
 struct PrefillLayout {
   int nt_max;  // upper bound on the chunk count from (T, N) alone
   // The T form keeps T in the w region and (beta, beta e^G) in the u region.
-  size_t chunks, offsets, G, dcy, eg, w, u, kt, ht, vnt;
+  // status: the contract bits of each sequence's cu_seqlens bounds (int per
+  // sequence; bit 0 decreasing, bit 1 outside [0, T]), written by every call.
+  size_t chunks, offsets, status, G, dcy, eg, w, u, kt, ht, vnt;
   // Two-segment scan of one sequence (N == 1 only, else empty): the map's
   // linear part per chunk of the second segment, the first segment's final
   // state and the second segment's map (offset, linear part).

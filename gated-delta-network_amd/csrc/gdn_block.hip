@@ -53,7 +53,7 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
                   const float *__restrict__ A_log, const uint16_t *__restrict__ a,
                   const float *__restrict__ dt_bias, const uint16_t *__restrict__ b,
                   const void *__restrict__ cu, int cu64, int N, int T, int fixed_len,
-                  const int *__restrict__ enable, Heads H, float scale,
+                  const int *__restrict__ enable, int *__restrict__ status, Heads H, float scale,
                   uint16_t *__restrict__ out, float *new_state) {
   __shared__ __align__(16) uint16_t sQ[kBlk * kBStride];
   __shared__ __align__(16) uint16_t sK[kBlk * kBStride];
@@ -81,6 +81,9 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
     bos = load_cu(cu, cu64, s, T);
     const int eos = load_cu(cu, cu64, s + 1, T);
     len = eos > bos ? eos - bos : 0;
+    // the batch's contract bits, one entry per sequence (host-routed batches)
+    if (status != nullptr && h == 0 && half == 0 && threadIdx.x == 0)
+      status[s] = cu_status_bits(raw_cu(cu, cu64, s), raw_cu(cu, cu64, s + 1), T);
   } else {
     bos = s * fixed_len;
     len = fixed_len;
@@ -419,7 +422,7 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
 int block_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
                  const float *A_log, const uint16_t *a, const float *dt_bias, const uint16_t *b,
                  const void *cu, int cu64, int num_seqs, int T, int fixed_len, const int *enable,
-                 const Heads &H, float scale, uint16_t *out, float *new_state,
+                 int *status, const Heads &H, float scale, uint16_t *out, float *new_state,
                  hipStream_t stream, const char *what) {
   const long long pairs = static_cast<long long>(num_seqs) * H.v;
   if (pairs > 0x3fffffffLL) return fail(GDN_ERR_INVALID, "%s: too many sequences for one launch", what);
@@ -429,11 +432,11 @@ int block_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const 
   // columns otherwise.
   if (pairs <= kBlockHalfMaxPairs)
     hipLaunchKernelGGL(block_kernel<1>, dim3(static_cast<unsigned>(2 * pairs)), dim3(256), 0, stream,
-                       q, k, v, state, A_log, a, dt_bias, b, cu, cu64, num_seqs, T, fixed_len, enable, H,
+                       q, k, v, state, A_log, a, dt_bias, b, cu, cu64, num_seqs, T, fixed_len, enable, status, H,
                        scale, out, new_state);
   else
     hipLaunchKernelGGL(block_kernel<2>, dim3(static_cast<unsigned>(pairs)), dim3(256), 0, stream,
-                       q, k, v, state, A_log, a, dt_bias, b, cu, cu64, num_seqs, T, fixed_len, enable, H,
+                       q, k, v, state, A_log, a, dt_bias, b, cu, cu64, num_seqs, T, fixed_len, enable, status, H,
                        scale, out, new_state);
   return check_launch(what);
 }

@@ -12,6 +12,6 @@ int check_launch(const char *what) {
 
 }  // namespace gdn
 
-extern "C" int gdn_abi_version(void) { return 3; }
+extern "C" int gdn_abi_version(void) { return 4; }
 
 extern "C" const char *gdn_last_error(void) { return gdn::last_error_text(); }

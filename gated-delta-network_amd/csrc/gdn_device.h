@@ -78,6 +78,16 @@ __device__ __forceinline__ int load_cu(const void *cu, int is64, int i, int T) {
   return static_cast<int>(x > T ? T : x);
 }
 
+// cu_seqlens as given (no clamp), and the contract bits of sequence s from
+// its bounds cu[s], cu[s+1]: bit 0 the bounds decrease, bit 1 one of them is
+// outside [0, T].  Zero for a well-formed batch.
+__device__ __forceinline__ long long raw_cu(const void *cu, int is64, int i) {
+  return is64 ? static_cast<const long long *>(cu)[i] : static_cast<const int *>(cu)[i];
+}
+__device__ __forceinline__ int cu_status_bits(long long lo, long long hi, int T) {
+  return (hi < lo ? 1 : 0) | ((lo < 0 || lo > T || hi < 0 || hi > T) ? 2 : 0);
+}
+
 // Token rows of a packed batch that no sequence covers -- [0, cu[0]) and
 // [cu[N], T) -- get a zero output, as in the reference, which zero-fills its
 // output and writes only the rows [cu[s], cu[s+1]) of each sequence

@@ -18,14 +18,15 @@ int check_launch(const char *what);
 // Token-sequential recurrence (gdn_recurrent.hip) over num_seqs sequences:
 // packed by cu (int32/int64 on the device) or, with cu == nullptr, of
 // fixed_len tokens each.  With a non-null `enable`, the kernel does nothing
-// unless *enable (on the device) is non-zero.  variant: row tiling index, -1 =
-// built-in.  Error messages start with `what`.
+// unless *enable (on the device) is non-zero.  With a non-null `status` (and
+// cu), status[s] receives the contract bits of sequence s (cu_status_bits).
+// variant: row tiling index, -1 = built-in.  Error messages start with `what`.
 int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
                      const float *A_log, const uint16_t *a, const float *dt_bias,
                      const uint16_t *b, const void *cu, int cu64, int num_seqs, int T,
-                     int fixed_len, const int *enable, const Heads &H, float scale,
-                     uint16_t *out, float *new_state, hipStream_t stream, int variant,
-                     const char *what);
+                     int fixed_len, const int *enable, int *status, const Heads &H,
+                     float scale, uint16_t *out, float *new_state, hipStream_t stream,
+                     int variant, const char *what);
 int recurrent_num_variants();
 // The variant of recurrent_launch that runs block_launch.
 int recurrent_block_variant();
@@ -36,7 +37,7 @@ int recurrent_block_variant();
 int block_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
                  const float *A_log, const uint16_t *a, const float *dt_bias, const uint16_t *b,
                  const void *cu, int cu64, int num_seqs, int T, int fixed_len, const int *enable,
-                 const Heads &H, float scale, uint16_t *out, float *new_state,
+                 int *status, const Heads &H, float scale, uint16_t *out, float *new_state,
                  hipStream_t stream, const char *what);
 
 // One decode step (gdn_decode.hip) with head layout H; variant as in

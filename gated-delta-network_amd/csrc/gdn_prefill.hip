@@ -52,6 +52,7 @@
 // f32.  The output path (Q S, Q K^T, P v_new) uses single bf16 operands: its
 // error stays ~2^-9 relative, far inside the bf16 output tolerance.
 #include <mutex>
+#include <vector>
 
 #include "gdn_device.h"
 #include "gdn_host.h"
@@ -121,12 +122,14 @@ __device__ __forceinline__ bool device_picks_sequential(int choose, int rec_max,
 __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int cu64, int N, int T,
                                                               int nt_max, int choose, int rec_max,
                                                               int hv, int form, int4 *chunks,
-                                                              int *offsets) {
+                                                              int *offsets, int *status) {
   __shared__ int s_incl[1024], s_bos[1024], s_eos[1024];
   __shared__ int s_wsum[16];
   __shared__ int s_longest, s_most_chunks, s_chunks;
   const int tid = threadIdx.x;
   if (tid == 0) s_longest = s_most_chunks = s_chunks = 0;
+  for (int s = tid; s < N; s += 1024)
+    status[s] = cu_status_bits(raw_cu(cu, cu64, s), raw_cu(cu, cu64, s + 1), T);
   __syncthreads();
   if (choose != 0) {
     int longest = 0, nch = 0;
@@ -239,6 +242,7 @@ struct SelfIndex {
   int cu64, N, T, choose, rec_max, form;
   int4 *chunks;
   int *offsets;
+  int *status;     // per-sequence contract bits (also for one sequence)
 };
 constexpr int kSelfIndexLds = 3 * kSelfIndexMax * 4 + 16 * 4;
 
@@ -257,8 +261,10 @@ __device__ __forceinline__ SelfIndexed self_index(char *smem, const SelfIndex &s
   int n = 0, len = 0;
   if (tid < 2) s_red[tid] = 0;
   if (tid < N) {
-    const int bos = load_cu(si.cu, si.cu64, tid, T);
-    int eos = load_cu(si.cu, si.cu64, tid + 1, T);
+    const long long lo = raw_cu(si.cu, si.cu64, tid), hi = raw_cu(si.cu, si.cu64, tid + 1);
+    if (blockIdx.x == 0) si.status[tid] = cu_status_bits(lo, hi, T);
+    const int bos = static_cast<int>(lo < 0 ? 0 : lo > T ? T : lo);
+    int eos = static_cast<int>(hi < 0 ? 0 : hi > T ? T : hi);
     eos = eos < bos ? bos : eos;
     len = eos - bos;
     n = (len + kChunk - 1) / kChunk;
@@ -865,6 +871,9 @@ __device__ __forceinline__ void intra_body(
     __syncthreads();  // the LDS arrays are dead: the unit's tiles take their place
     if (!unit) return;
   } else {
+    // one sequence: its contract bits (several: the index kernel's)
+    if (one.cu != nullptr && id == 0 && threadIdx.x == 0)
+      si.status[0] = cu_status_bits(raw_cu(one.cu, one.cu64, 0), raw_cu(one.cu, one.cu64, 1), one.T);
     if (!unit) return;
     if (FORM < 0) form = *form_flag;
     ch = chunk_info(chunks, c, one);
@@ -1975,11 +1984,13 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
     return rc;
   // The whole batch through one sequential kernel (token by token, or in
   // 16-token blocks), decided on the host.
+  char *ws = static_cast<char *>(workspace);
+  int *status = reinterpret_cast<int *>(ws + L.status);
   if (P.sequential)
     return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
-                            nullptr, H, scale, output, new_state, stream, P.seq_variant, what);
+                            nullptr, status, H, scale, output, new_state, stream, P.seq_variant,
+                            what);
 
-  char *ws = static_cast<char *>(workspace);
   int4 *chunks = reinterpret_cast<int4 *>(ws + L.chunks);
   int *offsets = reinterpret_cast<int *>(ws + L.offsets);
   float *wsG = reinterpret_cast<float *>(ws + L.G);
@@ -1999,13 +2010,13 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   // (P.self_index), launched first.
   if (!P.single && !P.self_index) {
     hipLaunchKernelGGL(prefill_index_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, cu64, N, T,
-                       L.nt_max, P.choose, rec_max, H.v, P.form, chunks, offsets);
+                       L.nt_max, P.choose, rec_max, H.v, P.form, chunks, offsets, status);
     if ((rc = check_launch(what))) return rc;
   }
   auto sequential_kernel = [&]() {
     return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu64, N, T, 0,
-                            offsets + N + 1, H, scale, output, new_state, stream, P.seq_variant,
-                            what);
+                            offsets + N + 1, nullptr, H, scale, output, new_state, stream,
+                            P.seq_variant, what);
   };
   if (P.choose != 0 && !P.self_index) {
     if ((rc = sequential_kernel())) return rc;
@@ -2013,7 +2024,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   if (P.intra_grid > 0) {
     const int *flag = offsets + N + 2;  // read only when the device picks the form
     const SelfIndex si{P.self_index ? cu_seqlens : nullptr, cu64, N, T, P.choose, rec_max, P.form,
-                       chunks, offsets};
+                       chunks, offsets, status};
     auto intra = P.intra_split ? prefill_intra_kernel<0, true>
                  : P.form == 0 ? prefill_intra_kernel<0, false>
                  : P.form == 1 ? prefill_intra_kernel<1, false>
@@ -2148,28 +2159,26 @@ static void *g_scratch_ptr[kMaxScratchDevices];
 
 // The scratch array of the device `stream` runs on, which must be the current
 // device (the lookup resolves the array of the current device).
-static int device_scratch(void *stream, void **ptr) {
+static int device_scratch(void *stream, void **ptr, const char *what) {
   int cur = -1;
   hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess || cur < 0 || cur >= kMaxScratchDevices)
-    return fail(GDN_ERR_LAUNCH, "gdn_prefill_fwd_noalloc: no usable current device (%s)",
-                hipGetErrorString(e));
+    return fail(GDN_ERR_LAUNCH, "%s: no usable current device (%s)", what, hipGetErrorString(e));
   if (stream != nullptr) {
     hipDevice_t sdev = -1;
     e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
-    if (e != hipSuccess)
-      return fail(GDN_ERR_INVALID, "gdn_prefill_fwd_noalloc: bad stream (%s)", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(GDN_ERR_INVALID, "%s: bad stream (%s)", what, hipGetErrorString(e));
     if (sdev != cur)
-      return fail(GDN_ERR_INVALID, "gdn_prefill_fwd_noalloc: the stream is on device %d, the "
-                  "current device is %d", static_cast<int>(sdev), cur);
+      return fail(GDN_ERR_INVALID, "%s: the stream is on device %d, the current device is %d", what,
+                  static_cast<int>(sdev), cur);
   }
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch_ptr[cur] == nullptr) {
     void *p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr)
-      return fail(GDN_ERR_LAUNCH, "gdn_prefill_fwd_noalloc: hipGetSymbolAddress(scratch) on device "
-                  "%d failed: %s", cur, hipGetErrorString(e));
+      return fail(GDN_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d failed: %s", what,
+                  cur, hipGetErrorString(e));
     g_scratch_ptr[cur] = p;
   }
   *ptr = g_scratch_ptr[cur];
@@ -2195,9 +2204,50 @@ extern "C" int gdn_prefill_fwd_noalloc(const gdn_bf16 *q, const gdn_bf16 *k, con
                      "gdn_prefill_fwd with a workspace)", total_tokens, num_seqs, need,
                      static_cast<size_t>(GDN_PREFILL_SCRATCH_BYTES));
   void *ws = nullptr;
-  if (int rc = gdn::device_scratch(stream, &ws)) return rc;
+  if (int rc = gdn::device_scratch(stream, &ws, "gdn_prefill_fwd_noalloc")) return rc;
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64,
                              num_seqs, total_tokens, scale, output, new_state, ws,
                              GDN_PREFILL_SCRATCH_BYTES, stream, -1, -1, -1, gdn::kHQK, gdn::kHV,
                              "gdn_prefill_fwd_noalloc");
+}
+
+extern "C" long long gdn_prefill_status_offset(int total_tokens, int num_seqs, int num_qk_heads,
+                                               int num_v_heads) {
+  if (total_tokens < 0 || num_seqs < 1 || num_qk_heads < 1 || num_v_heads < 1 ||
+      num_v_heads > gdn::kMaxHeads || num_v_heads % num_qk_heads != 0)
+    return -1;
+  const gdn::Heads H{num_qk_heads, num_v_heads, num_v_heads / num_qk_heads};
+  return static_cast<long long>(gdn::prefill_layout(total_tokens, num_seqs, H).status);
+}
+
+extern "C" int gdn_prefill_status(const void *workspace, int total_tokens, int num_seqs,
+                                  int num_qk_heads, int num_v_heads, void *stream, int *status) {
+  gdn::clear_error();
+  const long long off = gdn_prefill_status_offset(total_tokens, num_seqs, num_qk_heads, num_v_heads);
+  if (status == nullptr || off < 0)
+    return gdn::fail(GDN_ERR_INVALID, "gdn_prefill_status: status=%p, T=%d, N=%d, heads %d/%d",
+                     static_cast<void *>(status), total_tokens, num_seqs, num_qk_heads, num_v_heads);
+  const char *ws = static_cast<const char *>(workspace);
+  if (ws == nullptr) {
+    const size_t need = gdn_prefill_workspace_bytes_heads(total_tokens, num_seqs, num_qk_heads,
+                                                          num_v_heads);
+    if (need > GDN_PREFILL_SCRATCH_BYTES)
+      return gdn::fail(GDN_ERR_WORKSPACE, "gdn_prefill_status: %d tokens in %d sequences do not fit "
+                       "the static scratch", total_tokens, num_seqs);
+    void *p = nullptr;
+    if (int rc = gdn::device_scratch(stream, &p, "gdn_prefill_status")) return rc;
+    ws = static_cast<const char *>(p);
+  }
+  std::vector<int> words(static_cast<size_t>(num_seqs));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = hipMemcpyAsync(words.data(), ws + off, words.size() * sizeof(int),
+                                hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess)
+    return gdn::fail(GDN_ERR_LAUNCH, "gdn_prefill_status: reading the status words failed: %s",
+                     hipGetErrorString(e));
+  int bits = 0;
+  for (int w : words) bits |= w;
+  *status = bits;
+  return GDN_OK;
 }

@@ -42,8 +42,8 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
     const uint16_t *__restrict__ v, const float *state, const float *__restrict__ A_log,
     const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
     const uint16_t *__restrict__ b, const void *__restrict__ cu, int cu64, int N, int T,
-    int fixed_len, const int *__restrict__ enable, Heads H, float scale,
-    uint16_t *__restrict__ out, float *new_state) {
+    int fixed_len, const int *__restrict__ enable, int *__restrict__ status, Heads H,
+    float scale, uint16_t *__restrict__ out, float *new_state) {
   constexpr int kRows = 4 * WAVES * PASSES;
   constexpr int kTiles = kDV / kRows;
   static_assert(kDV % kRows == 0, "row block must divide 128");
@@ -61,6 +61,9 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
     bos = load_cu(cu, cu64, s, T);
     const int eos = load_cu(cu, cu64, s + 1, T);
     len = eos > bos ? eos - bos : 0;
+    // the batch's contract bits, one entry per sequence (host-routed batches)
+    if (status != nullptr && h == 0 && tile == 0 && threadIdx.x == 0)
+      status[s] = cu_status_bits(raw_cu(cu, cu64, s), raw_cu(cu, cu64, s + 1), T);
   } else {
     bos = s * fixed_len;
     len = fixed_len;
@@ -214,12 +217,12 @@ template <int W, int P>
 void launch_rec(long long groups, hipStream_t stream, const uint16_t *q, const uint16_t *k,
                 const uint16_t *v, const float *state, const float *A_log, const uint16_t *a,
                 const float *dt_bias, const uint16_t *b, const void *cu, int cu64, int N, int T,
-                int fixed_len, const int *enable, const Heads &H, float scale, uint16_t *out,
-                float *new_state) {
+                int fixed_len, const int *enable, int *status, const Heads &H, float scale,
+                uint16_t *out, float *new_state) {
   const long long blocks = groups * (kDV / (4 * W * P));
   hipLaunchKernelGGL((recurrent_kernel<W, P>), dim3(static_cast<unsigned>(blocks)), dim3(64 * W),
                      0, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, N, T, fixed_len,
-                     enable, H, scale, out, new_state);
+                     enable, status, H, scale, out, new_state);
 }
 
 }  // namespace
@@ -241,14 +244,14 @@ int recurrent_default_variant(long long groups) {
 int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,
                      const float *A_log, const uint16_t *a, const float *dt_bias,
                      const uint16_t *b, const void *cu, int cu64, int num_seqs, int T,
-                     int fixed_len, const int *enable, const Heads &H, float scale,
-                     uint16_t *out, float *new_state, hipStream_t stream, int variant,
-                     const char *what) {
+                     int fixed_len, const int *enable, int *status, const Heads &H,
+                     float scale, uint16_t *out, float *new_state, hipStream_t stream,
+                     int variant, const char *what) {
   const long long groups = static_cast<long long>(num_seqs) * H.v;
   if (variant < 0) variant = recurrent_default_variant(groups);
   if (variant == kNumRecVariants)
     return block_launch(q, k, v, state, A_log, a, dt_bias, b, cu, cu64, num_seqs, T, fixed_len,
-                        enable, H, scale, out, new_state, stream, what);
+                        enable, status, H, scale, out, new_state, stream, what);
   if (variant > kNumRecVariants)
     return fail(GDN_ERR_INVALID, "%s: recurrent tiling %d out of range", what, variant);
   const RecVariant rv = kRecVariants[variant];
@@ -257,7 +260,7 @@ int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, co
 #define GDN_REC(W, P)                                                                          \
   if (rv.waves == W && rv.passes == P)                                                        \
     launch_rec<W, P>(groups, stream, q, k, v, state, A_log, a, dt_bias, b, cu, cu64, num_seqs, \
-                     T, fixed_len, enable, H, scale, out, new_state);
+                     T, fixed_len, enable, status, H, scale, out, new_state);
   GDN_REC(1, 1)
   GDN_REC(2, 1)
   GDN_REC(4, 1)
@@ -297,8 +300,8 @@ static int multi_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
     return decode_launch(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch,
                          stream, -1, H, what);
   return recurrent_launch(q, k, v, state, A_log, a, dt_bias, b, nullptr, 0, batch,
-                          static_cast<int>(total), tokens, nullptr, H, scale, output, new_state,
-                          static_cast<hipStream_t>(stream), kernel, what);
+                          static_cast<int>(total), tokens, nullptr, nullptr, H, scale, output,
+                          new_state, static_cast<hipStream_t>(stream), kernel, what);
 }
 
 }  // namespace gdn

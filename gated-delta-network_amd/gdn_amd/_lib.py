@@ -19,7 +19,7 @@ GDN_ERR_INVALID = -1
 GDN_ERR_LAUNCH = -2
 GDN_ERR_WORKSPACE = -3
 PREFILL_SCRATCH_BYTES = 64 << 20  # GDN_PREFILL_SCRATCH_BYTES
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -47,6 +47,8 @@ SIGNATURES = {
                                    _P, _P, _P, _SZ, _P, _I, _I, _I]),
     "gdn_prefill_fwd_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P,
                                      _P]),
+    "gdn_prefill_status_offset": (ctypes.c_longlong, [_I, _I, _I, _I]),
+    "gdn_prefill_status": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "gdn_stream_copy": (_I, [_P, _P, _SZ, _P]),
 }
 

@@ -26,6 +26,7 @@ cu_seqlens[N] on) are written as zeros, as the reference's zero-filled output.
 
 from __future__ import annotations
 
+import ctypes
 import threading
 
 import torch
@@ -82,6 +83,36 @@ def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
         if capturing:
             entry[1] = True
         return entry[0]
+
+
+def batch_status(total_tokens: int, num_seqs: int, *, workspace=None, device=None,
+                 heads=(H_QK, HV)) -> int:
+    """Whether the last prefill call of (T, N) on torch's current stream kept
+    the cu_seqlens contract: the OR of the per-sequence status words it left
+    in its workspace (gdn_prefill_status_offset, include/gdn_amd.h): 0 for a
+    well-formed batch, bit 0 if some cu_seqlens[s+1] < cu_seqlens[s], bit 1 if
+    some offset is outside [0, T].  ``workspace`` is the buffer passed to that
+    call (default: the stream's cached one).  Synchronises the stream: for
+    tests and debugging, not the hot path."""
+    lib = _lib.load()
+    T, N = int(total_tokens), int(num_seqs)
+    if N < 1:
+        raise ValueError("a batch without sequences leaves no status")
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    if workspace is None:
+        with _ws_lock:
+            entry = _workspaces.get((dev.index, stream))
+        if entry is None:
+            raise ValueError("no prefill call has run on this stream")
+        workspace = entry[0]
+    need = workspace_bytes(T, N, heads)
+    _check_workspace(workspace, dev, need)
+    out = ctypes.c_int(0)
+    rc = lib.gdn_prefill_status(workspace.data_ptr(), T, N, int(heads[0]), int(heads[1]), stream,
+                                ctypes.byref(out))
+    _lib.check(rc, "gdn_prefill_status")
+    return int(out.value)
 
 
 def _validate(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state):

@@ -132,6 +132,30 @@ int gdn_decode_fwd_heads(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v
 size_t gdn_prefill_workspace_bytes(int total_tokens, int num_seqs);
 
 /*
+ * Where a prefill call leaves, in its workspace, whether cu_seqlens kept the
+ * contract below: num_seqs int32 words from this byte offset, word s = bit 0
+ * if cu_seqlens[s+1] < cu_seqlens[s], bit 1 if either is outside [0, T]; all
+ * zero for a well-formed batch.  Every call with num_seqs >= 1 writes them on
+ * the device, in the first kernel that reads the bounds, so the check needs
+ * no host read or sync of cu_seqlens.  -1 for invalid arguments.  No
+ * counterpart in the reference, which reads the bounds on the host and skips
+ * a sequence whose length is not positive (reference/gdn_prefill_ref.py:55-61)
+ * without reporting it.
+ */
+long long gdn_prefill_status_offset(int total_tokens, int num_seqs, int num_qk_heads,
+                                    int num_v_heads);
+
+/*
+ * Reader of those words for tests and debugging (it synchronizes: not for
+ * the hot path): waits for `stream`, then ORs the num_seqs words the last
+ * prefill call on `workspace` with this (T, N, heads) left into *status (0:
+ * well-formed).  workspace NULL reads the scratch of gdn_prefill_fwd_noalloc
+ * on the current device.  No counterpart in the reference.
+ */
+int gdn_prefill_status(const void *workspace, int total_tokens, int num_seqs, int num_qk_heads,
+                       int num_v_heads, void *stream, int *status);
+
+/*
  * Chunked prefill over a packed batch of variable-length sequences.
  *
  * Replaces the six launches behind the reference's prefill entry point
@@ -151,8 +175,9 @@ size_t gdn_prefill_workspace_bytes(int total_tokens, int num_seqs);
  * non-decreasing and within [0, T], but need not start at 0 or end at T: as
  * in the reference (gdn_prefill_ref.py:49-62), the output rows before
  * cu_seqlens[0] and from cu_seqlens[N] on are written as zeros, and a single
- * sequence's state covers exactly its own tokens (a decreasing batch leaves
- * the outputs unspecified but never accesses memory out of bounds).  With
+ * sequence's state covers exactly its own tokens (a batch outside this
+ * contract leaves the outputs unspecified but never accesses memory out of
+ * bounds, and says so in its status words: gdn_prefill_status_offset).  With
  * num_seqs = 0 the whole output is zeroed and the workspace may be NULL.  A
  * zero-length sequence gets an all-zero new_state, as the reference does.
  * new_state may alias state; output must be 16-byte aligned and must not
@@ -187,9 +212,10 @@ int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
  * shortest chain), 1 = T form (the intra kernel stores only (I+A)^-1; each
  * state step forms beta V - beta e^G K S from the inputs: less memory
  * traffic, one more exchange per step), -1 = the built-in choice (what
- * gdn_prefill_fwd uses: the T form for batches of at least 128 chunks with at
- * least three times the chunks of their longest sequence, decided on the
- * device; the WY form otherwise and for one sequence), 2 = WY form with one
+ * gdn_prefill_fwd uses: the T form for batches of at least 192 chunks with
+ * more than three times the chunks of their longest sequence, or of at least
+ * 384 with at least twice, decided on the device; the WY form otherwise and
+ * for one sequence), 2 = WY form with one
  * serial chain of state steps per sequence, 3 = WY form with the two-segment
  * scan for a single sequence of at least two chunks (the second half of the
  * chunks runs beside the first from a zero state and from the identity, and

@@ -223,6 +223,28 @@ def test_prefill_workspace_bytes_heads():
         assert lib.gdn_prefill_workspace_bytes_heads(64, 1, hqk, hv) == 0
 
 
+def test_prefill_status_offset():
+    # the status words follow the chunk table and the offsets/flags region,
+    # each region on a 256-byte boundary (prefill_layout, gdn_args.cpp)
+    lib = _lib.load()
+    up = lambda n: (n + 255) // 256 * 256
+    for T, N in [(1, 1), (1000, 1), (8192, 4), (4250, 6), (100, 300), (0, 5)]:
+        nt = min(T, (T + 63 * N) // 64) if T and N else 0
+        assert lib.gdn_prefill_status_offset(T, N, 4, 8) == up(nt * 16) + up((N + 3) * 4)
+        assert lib.gdn_prefill_status_offset(T, N, 4, 8) + 4 * N <= \
+            lib.gdn_prefill_workspace_bytes(T, N)
+    for T, N, hqk, hv in [(-1, 1, 4, 8), (10, 0, 4, 8), (10, 1, 3, 8), (10, 1, 0, 8)]:
+        assert lib.gdn_prefill_status_offset(T, N, hqk, hv) == -1
+
+
+def test_prefill_status_rejects_bad_arguments():
+    lib = _lib.load()
+    got = ctypes.c_int(0)
+    assert lib.gdn_prefill_status(None, 10, 1, 4, 8, None, None) == _lib.GDN_ERR_INVALID
+    assert "gdn_prefill_status" in _lib.last_error()
+    assert lib.gdn_prefill_status(None, 10, 0, 4, 8, None, ctypes.byref(got)) == _lib.GDN_ERR_INVALID
+
+
 @pytest.mark.parametrize("hqk, hv", [(3, 8), (0, 8), (8, 4)])
 def test_prefill_heads_rejects_bad_heads(hqk, hv):
     lib = _lib.load()

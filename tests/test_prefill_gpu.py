@@ -360,6 +360,7 @@ def _layout(T, N):
 
     take("chunks", nt * 16)
     take("offsets", (N + 3) * 4)  # offsets[0..N], then the path and form flags
+    take("status", N * 4)         # the cu_seqlens contract bits of each sequence
     take("G", nt * 8 * 64 * 4)
     take("dcy", nt * 8 * 64 * 4)
     take("eg", nt * 8 * 4)
