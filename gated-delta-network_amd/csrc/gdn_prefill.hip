@@ -565,10 +565,11 @@ __device__ __forceinline__ void wy_intra(
     f32x4 Y[4][2];
     wy_solve(sX, sBG, sA, col0, g, r16, Y);
     __syncthreads();  // K is dead: its space is the w scratch
-    // w -> hi/lo A-operand fragments [mb][kk][lane][hi 8 | lo 8] (row
-    // 16 mb + r16, features 32 kk + 8 g ..), in two passes of 64 features
-    // through the f32 scratch: waves 2p, 2p + 1 fill it, then each wave
-    // converts two of the pass's eight fragments.
+    // w -> hi/lo A-operand fragments [hi | lo][mb][kk][lane][8] (row
+    // 16 mb + r16, features 32 kk + 8 g ..; the hi plane alone serves the
+    // second-segment output), in two passes of 64 features through the f32
+    // scratch: waves 2p, 2p + 1 fill it, then each wave converts two of the
+    // pass's eight fragments.
     uint16_t *wf = ws_w + ch_head * (kChunk * kDK * 2);
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
@@ -591,9 +592,9 @@ __device__ __forceinline__ void wy_intra(
         const float x8[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
         u32x4 hi, lo;
         split8(x8, hi, lo);
-        uint16_t *dst = wf + ((mb * 4 + 2 * pass + kk2) * 64 + lane) * 16;
+        uint16_t *dst = wf + ((mb * 4 + 2 * pass + kk2) * 64 + lane) * 8;
         *reinterpret_cast<u32x4 *>(dst) = hi;
-        *reinterpret_cast<u32x4 *>(dst + 8) = lo;
+        *reinterpret_cast<u32x4 *>(dst + kChunk * kDK) = lo;
       }
       __syncthreads();
     }
@@ -935,13 +936,13 @@ __device__ __forceinline__ void load_wy_frag(WyFrag &f, int c, int h, const Head
                                                 const float *ws_u, const uint16_t *ws_kt) {
   const int q4 = 4 * (lane >> 4);
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
-  // w: [mb][kk][lane][hi 8 | lo 8] fragments of this wave's 16 rows
+  // w: [hi | lo][mb][kk][lane][8] fragments of this wave's 16 rows
   const auto rw = buf_rsrc(ws_w + ch_head * (kWBytes / 2), kWBytes);
-  const uint32_t wo = static_cast<uint32_t>(wave) * 8192u + static_cast<uint32_t>(lane) * 32u;
+  const uint32_t wo = static_cast<uint32_t>(wave) * 4096u + static_cast<uint32_t>(lane) * 16u;
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
-    f.wh[kk] = buf_load16(rw, wo + kk * 2048);
-    f.wl[kk] = buf_load16(rw, wo + kk * 2048 + 16);
+    f.wh[kk] = buf_load16(rw, wo + kk * 1024);
+    f.wl[kk] = buf_load16(rw, wo + kk * 1024 + kWBytes / 2);
   }
   // K^T: [mt][kk][lane][8] fragments of this wave's two 16-row tiles
   const auto rk = buf_rsrc(ws_kt + (static_cast<size_t>(c) * H.qk + h / H.ratio) * (kKtBytes / 2), kKtBytes);
@@ -1545,8 +1546,8 @@ void prefill_split_out_kernel(const uint16_t *__restrict__ q, const uint16_t *__
 
   // --- Every global load is issued here, so that one memory latency covers
   // them all: Q and K rows (rows past the chunk read zero through the
-  // descriptors' range), G and the hi halves of w's stored fragments
-  // [jb][kk][lane][hi 8 | lo 8] (A operands of w M^T, all 64 rows) -> LDS;
+  // descriptors' range), G and the hi plane of w's stored fragments
+  // [hi | lo][jb][kk][lane][8] (A operands of w M^T, all 64 rows) -> LDS;
   // the S0 rows of this wave's columns n = 32 wave + 16 nt + r16 (B operands
   // of R S0^T) into registers.
   const uint32_t rstride = static_cast<uint32_t>(H.qk) * (kDK * 2);
@@ -1561,7 +1562,7 @@ void prefill_split_out_kernel(const uint16_t *__restrict__ q, const uint16_t *__
       const uint32_t off = static_cast<uint32_t>(idx >> 4) * rstride + (idx & 15) * 16;
       qv[i] = buf_load16(rq, off);
       kv[i] = buf_load16(rk, off);
-      wv[i] = *reinterpret_cast<const u32x4 *>(wsrc + idx * 16);
+      wv[i] = *reinterpret_cast<const u32x4 *>(wsrc + idx * 8);  // the hi plane
     }
     if (tid < kChunk) sG[tid] = ws_G[ch_head * kChunk + tid];
 #pragma unroll

@@ -421,11 +421,11 @@ def test_prefill_stage_intermediates(cuda_device, form):
         ut = arr("u", np.float32, (L["nt"], 8, 4, 8, 4, 16, 4))[:nt]  # lane = (g, r16)
         u = ut.transpose(0, 1, 2, 4, 6, 3, 5).reshape(nt, 8, 64, 128)
         assert np.abs(u - it["u"]).max() <= 1e-4 * np.abs(it["u"]).max()
-        # w: A fragments [c][h][mb][kk][lane][hi 8 | lo 8] holding
+        # w: A fragments [c][h][hi | lo][mb][kk][lane][8] holding
         # w[16mb + (lane & 15)][32kk + 8(lane >> 4) + e]
-        wf = arr("w", np.uint16, (L["nt"], 8, 4, 4, 4, 16, 2, 8))[:nt]  # lane = (g, r16)
-        wv = (O.bf16_from_bits(wf[..., 0, :]).astype(np.float64)
-              + O.bf16_from_bits(wf[..., 1, :]))                       # [c,h,mb,kk,g,r16,e]
+        wf = arr("w", np.uint16, (L["nt"], 8, 2, 4, 4, 4, 16, 8))[:nt]  # lane = (g, r16)
+        wv = (O.bf16_from_bits(wf[:, :, 0]).astype(np.float64)
+              + O.bf16_from_bits(wf[:, :, 1]))                         # [c,h,mb,kk,g,r16,e]
         w = wv.transpose(0, 1, 2, 5, 3, 4, 6).reshape(nt, 8, 64, 128)
         assert np.abs(w - it["w"]).max() <= 1e-4 * np.abs(it["w"]).max()
     else:
