@@ -19,6 +19,7 @@ serves any batch of the same (T, N), including new cu_seqlens contents.  A
 graph captured without ``workspace=`` writes into the cached buffer of its
 stream; once a capture has used a cached buffer, that buffer is never freed
 (a larger call later gets a new one), so the graph can always replay into it.
+``release_workspaces()`` hands the other cached buffers back to torch.
 
 Rows of ``output`` outside every sequence (before cu_seqlens[0] or from
 cu_seqlens[N] on) are written as zeros, as the reference's zero-filled output.
@@ -83,6 +84,23 @@ def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
         if capturing:
             entry[1] = True
         return entry[0]
+
+
+def release_workspaces() -> int:
+    """Drops the cached per-stream workspaces that no captured graph can
+    write (torch's caching allocator then owns their memory again); a cached
+    buffer a capture has used stays, as it must for the graph's replays.  The
+    next call on a stream allocates afresh.  Safe with work still queued: each
+    buffer was allocated on its own stream, so the allocator hands its memory
+    only to later work on that stream.  Returns the bytes released."""
+    freed = 0
+    with _ws_lock:
+        for key in list(_workspaces):
+            buf, captured = _workspaces[key]
+            if not captured:
+                freed += buf.numel()
+                del _workspaces[key]
+    return freed
 
 
 def batch_status(total_tokens: int, num_seqs: int, *, workspace=None, device=None,

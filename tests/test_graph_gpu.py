@@ -207,6 +207,35 @@ def test_prefill_workspace_argument_checks(cuda_device):
     assert_state_close(ns.cpu().numpy(), s_ref)
 
 
+def test_prefill_release_workspaces(cuda_device):
+    # a call on a fresh stream caches a workspace for it; release_workspaces
+    # hands it back (it was never captured), and the next call allocates anew
+    # and gives the same result
+    dev = cuda_device
+    inp = O.make_prefill_inputs([300], seed=6)
+    st = _prefill_static(300, 1, dev)
+    _fill_prefill(st, inp)
+    side = torch.cuda.Stream(device=dev)
+    outs = []
+    for _ in range(2):
+        out = torch.empty((300, 8, 128), dtype=torch.bfloat16, device=dev)
+        ns = torch.empty((1, 8, 128, 128), dtype=torch.float32, device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            prefill.kernel(st["q"], st["k"], st["v"], st["state"], st["A_log"], st["a"],
+                           st["dt_bias"], st["b"], st["cu_seqlens"], None, out, ns)
+        torch.cuda.synchronize()
+        outs.append((out, ns))
+        key = (dev.index, side.cuda_stream)
+        assert key in prefill._workspaces
+        assert prefill.release_workspaces() >= prefill.workspace_bytes(300, 1)
+        assert key not in prefill._workspaces
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    assert_output_close(outs[0][0].float().cpu().numpy(), o_ref)
+    assert_state_close(outs[0][1].cpu().numpy(), s_ref)
+
+
 def test_prefill_graph_replays_two_segment_scan(cuda_device):
     # One sequence of 2500 tokens (40 chunks: the two-segment scan, its
     # second-segment output kernel and the new_state tiles), captured once and
