@@ -106,11 +106,12 @@ constexpr int kRecurrentMaxLen = 96;
 
 // Two-segment scan of one sequence (state kernel, SplitScan): three groups of
 // 8 workgroups per v-head, one per CU, so it needs 24 H.v <= 256; the built-in
-// choice takes it from kSplitMinChunks chunks on (MI355X, graph replay: one
-// chain vs two segments 41.0 vs 44.9 us at 16 chunks, 54.2 vs 51.6 at 32,
-// 173.9 vs ~130 at 128, 308 vs 275 at 256).  Variants: 0 / -1 built in, 2
-// never (one chain), 3 always (one sequence of at least two chunks).
-constexpr int kSplitMinChunks = 32;
+// choice takes it from kSplitMinChunks chunks on (MI355X, graph replay, one
+// chain vs two segments: 28.3 vs 28.4 us at 8 chunks, 30.3 vs 29.5 at 9, 39.3
+// vs 35.3 at 16, 53.3 vs 43.9 at 32, 64.5 vs 53.1 at 40).  Variants: 0 / -1
+// built in, 2 never (one chain), 3 always (one sequence of at least two
+// chunks).
+constexpr int kSplitMinChunks = 9;
 
 // Compute units of the target (MI355X: 256).  The WY intra kernel runs each
 // (chunk, v-head) as two workgroups (its w and u halves) while that leaves

@@ -470,7 +470,7 @@ def _stream(dev):
 # identity, and the second segment's output and new_state then apply the
 # first half's final state.
 # variant 3 forces it (one sequence of >= 2 chunks), 2 forbids it; the built-in
-# choice takes it from 32 chunks on.
+# choice takes it from 9 chunks on.
 SPLIT, CHAIN = 3, 2
 
 
@@ -492,7 +492,7 @@ def test_prefill_two_segment_scan(cuda_device, L, with_state, slow):
         assert np.array_equal(oi, res[SPLIT][0]) and np.array_equal(si, res[SPLIT][1])
 
 
-@pytest.mark.parametrize("L, expect", [(1024, CHAIN), (2048, SPLIT), (8192, SPLIT)])
+@pytest.mark.parametrize("L, expect", [(512, CHAIN), (577, SPLIT), (1024, SPLIT), (8192, SPLIT)])
 def test_prefill_two_segment_built_in_choice(cuda_device, L, expect):
     print(f"prefill two-segment choice L={L} expect variant {expect}", flush=True)
     inp = O.make_prefill_inputs([L], seed=41, with_state=True)
