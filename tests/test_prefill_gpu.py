@@ -209,6 +209,31 @@ def test_prefill_built_in_form_choice(cuda_device, lens):
 
 
 @pytest.mark.parametrize("form", list(FORMS))
+def test_prefill_self_index_matches_index_kernel(cuda_device, form):
+    # A batch of at most 256 sequences and two rounds of intra workgroups
+    # builds its chunk table inside the intra kernel; padded with empty
+    # sequences to 257 it goes through the index kernel.  Same chunks, same
+    # form, same kernels otherwise: bit-identical outputs and states.
+    lens = [300, 0, 1000, 64, 5]
+    inp = O.make_prefill_inputs(lens, seed=27)
+    T, N = sum(lens), len(lens)
+    print(f"prefill self index vs index kernel form={form} T={T}", flush=True)
+    d = to_dev(inp, cuda_device)
+    o_s, s_s = run_gpu(d, cuda_device, variant=FORMS[form], route="chunked")
+    pad = 257 - N
+    d2 = dict(d)
+    d2["cu_seqlens"] = torch.cat([d["cu_seqlens"], torch.full((pad,), T, dtype=d["cu_seqlens"].dtype,
+                                                               device=cuda_device)])
+    d2["state"] = torch.cat([d["state"], torch.zeros((pad, 8, 128, 128), dtype=torch.float32,
+                                                     device=cuda_device)])
+    o_i, s_i = run_gpu(d2, cuda_device, variant=FORMS[form], route="chunked")
+    assert np.array_equal(o_s, o_i)
+    assert np.array_equal(s_s, s_i[:N]) and not s_i[N:].any()
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    check(o_s, s_s, o_ref, s_ref)
+
+
+@pytest.mark.parametrize("form", list(FORMS))
 def test_prefill_forms_extreme_gates(cuda_device, form):
     # Per-head gates around softplus' threshold (x > 20), beta saturated at 0
     # and 1, decays ~1 and so fast that exp(G) underflows inside a chunk.
