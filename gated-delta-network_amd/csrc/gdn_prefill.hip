@@ -17,16 +17,21 @@
 //
 //   1. index  : one workgroup turns cu_seqlens (on the device, never copied
 //               to the host) into the chunk table and per-sequence chunk
-//               offsets, and picks the per-chunk form below.  A zero-length
-//               sequence gets no chunk (the reference's seq-id rule,
-//               fla_kernels.py:63, would misnumber every later sequence).
+//               offsets, and picks the per-chunk form below (for a batch of
+//               few sequences and intra workgroups the intra kernel does this
+//               itself, 1b).  A zero-length sequence gets no chunk (the
+//               reference's seq-id rule, fla_kernels.py:63, would misnumber
+//               every later sequence).  It also records whether cu_seqlens
+//               kept its contract (status words).
 //   2. intra  : per (chunk, v-head): gating, cumsum, K K^T on MFMA, the
 //               64x64 triangular inverse in LDS.  No GVA copies: v-head h
 //               reads q/k head h/2 directly.
 //   3. state  : per (sequence, v-head, 16 columns of V): the serial
 //               recurrence over chunks with the f32 state in MFMA
 //               accumulators; stores the chunk-start state and v_new.
-//   4. output : per (chunk, v-head): o from Q S, the masked Q K^T and v_new.
+//   4. output : per (chunk, v-head): o from Q S, the masked Q K^T and v_new
+//               (after a two-segment scan of one sequence, 3b: with the
+//               second segment's output in the same launch).
 //
 // Two forms of the state-independent per-chunk operands, chosen per batch:
 //   WY form: the intra kernel forms w and u (and K^T fragments); a state step
