@@ -29,7 +29,9 @@ pytestmark = pytest.mark.gpu
 from gdn_amd import prefill  # noqa: E402
 
 # (T, cu_seqlens): padded tails, a leading gap, both, gaps around an empty
-# sequence, and single sequences long enough for the two-segment scan.
+# sequence, and single sequences in buffers long enough for the two-segment
+# scan (whose split point comes from the chunk slots of T, so the sequence
+# may end before or at the second segment).
 CASES = [
     (128, [0, 100]),
     (256, [0, 100, 200]),
@@ -39,6 +41,9 @@ CASES = [
     (2500, [0, 2100]),
     (2500, [130, 2480]),
     (8192, [100, 5100]),
+    (1000, [0, 100]),     # 16 chunk slots: the two-segment scan, its second segment empty
+    (1000, [900, 1000]),
+    (1000, [40, 640]),    # the sequence ends exactly at the second segment's first chunk
 ]
 
 # name -> keyword arguments of prefill.kernel
