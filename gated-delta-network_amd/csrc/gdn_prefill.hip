@@ -133,14 +133,22 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
   __shared__ int s_longest, s_most_chunks, s_chunks;
   const int tid = threadIdx.x;
   if (tid == 0) s_longest = s_most_chunks = s_chunks = 0;
-  for (int s = tid; s < N; s += 1024)
-    status[s] = cu_status_bits(raw_cu(cu, cu64, s), raw_cu(cu, cu64, s + 1), T);
   __syncthreads();
+  // Sequence s's bounds as given, their contract bits into status[s] (in the
+  // first pass that reads them), and clamped into [0, T].
+  auto bounds = [&](int s, bool write_status, int &bos, int &eos) {
+    const long long lo = raw_cu(cu, cu64, s), hi = raw_cu(cu, cu64, s + 1);
+    if (write_status) status[s] = cu_status_bits(lo, hi, T);
+    bos = static_cast<int>(lo < 0 ? 0 : lo > T ? T : lo);
+    eos = static_cast<int>(hi < 0 ? 0 : hi > T ? T : hi);
+    eos = eos < bos ? bos : eos;
+  };
   if (choose != 0) {
     int longest = 0, nch = 0;
     for (int s = tid; s < N; s += 1024) {
-      int len = load_cu(cu, cu64, s + 1, T) - load_cu(cu, cu64, s, T);
-      len = len < 0 ? 0 : len;
+      int bos, eos;
+      bounds(s, true, bos, eos);
+      const int len = eos - bos;
       longest = len > longest ? len : longest;
       nch += (len + kChunk - 1) / kChunk;
     }
@@ -157,9 +165,8 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
     const int s = base + tid;
     int n = 0;
     if (s < N && !sequential) {
-      const int bos = load_cu(cu, cu64, s, T);
-      int eos = load_cu(cu, cu64, s + 1, T);
-      eos = eos < bos ? bos : eos;
+      int bos, eos;
+      bounds(s, choose == 0, bos, eos);
       n = (eos - bos + kChunk - 1) / kChunk;
       s_bos[tid] = bos;
       s_eos[tid] = eos;
