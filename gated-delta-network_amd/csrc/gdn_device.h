@@ -181,6 +181,55 @@ __device__ __forceinline__ u32x4 pack8(const float *x) {
   return r;
 }
 
+// OCP fp8 (e4m3) through gfx950's scaled conversions (scale 1: the callers
+// apply their own power-of-two scale).  pk4_fp8 packs four floats, element e
+// in byte e (round to nearest even); fp8x8_to_bf16 widens eight such bytes
+// (element e in byte e of d0:d1) to bf16, exactly: e4m3's 4 significant bits
+// and exponent range fit bf16.
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk4_fp8(float a, float b, float c, float d) {
+  s16x2 o = {0, 0};
+  o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o, a, b, 1.0f, false);
+  o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o, c, d, 1.0f, true);
+  return __builtin_bit_cast(uint32_t, o);
+}
+__device__ __forceinline__ u32x4 fp8x8_to_bf16(uint32_t d0, uint32_t d1) {
+  u32x4 r;
+  r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, false));
+  r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d0, 1.0f, true));
+  r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, false));
+  r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d1, 1.0f, true));
+  return r;
+}
+
+// Power-of-two scale for the fp8 low part of a bf16 split of values whose
+// largest magnitude is m: with hi rounded to nearest, |x - hi| <= 2^-8 |x|
+// < 2^(e-8) for m = f 2^e, f in [0.5, 1), so 2^s with s = 15 - e maps every
+// low part below 2^7, inside e4m3's range (448), and keeps those within
+// 2^-13 of the largest in its normal range.  Returns 2^s and sets *inv =
+// 2^-s (s clamped to [-126, 126]: both normal floats; m = 0 gives 2^126).
+__device__ __forceinline__ float fp8_lo_scale(float m, float *inv) {
+  const int e = static_cast<int>((__float_as_uint(m) >> 23) & 0xffu) - 126;
+  int s = 15 - e;
+  s = s < -126 ? -126 : (s > 126 ? 126 : s);
+  *inv = __uint_as_float(static_cast<uint32_t>(127 - s) << 23);
+  return __uint_as_float(static_cast<uint32_t>(127 + s) << 23);
+}
+
+// Largest value over the wave (every lane receives it): DPP within each row
+// of 16 lanes, then the four row results through readlane.
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp<0xB1>(x));
+  x = fmaxf(x, dpp<0x4E>(x));
+  x = fmaxf(x, dpp<0x141>(x));
+  x = fmaxf(x, dpp<0x140>(x));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // Unpacks 8 bf16 (as produced by pack8 / loaded from memory) to floats.
 __device__ __forceinline__ void unpack8(const u32x4 p, float *x) {
 #pragma unroll

@@ -373,7 +373,11 @@ __device__ __forceinline__ bool chunk_head_of(int id, int nt, const Heads &H, in
 // reads: u as MFMA result tiles, w as hi/lo A-operand fragments, K^T as
 // A-operand fragments.
 constexpr int kABlk = 16 * 20;  // one 16x16 f32 block of A, rows padded to 20
-constexpr int kIntraWyLds = kChunk * kStrideK * 2 + 10 * kABlk * 4 + 3 * kChunk * 4;
+// The w region of one (chunk, head) in the WY form (32 KB): the bf16 hi
+// plane (16 KB), the fp8 lo plane (8 KB), then lo's inverse scale (a float).
+constexpr uint32_t kWLoOff = kChunk * kDK * 2;
+constexpr uint32_t kWScaleOff = kWLoOff + kChunk * kDK;
+constexpr int kIntraWyLds = kChunk * kStrideK * 2 + 10 * kABlk * 4 + 3 * kChunk * 4 + 16;
 // Block (ib, jb), jb <= ib, of the compact lower-triangular A.
 __device__ __forceinline__ int ablk(int ib, int jb) { return (ib * (ib + 1) / 2 + jb) * kABlk; }
 
@@ -444,6 +448,7 @@ __device__ __forceinline__ void wy_intra(
   uint16_t *const sX = reinterpret_cast<uint16_t *>(smem);                   // [64][136]
   float *const sA = reinterpret_cast<float *>(sX + kChunk * kStrideK);        // 10 blocks
   float *const sBeta = sA + 10 * kABlk, *const sBG = sBeta + kChunk, *const sG = sBG + kChunk;
+  float *const sWmax = sG + kChunk;                                           // max |w| per wave
   float *const scr = reinterpret_cast<float *>(sX);                           // [64][68]
   constexpr int kStrideS = 68;
   static_assert(kChunk * kStrideS * 4 <= kChunk * kStrideK * 2, "w scratch must fit the tile");
@@ -576,13 +581,30 @@ __device__ __forceinline__ void wy_intra(
   if (kW) {
     f32x4 Y[4][2];
     wy_solve(sX, sBG, sA, col0, g, r16, Y);
+    {
+      float m = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(Y[i][nt][r]));
+      m = wave_max(m);
+      if (lane == 0) sWmax[wave] = m;
+    }
     __syncthreads();  // K is dead: its space is the w scratch
-    // w -> hi/lo A-operand fragments [hi | lo][mb][kk][lane][8] (row
-    // 16 mb + r16, features 32 kk + 8 g ..; the hi plane alone serves the
-    // second-segment output), in two passes of 64 features through the f32
-    // scratch: waves 2p, 2p + 1 fill it, then each wave converts two of the
-    // pass's eight fragments.
+    // w -> A-operand fragments (row 16 mb + r16, features 32 kk + 8 g ..):
+    // hi = w rounded to bf16, [mb][kk][lane][8] (this plane alone serves the
+    // second-segment output); lo = (w - hi) 2^s as OCP fp8, [mb][kk / 2]
+    // [lane][kk % 2][8] at byte kWLoOff, 2^-s (one float) at kWScaleOff.  In
+    // two passes of 64 features through the f32 scratch: waves 2p, 2p + 1
+    // fill it, then wave w converts fragments (w, 2p) and (w, 2p + 1) and
+    // stores their low parts as one 16-byte row.
     uint16_t *wf = ws_w + ch_head * (kChunk * kDK * 2);
+    float lo_inv;
+    const float lo_sc = fp8_lo_scale(fmaxf(fmaxf(sWmax[0], sWmax[1]), fmaxf(sWmax[2], sWmax[3])),
+                                     &lo_inv);
+    if (tid == 0) *reinterpret_cast<float *>(reinterpret_cast<char *>(wf) + kWScaleOff) = lo_inv;
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
       if ((wave >> 1) == pass) {
@@ -595,19 +617,25 @@ __device__ __forceinline__ void wy_intra(
               scr[(16 * i + 4 * g + r) * kStrideS + (col0 & 63) + 16 * nt + r16] = Y[i][nt][r];
       }
       __syncthreads();
+      u32x4 lo8;
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        const int fi = 2 * wave + f, mb = fi >> 1, kk2 = fi & 1;
-        const float *row = &scr[(16 * mb + r16) * kStrideS + 32 * kk2 + kg];
+      for (int kk2 = 0; kk2 < 2; ++kk2) {
+        const float *row = &scr[(16 * wave + r16) * kStrideS + 32 * kk2 + kg];
         const f32x4 x0 = *reinterpret_cast<const f32x4 *>(row);
         const f32x4 x1 = *reinterpret_cast<const f32x4 *>(row + 4);
         const float x8[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        u32x4 hi, lo;
-        split8(x8, hi, lo);
-        uint16_t *dst = wf + ((mb * 4 + 2 * pass + kk2) * 64 + lane) * 8;
-        *reinterpret_cast<u32x4 *>(dst) = hi;
-        *reinterpret_cast<u32x4 *>(dst + kChunk * kDK) = lo;
+        const u32x4 hi = pack8(x8);
+        float hf[8];
+        unpack8(hi, hf);
+        float lo[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) lo[e] = (x8[e] - hf[e]) * lo_sc;
+        lo8[2 * kk2] = pk4_fp8(lo[0], lo[1], lo[2], lo[3]);
+        lo8[2 * kk2 + 1] = pk4_fp8(lo[4], lo[5], lo[6], lo[7]);
+        *reinterpret_cast<u32x4 *>(wf + ((wave * 4 + 2 * pass + kk2) * 64 + lane) * 8) = hi;
       }
+      *reinterpret_cast<u32x4 *>(reinterpret_cast<char *>(wf) + kWLoOff + wave * 2048 +
+                                 pass * 1024 + lane * 16) = lo8;
       __syncthreads();
     }
     if (kU) {
@@ -929,50 +957,62 @@ void prefill_intra_either_kernel(
 // ---------------------------------------------------------------------------
 // 3. state recurrence: the two forms of a step, then the kernel.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kWBytes = kChunk * kDK * 4;    // w of one (chunk, head): hi + lo bf16
+constexpr uint32_t kWBytes = kChunk * kDK * 4;    // w region of one (chunk, head)
 constexpr uint32_t kKtBytes = kDK * kChunk * 2;   // K^T of one (chunk, q/k head)
 constexpr uint32_t kUBytes = kChunk * kDV * 4;    // u of one (chunk, head), f32
 
 struct WyFrag {
-  u32x4 wh[4], wl[4];  // w rows 16*wave + (lane & 15), k-steps 0..3 (hi / lo)
+  u32x4 wh[4];         // w rows 16*wave + (lane & 15), k-steps 0..3 (bf16 hi)
+  u32x4 wl8[2];        // the same rows' low parts, fp8, k-steps (0, 1) and (2, 3)
+  float wls;           // the low parts' inverse scale
   u32x4 ka[2][2];      // K^T rows 16*(2*wave + mi) + (lane & 15), k-steps 0..1
   f32x4 u;             // u[16*rw + 4*(lane >> 4) + r][vw + (lane & 15)]
   f32x4 dcy;           // exp(G_last - G_i) of the lane's four v_new rows
   float eg;            // exp(G_last)
 };
 
-template <bool LOAD_U>
-__device__ __forceinline__ void load_wy_frag(WyFrag &f, int c, int h, const Heads &H,
-                                                int vw, int wave, int lane, const float *ws_dcy,
-                                                const float *ws_eg, const uint16_t *ws_w,
-                                                const float *ws_u, const uint16_t *ws_kt) {
-  const int q4 = 4 * (lane >> 4);
+// The fragments of chunk c, in seven parts of at most two loads that the
+// state step issues at seven points of the step before (so that no wave
+// issues a burst of loads and waits for the texture unit): 0-1 K^T, 2-3 w hi,
+// 4 w lo, 5 u and the decay factors, 6 exp(G_last) and w lo's scale.
+template <int PART, bool LOAD_U>
+__device__ __forceinline__ void load_wy_part(WyFrag &f, int c, int h, const Heads &H,
+                                             int vw, int wave, int lane, const float *ws_dcy,
+                                             const float *ws_eg, const uint16_t *ws_w,
+                                             const float *ws_u, const uint16_t *ws_kt) {
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
-  // w: [hi | lo][mb][kk][lane][8] fragments of this wave's 16 rows
+  // w: hi [mb][kk][lane][8] and fp8 lo [mb][kk / 2][lane][kk % 2][8]
+  // fragments of this wave's 16 rows, and lo's inverse scale
   const auto rw = buf_rsrc(ws_w + ch_head * (kWBytes / 2), kWBytes);
   const uint32_t wo = static_cast<uint32_t>(wave) * 4096u + static_cast<uint32_t>(lane) * 16u;
+  const uint32_t lo = kWLoOff + static_cast<uint32_t>(wave) * 2048u + static_cast<uint32_t>(lane) * 16u;
+  if constexpr (PART <= 1) {
+    // K^T: [mt][kk][lane][8] fragments of this wave's two 16-row tiles
+    const auto rk = buf_rsrc(ws_kt + (static_cast<size_t>(c) * H.qk + h / H.ratio) * (kKtBytes / 2), kKtBytes);
+    const uint32_t ko = static_cast<uint32_t>(wave) * 4096u + static_cast<uint32_t>(lane) * 16u;
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    f.wh[kk] = buf_load16(rw, wo + kk * 1024);
-    f.wl[kk] = buf_load16(rw, wo + kk * 1024 + kWBytes / 2);
-  }
-  // K^T: [mt][kk][lane][8] fragments of this wave's two 16-row tiles
-  const auto rk = buf_rsrc(ws_kt + (static_cast<size_t>(c) * H.qk + h / H.ratio) * (kKtBytes / 2), kKtBytes);
-  const uint32_t ko = static_cast<uint32_t>(wave) * 4096u + static_cast<uint32_t>(lane) * 16u;
+    for (int kk = 0; kk < 2; ++kk) f.ka[PART][kk] = buf_load16(rk, ko + PART * 2048 + kk * 1024);
+  } else if constexpr (PART <= 3) {
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) f.ka[mi][kk] = buf_load16(rk, ko + mi * 2048 + kk * 1024);
-  // u: [row tile][col tile][lane][4] result tiles
-  if constexpr (LOAD_U) {
-    const auto ru = buf_rsrc(ws_u + ch_head * (kUBytes / 4), kUBytes);
-    f.u = __builtin_bit_cast(f32x4, buf_load16(ru, static_cast<uint32_t>((wave * 8 + (vw >> 4)) * 64 + lane) * 16u));
+    for (int kk = 2 * (PART - 2); kk < 2 * (PART - 1); ++kk) f.wh[kk] = buf_load16(rw, wo + kk * 1024);
+  } else if constexpr (PART == 4) {
+    f.wl8[0] = buf_load16(rw, lo);
+    f.wl8[1] = buf_load16(rw, lo + 1024);
+  } else if constexpr (PART == 5) {
+    const int q4 = 4 * (lane >> 4);
+    // u: [row tile][col tile][lane][4] result tiles
+    if constexpr (LOAD_U) {
+      const auto ru = buf_rsrc(ws_u + ch_head * (kUBytes / 4), kUBytes);
+      f.u = __builtin_bit_cast(f32x4, buf_load16(ru, static_cast<uint32_t>((wave * 8 + (vw >> 4)) * 64 + lane) * 16u));
+    } else {
+      f.u = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const auto rd = buf_rsrc(ws_dcy + ch_head * kChunk, kChunk * 4);
+    f.dcy = __builtin_bit_cast(f32x4, buf_load16(rd, static_cast<uint32_t>(16 * wave + q4) * 4u));
   } else {
-    f.u = f32x4{0.f, 0.f, 0.f, 0.f};
+    f.eg = buf_load_f32(ws_eg + ch_head);
+    f.wls = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rw, kWScaleOff, 0, 0));
   }
-  const auto rd = buf_rsrc(ws_dcy + ch_head * kChunk, kChunk * 4);
-  f.dcy = __builtin_bit_cast(f32x4, buf_load16(rd, static_cast<uint32_t>(16 * wave + q4) * 4u));
-  f.eg = buf_load_f32(ws_eg + ch_head);
 }
 
 // WY form of a state step (see the kernel comment): wave w owns K-rows
@@ -1015,11 +1055,22 @@ __device__ __forceinline__ void wy_state(
     }
   }
 
-  // One chunk of the recurrence, from the prefetched fragments f.
-  auto step = [&](const WyFrag &f, int c) {
+  // One chunk of the recurrence, from the prefetched fragments f, while the
+  // fragments of chunk cn go into g (free since the step before) in seven
+  // parts, each pinned between scheduling barriers where the wave would wait
+  // anyway: at the start of (a) (for the update's results), before each
+  // barrier, after (b)'s and (d)'s LDS reads, and among (b)'s and (d)'s MFMAs.
+  auto chunk_at = [&](int i) { return c0 + (i < npre ? i : npre - 1); };
+#define GDN_PART(P, G, I)                                                                     \
+  __builtin_amdgcn_sched_barrier(0);                                                          \
+  load_wy_part<P, !MAP>(G, chunk_at(I), h, H, vw, wave, lane, ws_dcy, ws_eg, ws_w, ws_u,    \
+                        ws_kt);                                                               \
+  __builtin_amdgcn_sched_barrier(0)
+  auto step = [&](const WyFrag &f, int c, WyFrag &g, int cn) {
     const size_t ch_head = static_cast<size_t>(c) * H.v + h;
     uint16_t *ht = ws_ht + (static_cast<size_t>(c - ht_c0) * H.v + h) * (kDV * kDK);
     uint16_t *vnt = ws_vnt + ch_head * (kDV * kChunk);
+    GDN_PART(0, g, cn);
     // (a) chunk-start state: split copy into LDS ([v][k]) for w S, and a bf16
     //     copy ([v][k]) for the output kernel.
 #pragma unroll
@@ -1034,18 +1085,30 @@ __device__ __forceinline__ void wy_state(
       *reinterpret_cast<u32x2 *>(&sSl[vl * kStrideK + kr]) = lo;
       *reinterpret_cast<u32x2 *>(ht + (vw + r16) * kDK + kr) = rn;
     }
+    GDN_PART(1, g, cn);
     __syncthreads();
 
     // (b) w S for rows 16*wave..+15; three independent accumulation chains
-    //     (hi*hi, hi*lo, lo*hi) shorten the dependent MFMA sequence.
+    //     (hi*hi, hi*lo, lo*hi) shorten the dependent MFMA sequence.  w's
+    //     low part is widened from fp8 to bf16 here, at its use (exact), and
+    //     its scale applied to the lo*hi chain in (c).
     f32x4 P0 = {0.f, 0.f, 0.f, 0.f}, P1 = P0, P2 = P0;
+    u32x4 sh[4], sl[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const u32x4 sh = *reinterpret_cast<const u32x4 *>(&sSh[(lc + r16) * kStrideK + 32 * kk + kg]);
-      const u32x4 sl = *reinterpret_cast<const u32x4 *>(&sSl[(lc + r16) * kStrideK + 32 * kk + kg]);
-      P0 = mfma_bf16(f.wh[kk], sh, P0);
-      P1 = mfma_bf16(f.wh[kk], sl, P1);
-      P2 = mfma_bf16(f.wl[kk], sh, P2);
+      sh[kk] = *reinterpret_cast<const u32x4 *>(&sSh[(lc + r16) * kStrideK + 32 * kk + kg]);
+      sl[kk] = *reinterpret_cast<const u32x4 *>(&sSl[(lc + r16) * kStrideK + 32 * kk + kg]);
+    }
+    GDN_PART(2, g, cn);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 wl = fp8x8_to_bf16(f.wl8[kk >> 1][2 * (kk & 1)], f.wl8[kk >> 1][2 * (kk & 1) + 1]);
+      P0 = mfma_bf16(f.wh[kk], sh[kk], P0);
+      P1 = mfma_bf16(f.wh[kk], sl[kk], P1);
+      P2 = mfma_bf16(wl, sh[kk], P2);
+      if (kk == 1) {
+        GDN_PART(3, g, cn);
+      }
     }
 
     // (c) v_new = u - w S -> workspace (bf16, [v][token]) for the output
@@ -1055,7 +1118,7 @@ __device__ __forceinline__ void wy_state(
       float vn[4], vs[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        vn[r] = f.u[r] - ((P0[r] + P1[r]) + P2[r]);
+        vn[r] = f.u[r] - ((P0[r] + P1[r]) + P2[r] * f.wls);
         vs[r] = f.dcy[r] * vn[r];
       }
       const u32x2 rn = {pk_bf16(vn[0], vn[1]), pk_bf16(vn[2], vn[3])};
@@ -1068,60 +1131,72 @@ __device__ __forceinline__ void wy_state(
       *reinterpret_cast<u32x2 *>(&sVh[vl * kStrideT + i0]) = hi;
       *reinterpret_cast<u32x2 *>(&sVl[vl * kStrideT + i0]) = lo;
     }
+    GDN_PART(4, g, cn);
     __syncthreads();
 
     // (d) S <- exp(G_last) S + K^T (exp(G_last - G) v_new); K is exact in bf16,
     //     so two MFMAs (hi, lo) per k-step, in two independent chains.
+    u32x4 vh[2], vl[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      vh[kk] = *reinterpret_cast<const u32x4 *>(&sVh[(lc + r16) * kStrideT + 32 * kk + kg]);
+      vl[kk] = *reinterpret_cast<const u32x4 *>(&sVl[(lc + r16) * kStrideT + 32 * kk + kg]);
+    }
+    GDN_PART(5, g, cn);
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
+      if (mi == 1) {
+        GDN_PART(6, g, cn);
+      }
       f32x4 acc = S[mi];
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[r] *= f.eg;
       f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const u32x4 vh = *reinterpret_cast<const u32x4 *>(&sVh[(lc + r16) * kStrideT + 32 * kk + kg]);
-        const u32x4 vl = *reinterpret_cast<const u32x4 *>(&sVl[(lc + r16) * kStrideT + 32 * kk + kg]);
-        acc = mfma_bf16(f.ka[mi][kk], vh, acc);
-        acc2 = mfma_bf16(f.ka[mi][kk], vl, acc2);
+        acc = mfma_bf16(f.ka[mi][kk], vh[kk], acc);
+        acc2 = mfma_bf16(f.ka[mi][kk], vl[kk], acc2);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) S[mi][r] = acc[r] + acc2[r];
     }
   };
 
-  // Ring of three fragment sets: chunk i uses set i % 3 while the sets of
-  // chunks i + 1 and i + 2 are in flight.  The loop body is three straight
-  // steps with one exit test, at the back edge, so the loop head is reached
-  // with the same loads pending from both of its predecessors and the
-  // compiler waits for exactly the set in use (an exit after each step made it
-  // merge those paths and wait for nearly every prefetch).  The last 0-2
-  // chunks run after the loop.  Prefetches are clamped to npre chunks, a
-  // bound known at launch (for one sequence, from T), so the first ones go
-  // out before the chunk count arrives from memory; past the last chunk they
-  // re-read a chunk slot of the workspace and are never used.  (A fourth set
-  // measured slower: the extra registers push accumulators into AGPRs.)
+  // Ring of three fragment sets: chunk i uses set i % 3 while the set of
+  // chunk i + 1 is in flight and that of chunk i + 2 goes out during the step.
+  // The loop body is three straight steps with one exit test, at the back
+  // edge, so the loop head is reached with the same loads pending from both
+  // of its predecessors and the compiler waits for exactly the set in use (an
+  // exit after each step made it merge those paths and wait for nearly every
+  // prefetch).  The last 0-2 chunks run after the loop.  Prefetches are
+  // clamped to npre chunks, a bound known at launch (for one sequence, from
+  // T), so the first ones go out before the chunk count arrives from memory;
+  // past the last chunk they re-read a chunk slot of the workspace and are
+  // never used.  (A fourth set measured slower: the extra registers push
+  // accumulators into AGPRs.)
   if (npre > 0) {
-    auto chunk_at = [&](int i) { return c0 + (i < npre ? i : npre - 1); };
     WyFrag fa, fb, fc;
-#define GDN_LOAD(F, I) \
-    load_wy_frag<!MAP>(F, chunk_at(I), h, H, vw, wave, lane, ws_dcy, ws_eg, ws_w, ws_u, ws_kt)
-    GDN_LOAD(fa, 0);
-    GDN_LOAD(fb, 1);
-    GDN_LOAD(fc, 2);
+    auto load_all = [&](WyFrag &g, int i) {
+      GDN_PART(0, g, i);
+      GDN_PART(1, g, i);
+      GDN_PART(2, g, i);
+      GDN_PART(3, g, i);
+      GDN_PART(4, g, i);
+      GDN_PART(5, g, i);
+      GDN_PART(6, g, i);
+    };
+    load_all(fa, 0);
+    load_all(fb, 1);
     int ci = 0;
     for (; ci + 3 <= nch; ci += 3) {
-      step(fa, c0 + ci);
-      GDN_LOAD(fa, ci + 3);
-      step(fb, c0 + ci + 1);
-      GDN_LOAD(fb, ci + 4);
-      step(fc, c0 + ci + 2);
-      GDN_LOAD(fc, ci + 5);
+      step(fa, c0 + ci, fc, ci + 2);
+      step(fb, c0 + ci + 1, fa, ci + 3);
+      step(fc, c0 + ci + 2, fb, ci + 4);
     }
-    if (ci < nch) step(fa, c0 + ci);
-    if (ci + 1 < nch) step(fb, c0 + ci + 1);
-#undef GDN_LOAD
+    if (ci < nch) step(fa, c0 + ci, fc, ci + 2);
+    if (ci + 1 < nch) step(fb, c0 + ci + 1, fa, ci + 3);
   }
+#undef GDN_PART
 
   // Final state (zeros for a zero-length sequence, as the reference).
 #pragma unroll

@@ -446,13 +446,24 @@ def test_prefill_stage_intermediates(cuda_device, form):
         ut = arr("u", np.float32, (L["nt"], 8, 4, 8, 4, 16, 4))[:nt]  # lane = (g, r16)
         u = ut.transpose(0, 1, 2, 4, 6, 3, 5).reshape(nt, 8, 64, 128)
         assert np.abs(u - it["u"]).max() <= 1e-4 * np.abs(it["u"]).max()
-        # w: A fragments [c][h][hi | lo][mb][kk][lane][8] holding
-        # w[16mb + (lane & 15)][32kk + 8(lane >> 4) + e]
-        wf = arr("w", np.uint16, (L["nt"], 8, 2, 4, 4, 4, 16, 8))[:nt]  # lane = (g, r16)
-        wv = (O.bf16_from_bits(wf[:, :, 0]).astype(np.float64)
-              + O.bf16_from_bits(wf[:, :, 1]))                         # [c,h,mb,kk,g,r16,e]
+        # w (32 KB per chunk and head): A fragments holding
+        # w[16mb + (lane & 15)][32kk + 8(lane >> 4) + e] as hi = bf16 [mb][kk][lane][8]
+        # (16 KB), lo = OCP fp8 e4m3 [mb][kk / 2][lane][kk % 2][8] (8 KB), and lo's
+        # inverse power-of-two scale (f32 at byte 24576): w = hi + lo * scale
+        reg = arr("w", np.uint8, (L["nt"], 8, 32768))[:nt]
+        hi = np.ascontiguousarray(reg[..., :16384]).view(np.uint16).reshape(nt, 8, 4, 4, 4, 16, 8)
+        lo = _e4m3(reg[..., 16384:24576].reshape(nt, 8, 4, 2, 4, 16, 2, 8))
+        lo = lo.transpose(0, 1, 2, 3, 6, 4, 5, 7).reshape(nt, 8, 4, 4, 4, 16, 8)
+        inv = np.ascontiguousarray(reg[..., 24576:24580]).view(np.float32)[..., 0]  # [c, h]
+        assert (inv > 0).all() and (np.log2(inv) == np.round(np.log2(inv))).all()
+        assert np.abs(lo).max() < 128  # the scale keeps e4m3 away from its range end
+        wv = (O.bf16_from_bits(hi).astype(np.float64)
+              + lo * inv[:, :, None, None, None, None, None])           # [c,h,mb,kk,g,r16,e]
         w = wv.transpose(0, 1, 2, 5, 3, 4, 6).reshape(nt, 8, 64, 128)
+        # hi is w rounded to bf16 (nearest), lo its remainder to 4 significant bits
         assert np.abs(w - it["w"]).max() <= 1e-4 * np.abs(it["w"]).max()
+        hw = O.bf16_from_bits(hi).transpose(0, 1, 2, 5, 3, 4, 6).reshape(nt, 8, 64, 128)
+        assert (hw == O.bf16_round(it["w"].astype(np.float32))).mean() > 0.99
     else:
         # T = (I + A)^-1 in the w region: A fragments [c][h][rt][kk][lane][hi 8 | lo 8]
         # holding T[16rt + (lane & 15)][32kk + 8(lane >> 4) + e]
@@ -483,6 +494,16 @@ def test_prefill_stage_intermediates(cuda_device, form):
     vnt = O.bf16_from_bits(arr("vnt", np.uint16, (L["nt"], 8, 128, 64))[:nt])
     assert np.abs(vnt - it["v_new"].transpose(0, 1, 3, 2)).max() <= \
         1e-2 * np.abs(it["v_new"]).max()
+
+
+def _e4m3(bits):
+    """OCP fp8 e4m3 (bias 7, no infinities; 0x7f/0xff are NaN) to float64."""
+    bits = np.asarray(bits, np.int64)
+    sign = np.where(bits & 0x80, -1.0, 1.0)
+    e, m = (bits >> 3) & 0xF, bits & 7
+    val = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * 2.0 ** (e - 7.0))
+    val = np.where((e == 15) & (m == 7), np.nan, val)
+    return sign * val
 
 
 def _stream(dev):
