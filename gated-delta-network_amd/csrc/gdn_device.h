@@ -39,6 +39,14 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t 
   lo = pk_bf16(a - __uint_as_float(ua), b - __uint_as_float(ub));
 }
 
+// The same split with hi rounded to nearest even (x - hi is still exact), so
+// that hi is also x's bf16 value: one copy serves both the split products and
+// a bf16 image of x.
+__device__ __forceinline__ void split2_rne(float a, float b, uint32_t &hi, uint32_t &lo) {
+  hi = pk_bf16(a, b);
+  lo = pk_bf16(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+}
+
 // Data-parallel-primitive lane moves.  CTRL is a DPP control word:
 //   0xB1 quad_perm[1,0,3,2] (lane ^ 1)   0x4E quad_perm[2,3,0,1] (lane ^ 2)
 //   0x141 row_half_mirror (i <-> 7-i within 8 lanes)

@@ -1025,7 +1025,7 @@ __device__ __forceinline__ void load_wy_part(WyFrag &f, int c, int h, const Head
 // rows v0..v0+15 of the identity as the start, u = 0 (no u loads), no v_new
 // stores; ht then receives M over the chunks before c (rows j = v0..v0+15 of
 // [j][k]) at chunk index c - ht_c0.
-constexpr int kStateWyLds = 2 * 16 * kStrideK * 2 + 2 * 16 * kStrideT * 2;
+constexpr int kStateWyLds = 2 * 16 * kStrideK * 2 + 3 * 16 * kStrideT * 2;
 template <bool MAP>
 __device__ __forceinline__ void wy_state(
     char *smem, int c0, int nch, int npre, int h, int v0, int wave, int lane, size_t sbase,
@@ -1040,6 +1040,7 @@ __device__ __forceinline__ void wy_state(
   uint16_t *const sSl = sSh + 16 * kStrideK;
   uint16_t *const sVh = sSl + 16 * kStrideK;
   uint16_t *const sVl = sVh + 16 * kStrideT;
+  uint16_t *const sN = sVl + 16 * kStrideT;  // v_new, bf16 [v][token]
 
   f32x4 S[2];
 #pragma unroll
@@ -1071,22 +1072,27 @@ __device__ __forceinline__ void wy_state(
     uint16_t *ht = ws_ht + (static_cast<size_t>(c - ht_c0) * H.v + h) * (kDV * kDK);
     uint16_t *vnt = ws_vnt + ch_head * (kDV * kChunk);
     GDN_PART(0, g, cn);
-    // (a) chunk-start state: split copy into LDS ([v][k]) for w S, and a bf16
-    //     copy ([v][k]) for the output kernel.
+    // (a) chunk-start state: split copy into LDS ([v][k]) for w S, whose hi
+    //     half (rounded to nearest) is also the bf16 chunk-start state of the
+    //     output kernel.
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
       const int kr = 16 * (2 * wave + mi) + q4, vl = lc + r16;
       uint32_t h0, h1, l0, l1;
-      split2(S[mi][0], S[mi][1], h0, l0);
-      split2(S[mi][2], S[mi][3], h1, l1);
-      const u32x2 hi = {h0, h1}, lo = {l0, l1};
-      const u32x2 rn = {pk_bf16(S[mi][0], S[mi][1]), pk_bf16(S[mi][2], S[mi][3])};
-      *reinterpret_cast<u32x2 *>(&sSh[vl * kStrideK + kr]) = hi;
-      *reinterpret_cast<u32x2 *>(&sSl[vl * kStrideK + kr]) = lo;
-      *reinterpret_cast<u32x2 *>(ht + (vw + r16) * kDK + kr) = rn;
+      split2_rne(S[mi][0], S[mi][1], h0, l0);
+      split2_rne(S[mi][2], S[mi][3], h1, l1);
+      *reinterpret_cast<u32x2 *>(&sSh[vl * kStrideK + kr]) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2 *>(&sSl[vl * kStrideK + kr]) = u32x2{l0, l1};
     }
     GDN_PART(1, g, cn);
     __syncthreads();
+    // ht: the workgroup's 16 rows of the bf16 chunk-start state ([v][k], 4 KB
+    // contiguous) from the LDS copy, one 16-byte store per thread
+    {
+      const int t = threadIdx.x, row = t >> 4, k0 = (t & 15) * 8;
+      *reinterpret_cast<u32x4 *>(ht + (vw + row) * kDK + k0) =
+          *reinterpret_cast<const u32x4 *>(&sSh[(lc + row) * kStrideK + k0]);
+    }
 
     // (b) w S for rows 16*wave..+15; three independent accumulation chains
     //     (hi*hi, hi*lo, lo*hi) shorten the dependent MFMA sequence.  w's
@@ -1127,12 +1133,19 @@ __device__ __forceinline__ void wy_state(
       split2(vs[2], vs[3], h1, l1);
       const u32x2 hi = {h0, h1}, lo = {l0, l1};
       const int i0 = 16 * wave + q4;
-      if constexpr (!MAP) *reinterpret_cast<u32x2 *>(vnt + (vw + r16) * kChunk + i0) = rn;
+      if constexpr (!MAP) *reinterpret_cast<u32x2 *>(&sN[vl * kStrideT + i0]) = rn;
       *reinterpret_cast<u32x2 *>(&sVh[vl * kStrideT + i0]) = hi;
       *reinterpret_cast<u32x2 *>(&sVl[vl * kStrideT + i0]) = lo;
     }
     GDN_PART(4, g, cn);
     __syncthreads();
+    // v_new: the workgroup's 16 rows of [v][token] bf16 (2 KB contiguous) from
+    // the LDS copy, one 8-byte store per thread
+    if constexpr (!MAP) {
+      const int t = threadIdx.x, row = t >> 4, i0 = (t & 15) * 4;
+      *reinterpret_cast<u32x2 *>(vnt + (vw + row) * kChunk + i0) =
+          *reinterpret_cast<const u32x2 *>(&sN[(lc + row) * kStrideT + i0]);
+    }
 
     // (d) S <- exp(G_last) S + K^T (exp(G_last - G) v_new); K is exact in bf16,
     //     so two MFMAs (hi, lo) per k-step, in two independent chains.
@@ -1212,9 +1225,9 @@ struct TFrag {
   u32x4 kf[4];          // K rows 16*wave + (lane & 15), k-steps 0..3 (A operand of K S)
   u32x4 th[2], tl[2];   // T rows 16*wave + (lane & 15), k-steps 0..1 (hi / lo)
   f32x4 beta, bg, dcy;  // beta, beta e^G, exp(G_last - G) of rows 16*wave + 4*(lane >> 4) + r
-  uint32_t vv[4];       // bf16 bits of V[16*wave + 4*(lane >> 4) + r][v0 + (lane & 15)]
-                        // (widened where used: converting at the load let the
-                        // compiler hoist it, and its wait, into the step before)
+  u32x2 vr;             // V[16*wave + (lane >> 2)][v0 + 4*(lane & 3) + 0..3], bf16 (through
+                        // LDS to the rows 16*wave + 4*(lane >> 4) + r of column
+                        // v0 + (lane & 15) that Y needs)
   float eg;             // exp(G_last)
 };
 
@@ -1222,42 +1235,57 @@ struct TFrag {
 struct FragOffsets {
   uint32_t k, t, v, vec;
 };
+__device__ __forceinline__ u32x2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0));
+}
 
-// Fragments of chunk c (tokens [start, start + len)) for v-head h.  T is
-// lower triangular: the rows of waves 0 and 1 (0..31) are zero in columns
-// 32..63, so those waves load (and multiply) only the first k-step.
-__device__ __forceinline__ void load_t_frag(TFrag &f, int c, int start, int len, int h,
-                                                const Heads &H, const FragOffsets &o,
-                                                const uint16_t *k, const uint16_t *v,
-                                                const float *ws_dcy, const float *ws_eg,
-                                                const uint16_t *ws_w, const float *ws_u,
-                                                bool t_upper) {
+// Fragments of chunk c (tokens [start, start + len)) for v-head h, in six
+// parts that the state step issues after the last use of the registers they
+// refill (so that no wave issues all of a set's loads at once): 0 K rows
+// 0..1, 1 K rows 2..3 and the per-token beta, beta e^G, 2 T, 3 V, 4 the decay
+// factors, 5 exp(G_last).  V is one 8-byte load per lane (a row's 16
+// columns in four lanes) instead of four 2-byte loads.  T is lower triangular: the rows of waves 0 and 1
+// (0..31) are zero in columns 32..63, so those waves load (and multiply)
+// only the first k-step.
+template <int PART>
+__device__ __forceinline__ void load_t_part(TFrag &f, int c, int start, int len, int h,
+                                            const Heads &H, const FragOffsets &o,
+                                            const uint16_t *k, const uint16_t *v,
+                                            const float *ws_dcy, const float *ws_eg,
+                                            const uint16_t *ws_w, const float *ws_u,
+                                            bool t_upper) {
   const size_t ch_head = static_cast<size_t>(c) * H.v + h;
   const uint32_t nlen = static_cast<uint32_t>(len);
-  const auto rk = buf_rsrc(k + (static_cast<size_t>(start) * H.qk + h / H.ratio) * kDK,
-                           nlen * static_cast<uint32_t>(H.qk) * (kDK * 2));
+  if constexpr (PART <= 1) {
+    const auto rk = buf_rsrc(k + (static_cast<size_t>(start) * H.qk + h / H.ratio) * kDK,
+                             nlen * static_cast<uint32_t>(H.qk) * (kDK * 2));
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) f.kf[kk] = buf_load16(rk, o.k + kk * 64);
-  const auto rt = buf_rsrc(ws_w + ch_head * (kChunk * kDK * 2), kTElems * 2);  // T, w region
-  f.th[0] = buf_load16(rt, o.t);
-  f.tl[0] = buf_load16(rt, o.t + 16);
-  if (t_upper) {
-    f.th[1] = buf_load16(rt, o.t + 2048);
-    f.tl[1] = buf_load16(rt, o.t + 2048 + 16);
+    for (int kk = 2 * PART; kk < 2 * PART + 2; ++kk) f.kf[kk] = buf_load16(rk, o.k + kk * 64);
+    if constexpr (PART == 1) {
+      const auto rb = buf_rsrc(ws_u + ch_head * (kChunk * kDV), 2 * kChunk * 4);  // (beta, beta e^G)
+      f.beta = __builtin_bit_cast(f32x4, buf_load16(rb, o.vec));
+      f.bg = __builtin_bit_cast(f32x4, buf_load16(rb, o.vec + kChunk * 4));
+    }
+  } else if constexpr (PART == 2) {
+    const auto rt = buf_rsrc(ws_w + ch_head * (kChunk * kDK * 2), kTElems * 2);  // T, w region
+    f.th[0] = buf_load16(rt, o.t);
+    f.tl[0] = buf_load16(rt, o.t + 16);
+    if (t_upper) {
+      f.th[1] = buf_load16(rt, o.t + 2048);
+      f.tl[1] = buf_load16(rt, o.t + 2048 + 16);
+    } else {
+      f.th[1] = f.tl[1] = u32x4{0u, 0u, 0u, 0u};
+    }
+  } else if constexpr (PART == 3) {
+    const auto rv = buf_rsrc(v + (static_cast<size_t>(start) * H.v + h) * kDV,
+                             nlen * static_cast<uint32_t>(H.v) * (kDV * 2));
+    f.vr = buf_load8(rv, o.v);
+  } else if constexpr (PART == 4) {
+    const auto rd = buf_rsrc(ws_dcy + ch_head * kChunk, kChunk * 4);
+    f.dcy = __builtin_bit_cast(f32x4, buf_load16(rd, o.vec));
   } else {
-    f.th[1] = f.tl[1] = u32x4{0u, 0u, 0u, 0u};
+    f.eg = buf_load_f32(ws_eg + ch_head);
   }
-  const auto rv = buf_rsrc(v + (static_cast<size_t>(start) * H.v + h) * kDV,
-                           nlen * static_cast<uint32_t>(H.v) * (kDV * 2));
-  const uint32_t vrow = static_cast<uint32_t>(H.v) * (kDV * 2);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) f.vv[r] = __builtin_amdgcn_raw_buffer_load_b16(rv, o.v + r * vrow, 0, 0);
-  const auto rb = buf_rsrc(ws_u + ch_head * (kChunk * kDV), 2 * kChunk * 4);  // (beta, beta e^G)
-  f.beta = __builtin_bit_cast(f32x4, buf_load16(rb, o.vec));
-  f.bg = __builtin_bit_cast(f32x4, buf_load16(rb, o.vec + kChunk * 4));
-  const auto rd = buf_rsrc(ws_dcy + ch_head * kChunk, kChunk * 4);
-  f.dcy = __builtin_bit_cast(f32x4, buf_load16(rd, o.vec));
-  f.eg = buf_load_f32(ws_eg + ch_head);
 }
 
 // T form of a state step (see the kernel comment): wave w owns K-rows
@@ -1272,7 +1300,8 @@ __device__ __forceinline__ void load_t_frag(TFrag &f, int c, int start, int len,
 // state (K, T, V, the per-token vectors) is prefetched into registers one
 // chunk ahead through buffer descriptors.  K^T, the A operand of the update,
 // is read transposed out of the LDS copy of the chunk's K rows.
-constexpr int kStateTLds = 2 * 16 * kStrideK * 2 + 4 * 16 * kStrideT * 2 + kChunk * kStrideK * 2;
+constexpr int kStateTLds =
+    2 * 16 * kStrideK * 2 + 5 * 16 * kStrideT * 2 + kChunk * kStrideK * 2 + kChunk * 16 * 2;
 __device__ __forceinline__ void t_state(
     char *smem, int c0, int nch, int bos, int eos, int h, int v0, int wave, int lane,
     size_t sbase, const uint16_t *k, const uint16_t *v, const float *state, float *new_state,
@@ -1287,6 +1316,8 @@ __device__ __forceinline__ void t_state(
   uint16_t *const sVh = sYl + 16 * kStrideT;                 // D v_new split, [v][token]
   uint16_t *const sVl = sVh + 16 * kStrideT;
   uint16_t *const sK = sVl + 16 * kStrideT;                  // the chunk's K rows, [token][k]
+  uint16_t *const sN = sK + kChunk * kStrideK;               // v_new, bf16 [v][token]
+  uint16_t *const sV = sN + 16 * kStrideT;                   // the chunk's V slice, [token][16]
 
   f32x4 S[2];
 #pragma unroll
@@ -1301,31 +1332,59 @@ __device__ __forceinline__ void t_state(
   FragOffsets fo;
   fo.k = (static_cast<uint32_t>(16 * wave + r16) * H.qk * kDK + kg) * 2;
   fo.t = static_cast<uint32_t>(wave) * 4096u + static_cast<uint32_t>(lane) * 32u;
-  fo.v = (static_cast<uint32_t>(16 * wave + q4) * H.v * kDV + vc) * 2;
+  fo.v = (static_cast<uint32_t>(16 * wave + (lane >> 2)) * H.v * kDV + v0 + 4 * (lane & 3)) * 2;
   fo.vec = static_cast<uint32_t>(16 * wave + q4) * 4u;
 
-  // One chunk of the recurrence, from the prefetched fragments f.
-  auto step = [&](const TFrag &f, int c) {
+  // Chunk i's fragments, part P (past the last chunk: the last chunk again,
+  // so every step issues the same loads).
+  auto load = [&](auto part, TFrag &f, int i) {
+    i = i < nch ? i : nch - 1;
+    const int start = bos + i * kChunk, rem = eos - start;
+    __builtin_amdgcn_sched_barrier(0);
+    load_t_part<decltype(part)::value>(f, c0 + i, start, rem < kChunk ? rem : kChunk, h, H, fo,
+                                       k, v, ws_dcy, ws_eg, ws_w, ws_u, wave >= 2);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  using TP0 = std::integral_constant<int, 0>;
+  using TP1 = std::integral_constant<int, 1>;
+  using TP2 = std::integral_constant<int, 2>;
+  using TP3 = std::integral_constant<int, 3>;
+  using TP4 = std::integral_constant<int, 4>;
+  using TP5 = std::integral_constant<int, 5>;
+
+  // One chunk of the recurrence, from the prefetched fragments f, which are
+  // refilled with chunk cn's as the step finishes with each part: K rows and
+  // the per-token vectors after (b), T after (c)'s products, V after Y, the
+  // decay factors after (c), exp(G_last) after (d).
+  auto step = [&](TFrag &f, int c, int cn) {
     const size_t ch_head = static_cast<size_t>(c) * H.v + h;
     uint16_t *ht = ws_ht + ch_head * (kDV * kDK);
     uint16_t *vnt = ws_vnt + ch_head * (kDV * kChunk);
-    // (a) chunk-start state: split copy into LDS ([v][k]) for K S, a bf16 copy
-    //     ([v][k]) for the output kernel; the chunk's K rows into LDS.
+    // (a) chunk-start state: split copy into LDS ([v][k]) for K S, whose hi
+    //     half (rounded to nearest) is also the bf16 chunk-start state of the
+    //     output kernel; the chunk's K rows and V slice into LDS.
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
       const int kr = 16 * (2 * wave + mi) + q4;
       uint32_t h0, h1, l0, l1;
-      split2(S[mi][0], S[mi][1], h0, l0);
-      split2(S[mi][2], S[mi][3], h1, l1);
-      const u32x2 rn = {pk_bf16(S[mi][0], S[mi][1]), pk_bf16(S[mi][2], S[mi][3])};
+      split2_rne(S[mi][0], S[mi][1], h0, l0);
+      split2_rne(S[mi][2], S[mi][3], h1, l1);
       *reinterpret_cast<u32x2 *>(&sSh[r16 * kStrideK + kr]) = u32x2{h0, h1};
       *reinterpret_cast<u32x2 *>(&sSl[r16 * kStrideK + kr]) = u32x2{l0, l1};
-      *reinterpret_cast<u32x2 *>(ht + vc * kDK + kr) = rn;
     }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
       *reinterpret_cast<u32x4 *>(&sK[(16 * wave + r16) * kStrideK + 32 * kk + kg]) = f.kf[kk];
+    *reinterpret_cast<u32x2 *>(&sV[(16 * wave + (lane >> 2)) * 16 + 4 * (lane & 3)]) = f.vr;
     __syncthreads();
+    // ht: the workgroup's 16 rows of the bf16 chunk-start state ([v][k], 4 KB
+    // contiguous) from the LDS copy, one 16-byte store per thread (stores of
+    // each lane's own 8 bytes, 32-byte pieces of 16 rows, cost ~20 us at 4x8192)
+    {
+      const int t = threadIdx.x, row = t >> 4, k0 = (t & 15) * 8;
+      *reinterpret_cast<u32x4 *>(ht + (v0 + row) * kDK + k0) =
+          *reinterpret_cast<const u32x4 *>(&sSh[row * kStrideK + k0]);
+    }
 
     // (b) X = K S for tokens 16*wave..+15 (two chains: S hi, S lo), then
     //     Y = beta V - beta e^G X -> LDS (split, [v][token]).  K^T fragments
@@ -1339,10 +1398,14 @@ __device__ __forceinline__ void t_state(
         X0 = mfma_bf16(f.kf[kk], sh, X0);
         X1 = mfma_bf16(f.kf[kk], sl, X1);
       }
+      load(TP0{}, f, cn);
+      // V[16 wave + 4 g + r][v0 + r16], r = 0..3, by one transposing read
+      const u32x2 vt = ds_read_tr16(&sV[(16 * wave + q4 + (r16 >> 2)) * 16 + 4 * (r16 & 3)]);
+      const float vf[4] = {__uint_as_float(vt[0] << 16), __uint_as_float(vt[0] & 0xffff0000u),
+                           __uint_as_float(vt[1] << 16), __uint_as_float(vt[1] & 0xffff0000u)};
       float y[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        y[r] = f.beta[r] * __uint_as_float(f.vv[r] << 16) - f.bg[r] * (X0[r] + X1[r]);
+      for (int r = 0; r < 4; ++r) y[r] = f.beta[r] * vf[r] - f.bg[r] * (X0[r] + X1[r]);
       uint32_t h0, h1, l0, l1;
       split2(y[0], y[1], h0, l0);
       split2(y[2], y[3], h1, l1);
@@ -1350,6 +1413,8 @@ __device__ __forceinline__ void t_state(
       *reinterpret_cast<u32x2 *>(&sYh[r16 * kStrideT + i0]) = u32x2{h0, h1};
       *reinterpret_cast<u32x2 *>(&sYl[r16 * kStrideT + i0]) = u32x2{l0, l1};
     }
+    load(TP1{}, f, cn);
+    load(TP3{}, f, cn);
     u32x4 ka[2][2];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
@@ -1378,6 +1443,7 @@ __device__ __forceinline__ void t_state(
         P1 = mfma_bf16(f.th[kk], yl, P1);
         P2 = mfma_bf16(f.tl[kk], yh, P2);
       }
+      load(TP2{}, f, cn);
       float vn[4], vs[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -1389,11 +1455,19 @@ __device__ __forceinline__ void t_state(
       split2(vs[0], vs[1], h0, l0);
       split2(vs[2], vs[3], h1, l1);
       const int i0 = 16 * wave + q4;
-      *reinterpret_cast<u32x2 *>(vnt + vc * kChunk + i0) = rn;
+      *reinterpret_cast<u32x2 *>(&sN[r16 * kStrideT + i0]) = rn;
       *reinterpret_cast<u32x2 *>(&sVh[r16 * kStrideT + i0]) = u32x2{h0, h1};
       *reinterpret_cast<u32x2 *>(&sVl[r16 * kStrideT + i0]) = u32x2{l0, l1};
     }
+    load(TP4{}, f, cn);
     __syncthreads();
+    // v_new: the workgroup's 16 rows of [v][token] bf16 (2 KB contiguous) from
+    // the LDS copy, one 8-byte store per thread
+    {
+      const int t = threadIdx.x, row = t >> 4, i0 = (t & 15) * 4;
+      *reinterpret_cast<u32x2 *>(vnt + (v0 + row) * kChunk + i0) =
+          *reinterpret_cast<const u32x2 *>(&sN[row * kStrideT + i0]);
+    }
 
     // (d) S <- exp(G_last) S + K^T (D v_new); K is exact in bf16, so two MFMAs
     //     (hi, lo) per k-step, in two independent chains.
@@ -1410,42 +1484,41 @@ __device__ __forceinline__ void t_state(
         acc = mfma_bf16(ka[mi][kk], vh, acc);
         acc2 = mfma_bf16(ka[mi][kk], vl, acc2);
       }
+      if (mi == 1) load(TP5{}, f, cn);
 #pragma unroll
       for (int r = 0; r < 4; ++r) S[mi][r] = acc[r] + acc2[r];
     }
   };
 
   // Two fragment sets: chunk i uses set i % 2 while the set of chunk i + 1
-  // is in flight (a third set does not fit in the registers).  The loop body
-  // is two straight steps with one exit test, at the back edge, so the loop
-  // head is reached with the same loads pending from both of its
-  // predecessors and the compiler waits for exactly the set in use (an exit
-  // after each step made it merge those paths and wait for nearly every
-  // prefetch).  A last odd chunk runs after the loop.  Prefetches past the
-  // last chunk re-read it, so every iteration issues the same loads.
+  // is in flight and its own registers are refilled with chunk i + 2's as
+  // the step finishes with them (a third set does not fit in the
+  // registers).  The loop body is two straight steps with one exit test, at
+  // the back edge, so the loop head is reached with the same loads pending
+  // from both of its predecessors and the compiler waits for exactly the set
+  // in use (an exit after each step made it merge those paths and wait for
+  // nearly every prefetch).  A last odd chunk runs after the loop.  The
+  // scheduling barriers around each part keep the compiler from moving a
+  // load, or work on the other set's registers (with its load waits), across
+  // the step.
   if (nch > 0) {
-    auto load = [&](TFrag &f, int i) {
-      i = i < nch ? i : nch - 1;
-      const int start = bos + i * kChunk, rem = eos - start;
-      load_t_frag(f, c0 + i, start, rem < kChunk ? rem : kChunk, h, H, fo, k, v, ws_dcy, ws_eg,
-                  ws_w, ws_u, wave >= 2);
-    };
     TFrag fa, fb;
-    load(fa, 0);
-    load(fb, 1);
+    auto load_all = [&](TFrag &f, int i) {
+      load(TP0{}, f, i);
+      load(TP1{}, f, i);
+      load(TP2{}, f, i);
+      load(TP3{}, f, i);
+      load(TP4{}, f, i);
+      load(TP5{}, f, i);
+    };
+    load_all(fa, 0);
+    load_all(fb, 1);
     int ci = 0;
-    // (The scheduling barriers keep the compiler from moving work on the
-    // other set's registers into a step, which made it wait for that set's
-    // loads too.)
     for (; ci + 2 <= nch; ci += 2) {
-      step(fa, c0 + ci);
-      __builtin_amdgcn_sched_barrier(0);
-      load(fa, ci + 2);
-      step(fb, c0 + ci + 1);
-      __builtin_amdgcn_sched_barrier(0);
-      load(fb, ci + 3);
+      step(fa, c0 + ci, ci + 2);
+      step(fb, c0 + ci + 1, ci + 3);
     }
-    if (ci < nch) step(fa, c0 + ci);
+    if (ci < nch) step(fa, c0 + ci, ci + 2);
   }
 
   // Final state (zeros for a zero-length sequence, as the reference).
