@@ -388,6 +388,75 @@ __device__ __forceinline__ u32x2 tile_col4(const uint16_t *tile, int r0, int c0,
   return ds_read_tr16(&tile[(r0 + (r16 >> 2)) * kStrideK + c0 + 4 * (r16 & 3)]);
 }
 
+// A = strictly-lower(beta_i exp(G_i - G_j) K K^T) of one chunk from its K
+// rows in LDS (row-major, stride kStrideK), as the ten lower 16x16 blocks of
+// sA (ablk; rows padded to 20 floats).  Wave w computes blocks w, w + 4 and
+// (waves 0, 1) w + 8, the three as independent MFMA chains side by side (one
+// block at a time left each wave waiting on its LDS reads and a 4-deep MFMA
+// chain per block).  G_i - G_j <= 0 for every kept entry (g <= 0); the clamp
+// keeps the others finite; exp is the hardware exp2 of x log2(e) (a few
+// 2^-24 relative, far below the split-bf16 products' 2^-17).
+__device__ __forceinline__ void build_A(const uint16_t *sK, float *sA, const float *sG,
+                                        const float *sBeta, int len, int wave, int lane) {
+  const int r16 = lane & 15, g = lane >> 4, kg = 8 * g;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  int mb[3], nb[3];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    int t = wv + 4 * q;
+    t = t < 10 ? t : 9;  // waves 2, 3 repeat block 9 as their third (not stored)
+    // t = 0..9 -> (mb, nb) = (3,3) (3,2) (3,1) (3,0) (2,2) (2,1) (2,0) (1,1) (1,0) (0,0)
+    mb[q] = t < 4 ? 3 : t < 7 ? 2 : t < 9 ? 1 : 0;
+    nb[q] = t < 4 ? 3 - t : t < 7 ? 6 - t : t < 9 ? 8 - t : 0;
+  }
+  f32x4 acc[3];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const u32x4 af = *reinterpret_cast<const u32x4 *>(&sK[(16 * mb[q] + r16) * kStrideK + 32 * kk + kg]);
+      const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[(16 * nb[q] + r16) * kStrideK + 32 * kk + kg]);
+      acc[q] = mfma_bf16(af, bf, acc[q]);
+    }
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    if (q == 2 && wv >= 2) break;
+    const float Gj = sG[16 * nb[q] + r16];
+    const f32x4 Gi = *reinterpret_cast<const f32x4 *>(&sG[16 * mb[q] + 4 * g]);
+    const f32x4 Bi = *reinterpret_cast<const f32x4 *>(&sBeta[16 * mb[q] + 4 * g]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * mb[q] + 4 * g + r, j = 16 * nb[q] + r16;
+      const float d = __builtin_amdgcn_exp2f(fminf(Gi[r] - Gj, 0.f) * 1.44269504088896341f);
+      const float e = Bi[r] * d * acc[q][r];
+      sA[ablk(mb[q], nb[q]) + (4 * g + r) * 20 + r16] = (i > j && i < len) ? e : 0.f;
+    }
+  }
+}
+
+// Diagonal blocks D_w = (I + A_ww)^-1 in place of A_ww: wave w, lane j < 16
+// solves column j, column-oriented (each solved x_m is applied to all later
+// rows at once, so the serial chain is one FMA per row).  Every read of A_ww
+// precedes the writes in the wave's program order.
+__device__ __forceinline__ void diag_inverse(float *sA, int wave, int lane) {
+  if (lane < 16) {
+    float *Aw = sA + ablk(wave, wave);
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = i == lane ? 1.f : 0.f;
+#pragma unroll
+    for (int m = 0; m < 15; ++m) {
+      const float xm = x[m];
+#pragma unroll
+      for (int i = m + 1; i < 16; ++i) x[i] -= Aw[i * 20 + m] * xm;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) Aw[i * 20 + lane] = x[i];
+  }
+}
+
 // Blocked forward substitution (I + A) Y = diag(scl) X for the 32 columns
 // col0.. of this wave; X row-major in sX ([64][kStrideK] bf16).
 __device__ __forceinline__ void wy_solve(const uint16_t *sX, const float *scl, const float *sA,
@@ -507,28 +576,7 @@ __device__ __forceinline__ void wy_intra(
   }
   __syncthreads();
 
-  // A = strictly-lower(beta_i exp(G_i - G_j) K K^T): its ten lower 16x16
-  // tiles dealt three, three, two and two to the waves.  G_i - G_j <= 0 for
-  // every kept entry (g <= 0); the clamp keeps the others finite.
-  for (int t = wave; t < 10; t += 4) {
-    // t = 0..9 -> (mb, nb) = (3,3) (3,2) (3,1) (3,0) (2,2) (2,1) (2,0) (1,1) (1,0) (0,0)
-    const int mb = t < 4 ? 3 : t < 7 ? 2 : t < 9 ? 1 : 0;
-    const int nb = t < 4 ? 3 - t : t < 7 ? 6 - t : t < 9 ? 8 - t : 0;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const u32x4 af = *reinterpret_cast<const u32x4 *>(&sX[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
-      const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sX[(16 * nb + r16) * kStrideK + 32 * kk + kg]);
-      acc = mfma_bf16(af, bf, acc);
-    }
-    const float Gj = sG[16 * nb + r16];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * mb + 4 * g + r, j = 16 * nb + r16;
-      const float e = sBeta[i] * expf(fminf(sG[i] - Gj, 0.f)) * acc[r];
-      sA[ablk(mb, nb) + (4 * g + r) * 20 + r16] = (i > j && i < len) ? e : 0.f;
-    }
-  }
+  build_A(sX, sA, sG, sBeta, len, wave, lane);
   // K^T as A-operand fragments of the state kernel (one v-head per q/k head
   // writes them): fragment (mt, kk), lane (g, r16) = the 8 tokens 32 kk +
   // 8 g .. of feature 16 mt + r16; wave w writes fragments 4 w .. 4 w + 3.
@@ -549,10 +597,7 @@ __device__ __forceinline__ void wy_intra(
   }
   __syncthreads();
 
-  // Diagonal blocks D_w = (I + A_ww)^-1 in place of A_ww: wave w, lane j < 16
-  // solves column j, column-oriented (each solved x_m is applied to all later
-  // rows at once, so the serial chain is one FMA per row).  Every read of
-  // A_ww precedes the writes in the wave's program order.
+  // Diagonal blocks D_w = (I + A_ww)^-1 in place of A_ww (diag_inverse).
   if (kU && !kW) {
     // the u-only half: K is dead once A is built, V takes its place
 #pragma unroll
@@ -561,20 +606,7 @@ __device__ __forceinline__ void wy_intra(
       *reinterpret_cast<u32x4 *>(&sX[(idx >> 4) * kStrideK + (idx & 15) * 8]) = vrows[i];
     }
   }
-  if (lane < 16) {
-    float *Aw = sA + ablk(wave, wave);
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = i == lane ? 1.f : 0.f;
-#pragma unroll
-    for (int m = 0; m < 15; ++m) {
-      const float xm = x[m];
-#pragma unroll
-      for (int i = m + 1; i < 16; ++i) x[i] -= Aw[i * 20 + m] * xm;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) Aw[i * 20 + lane] = x[i];
-  }
+  diag_inverse(sA, wave, lane);
   __syncthreads();
 
   const int col0 = 32 * wave;
@@ -737,51 +769,10 @@ __device__ __forceinline__ void t_intra(
   }
   __syncthreads();
 
-  // A = strictly-lower(beta_i exp(G_i - G_j) K K^T): its ten lower 16x16
-  // tiles dealt three, three, two and two to the waves.  G_i - G_j <= 0 for
-  // every kept entry (g <= 0); the clamp keeps the others finite.
-  {
-    const int wv = __builtin_amdgcn_readfirstlane(wave);
-    for (int t = wv; t < 10; t += 4) {
-      // t = 0..9 -> (mb, nb) = (3,3) (3,2) (3,1) (3,0) (2,2) (2,1) (2,0) (1,1) (1,0) (0,0)
-      const int mb = t < 4 ? 3 : t < 7 ? 2 : t < 9 ? 1 : 0;
-      const int nb = t < 4 ? 3 - t : t < 7 ? 6 - t : t < 9 ? 8 - t : 0;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const u32x4 af = *reinterpret_cast<const u32x4 *>(&sK[(16 * mb + r16) * kStrideK + 32 * kk + kg]);
-        const u32x4 bf = *reinterpret_cast<const u32x4 *>(&sK[(16 * nb + r16) * kStrideK + 32 * kk + kg]);
-        acc = mfma_bf16(af, bf, acc);
-      }
-      const float Gj = sG[16 * nb + r16];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * mb + 4 * g + r, j = 16 * nb + r16;
-        const float e = sBeta[i] * expf(fminf(sG[i] - Gj, 0.f)) * acc[r];
-        sA[ablk(mb, nb) + (4 * g + r) * 20 + r16] = (i > j && i < len) ? e : 0.f;
-      }
-    }
-  }
+  build_A(sK, sA, sG, sBeta, len, wave, lane);
   __syncthreads();
 
-  // Diagonal blocks D_w = (I + A_ww)^-1 in place of A_ww: wave w, lane j < 16
-  // solves column j, column-oriented (each solved x_m is applied to all
-  // later rows at once, so the serial chain is one FMA per row); every read
-  // of A_ww precedes the wave's writes.
-  if (lane < 16) {
-    float *Aw = sA + ablk(wave, wave);
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = i == lane ? 1.f : 0.f;
-#pragma unroll
-    for (int m = 0; m < 15; ++m) {
-      const float xm = x[m];
-#pragma unroll
-      for (int i = m + 1; i < 16; ++i) x[i] -= Aw[i * 20 + m] * xm;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) Aw[i * 20 + lane] = x[i];
-  }
+  diag_inverse(sA, wave, lane);  // D_w = (I + A_ww)^-1 in place of A_ww
   __syncthreads();
 
   // Block column j = wave of T.  Tiles in MFMA result order: lane holds
