@@ -157,6 +157,7 @@ def test_prefill_config4_long_context(cuda_device):
 
 # Forms of the per-chunk operands (variant): 0 WY, 1 T.
 FORMS = {"wy": 0, "t": 1}
+CHAIN_WY, SPLIT_WY = 2, 3  # WY with one serial chain / with the two-segment scan
 
 
 def form_rule(lens):
@@ -251,6 +252,29 @@ def test_prefill_forms_extreme_gates(cuda_device, form):
     o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, variant=FORMS[form], route="chunked")
     assert np.isfinite(o).all() and np.isfinite(s).all()
     check(o, s, o_ref, s_ref)
+
+
+@pytest.mark.parametrize("variant", [0, 1, CHAIN_WY, SPLIT_WY])
+def test_prefill_operand_magnitudes(cuda_device, variant):
+    # Keys and values far from unit size, per head: the WY form stores w's
+    # low half in fp8 under a power-of-two scale taken from max|w| of each
+    # (chunk, head), and w scales with k.  q/k head 0 keys x 1e-3, head 1
+    # x 0.05; v-heads 0-1 values x 1e4, 2-3 x 1e-4.  Each head's output and
+    # state are checked against its own magnitude.
+    lens = [700, 130] if variant in (0, 1) else [900]
+    inp = O.make_prefill_inputs(lens, seed=33, slow_decay_heads=(7,))
+    inp["k"] = O.bf16_round(inp["k"] * np.array([1e-3, 0.05, 1.0, 1.0], np.float32)[None, :, None])
+    vs = np.array([1e4, 1e4, 1e-4, 1e-4, 1.0, 1.0, 1.0, 1.0], np.float32)
+    inp["v"] = O.bf16_round(inp["v"] * vs[None, :, None])
+    if inp["state"] is not None:
+        inp["state"] = (inp["state"] * vs[None, :, None, None]).astype(np.float32)
+    print(f"prefill operand magnitudes variant={variant} lens={lens}", flush=True)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, variant=variant, route="chunked")
+    for h in range(8):
+        m = max(float(np.abs(o_ref[:, h]).max()), 1e-30)
+        assert_output_close(o[:, h] / m, o_ref[:, h] / m, what=f"output head {h}")
+        assert_state_close(s[:, h], s_ref[:, h], what=f"state head {h}")
 
 
 def test_prefill_forms_long_sequence(cuda_device):
