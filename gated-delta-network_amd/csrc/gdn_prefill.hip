@@ -1370,11 +1370,15 @@ __device__ __forceinline__ void t_state(
     __syncthreads();
     // ht: the workgroup's 16 rows of the bf16 chunk-start state ([v][k], 4 KB
     // contiguous) from the LDS copy, one 16-byte store per thread (stores of
-    // each lane's own 8 bytes, 32-byte pieces of 16 rows, cost ~20 us at 4x8192)
+    // each lane's own 8 bytes, 32-byte pieces of 16 rows, cost ~20 us at
+    // 4x8192), non-temporal: the T form runs batches whose ht and v_new
+    // (48 KB per chunk and head) outgrow the caches, and streaming them past
+    // L2 leaves it to the K, T and V lines the head's workgroups share
+    // (4x8192 state 163 -> 156 us)
     {
       const int t = threadIdx.x, row = t >> 4, k0 = (t & 15) * 8;
-      *reinterpret_cast<u32x4 *>(ht + (v0 + row) * kDK + k0) =
-          *reinterpret_cast<const u32x4 *>(&sSh[row * kStrideK + k0]);
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4 *>(&sSh[row * kStrideK + k0]),
+                                  reinterpret_cast<u32x4 *>(ht + (v0 + row) * kDK + k0));
     }
 
     // (b) X = K S for tokens 16*wave..+15 (two chains: S hi, S lo), then
@@ -1456,8 +1460,8 @@ __device__ __forceinline__ void t_state(
     // the LDS copy, one 8-byte store per thread
     {
       const int t = threadIdx.x, row = t >> 4, i0 = (t & 15) * 4;
-      *reinterpret_cast<u32x2 *>(vnt + (v0 + row) * kChunk + i0) =
-          *reinterpret_cast<const u32x2 *>(&sN[row * kStrideT + i0]);
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x2 *>(&sN[row * kStrideT + i0]),
+                                  reinterpret_cast<u32x2 *>(vnt + (v0 + row) * kChunk + i0));
     }
 
     // (d) S <- exp(G_last) S + K^T (D v_new); K is exact in bf16, so two MFMAs
