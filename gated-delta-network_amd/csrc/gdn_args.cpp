@@ -242,7 +242,8 @@ int plan_prefill(int T, int N, const Heads &H, const PrefillLayout &L, int varia
   if (P.form < 0) {
     const long long mean_chunks = ((static_cast<long long>(T) + N - 1) / N + kChunk - 1) / kChunk;
     const bool t_possible =
-        !P.single && t_form_wins(static_cast<float>(L.nt_max), static_cast<float>(mean_chunks));
+        !P.single && t_form_wins(static_cast<float>(L.nt_max), static_cast<float>(mean_chunks),
+                                 state_units(static_cast<float>(N), static_cast<float>(H.v)));
     P.form = t_possible ? -1 : 0;
   }
   const long long grid = chunk_head_grid(L.nt_max, H);

@@ -41,31 +41,46 @@ __host__ __device__ inline float cost_by_block(float L, float g) {
   return 4.5f + 0.015f * g + 0.008f * fmaxf(g - 256.0f, 0.0f) + rounds * blocks * per_block;
 }
 // Operand form of the chunks (WY or T) for a batch of nt chunks whose
-// longest sequence has lc chunks, from graph-replay sweeps of both forms on
-// MI355X (N = 1..64 equal sequences of 128..16384 tokens; 0.3 % above the
-// faster form over the sweep): the T form from 192 chunks on when the batch
-// holds more than three times the longest sequence's chunks, or from 384 on
-// with at least twice (the WY form's workspace, ~1 MB per chunk, then no
-// longer stays in the memory-side cache); else the WY form, and always for
-// one sequence (nt == lc).
-__host__ __device__ inline bool t_form_wins(float nt, float lc) {
-  return nt >= 192.0f && (nt > 3.0f * lc || (nt >= 384.0f && nt >= 2.0f * lc));
+// longest sequence has lc chunks and whose state recurrence has `units`
+// (sequence, v-head, 16-column) workgroups, from graph-replay sweeps of both
+// forms on MI355X (129 batches: N = 2..64 equal sequences of 64..16384
+// tokens and ragged mixes; 0.25 % above the faster form on average, at most
+// 7.8 %).  The T form (a quarter of the WY form's per-chunk workspace
+// traffic, a longer serial step):
+//  * for large batches -- from 144 chunks on when the batch holds more than
+//    three times the longest sequence's chunks, or from 384 on with at least
+//    1.5 times (the WY form's ~0.6 MB per chunk slot then no longer stays in
+//    the memory-side cache);
+//  * for small ones -- at most 768 units (three per CU) and chains of at
+//    most 12 chunks, where the WY intra kernel's heavier outputs outweigh
+//    T's longer steps (4 x 384 tokens: 35.8 vs 30.0 us, 8 x 192: 36.0 vs
+//    30.4 us);
+// else the WY form, and always for one sequence (nt == lc).  Both clauses
+// only turn true as chunks grow or the longest sequence shrinks.
+__host__ __device__ inline bool t_form_wins(float nt, float lc, float units) {
+  const bool large = nt >= 144.0f && (nt > 3.0f * lc || (nt >= 384.0f && nt >= 1.5f * lc));
+  const bool small = units <= 768.0f && lc <= 12.0f && nt > lc;
+  return large || small;
 }
+// State units of the chunk recurrence: (sequence, v-head, 16-column V block).
+__host__ __device__ inline float state_units(float N, float hv) { return N * hv * 8.0f; }
 // Chunks in one form (t: T, else WY) for N > 1 sequences, fitted to the same
-// sweeps (rms 4-5 %): fixed launches, the intra and output kernels' work per
-// chunk and v-head, and the state recurrence -- the longest sequence's chain
-// of lc steps, or the batch's nt * hv * 8 unit-steps over the 512 resident
-// state workgroups, whichever is longer; a step takes longer once some CU
-// holds two state workgroups (more than 256 units of N * hv * 8).
+// sweeps where the sequential paths compete (at most 256 chunks; rms 8-9 %):
+// fixed launches, the intra and output kernels' work per chunk and v-head,
+// and the state recurrence -- the longest sequence's chain of lc steps, or
+// the batch's nt * hv * 8 unit-steps over the 512 resident state workgroups,
+// whichever is longer; a step takes longer once some CU holds two state
+// workgroups (more than 256 units).
 __host__ __device__ inline float cost_by_chunks_form(float L, float nt, float hv, float N, bool t) {
-  const float lc = ceilf(L / 64.0f), units = N * hv * 8.0f;
+  const float lc = ceilf(L / 64.0f), units = state_units(N, hv);
   const float steps = fmaxf(lc, nt * hv / 64.0f);
-  if (t) return 10.6f + 0.039f * nt * hv + (units <= 256.0f ? 1.09f : 1.85f) * steps;
-  return 24.6f + 0.033f * nt * hv + (units <= 256.0f ? 0.81f : 1.80f) * steps;
+  if (t) return 20.6f + 0.0457f * nt * hv + (units <= 256.0f ? 0.631f : 0.785f) * steps;
+  return 19.8f + 0.0567f * nt * hv + (units <= 256.0f ? 0.373f : 0.454f) * steps;
 }
 // Chunks in the form t_form_wins picks.
 __host__ __device__ inline float cost_by_chunks(float L, float nt, float hv, float N) {
-  return cost_by_chunks_form(L, nt, hv, N, t_form_wins(nt, ceilf(L / 64.0f)));
+  return cost_by_chunks_form(L, nt, hv, N,
+                             t_form_wins(nt, ceilf(L / 64.0f), state_units(N, hv)));
 }
 
 // What a path choice made on the device costs (graph replay, MI355X): the

@@ -120,7 +120,8 @@ __device__ __forceinline__ bool device_picks_sequential(int choose, int rec_max,
   const float by_seq = choose == 2 ? cost_by_token(L, static_cast<float>(T), fhv, g)
                                    : cost_by_block(L, g);
   const float fnt = static_cast<float>(chunks);
-  const bool t = form == 1 || (form != 0 && t_form_wins(fnt, ceilf(L / kChunk)));
+  const bool t = form == 1 ||
+                 (form != 0 && t_form_wins(fnt, ceilf(L / kChunk), state_units(static_cast<float>(N), fhv)));
   return by_seq + kSeqChoiceMargin <= cost_by_chunks_form(L, fnt, fhv, static_cast<float>(N), t);
 }
 
@@ -216,7 +217,10 @@ __global__ __launch_bounds__(1024) void prefill_index_kernel(const void *cu, int
     offsets[N] = nt;
     offsets[N + 2] = (form == 0 || form == 1)
                          ? form
-                         : (t_form_wins(static_cast<float>(nt), static_cast<float>(s_most_chunks)) ? 1 : 0);
+                         : (t_form_wins(static_cast<float>(nt), static_cast<float>(s_most_chunks),
+                                        state_units(static_cast<float>(N), static_cast<float>(hv)))
+                                ? 1
+                                : 0);
   }
   for (int c = nt + tid; c < nt_max; c += 1024) chunks[c] = make_int4(-1, 0, 0, 0);
 }
@@ -302,7 +306,10 @@ __device__ __forceinline__ SelfIndexed self_index(char *smem, const SelfIndex &s
   const int nt = sequential ? 0 : (total < nt_max ? total : nt_max);
   const int form = (si.form == 0 || si.form == 1)
                        ? si.form
-                       : (t_form_wins(static_cast<float>(nt), static_cast<float>(s_red[1])) ? 1 : 0);
+                       : (t_form_wins(static_cast<float>(nt), static_cast<float>(s_red[1]),
+                                      state_units(static_cast<float>(N), static_cast<float>(hv)))
+                              ? 1
+                              : 0);
   if (blockIdx.x == 0) {
     if (tid < N) {
       const int first = sequential ? 0 : s_incl[tid] - n;

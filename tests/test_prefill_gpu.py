@@ -160,14 +160,18 @@ FORMS = {"wy": 0, "t": 1}
 CHAIN_WY, SPLIT_WY = 2, 3  # WY with one serial chain / with the two-segment scan
 
 
-def form_rule(lens):
+def form_rule(lens, hv=8):
     """Restatement of the built-in form choice of gdn_prefill.hip (index
-    kernel, t_form_wins in gdn_common.h): the T form from 192 chunks on for a
+    kernel, t_form_wins in gdn_common.h): the T form from 144 chunks on for a
     batch holding more than three times the chunks of its longest sequence,
-    or from 384 on with at least twice."""
+    or from 384 on with at least 1.5 times; and for batches of at most 768
+    state units (sequence, v-head, 16 columns) whose longest sequence has at
+    most 12 chunks, with more than one sequence holding chunks."""
     chunks = [-(-L // 64) for L in lens]
-    nt, longest = sum(chunks), max(chunks)
-    return 1 if nt >= 192 and (nt > 3 * longest or (nt >= 384 and nt >= 2 * longest)) else 0
+    nt, longest, units = sum(chunks), max(chunks), len(lens) * hv * 8
+    large = nt >= 144 and (nt > 3 * longest or (nt >= 384 and nt >= 1.5 * longest))
+    small = units <= 768 and longest <= 12 and nt > longest
+    return 1 if large or small else 0
 
 
 @pytest.mark.parametrize("form", list(FORMS))
@@ -189,7 +193,9 @@ def test_prefill_forms_reference_and_edge_cases(cuda_device, form):
 
 @pytest.mark.parametrize("lens", [[512] * 16, [1024] * 8, [2048] * 4, [4096] * 2, [8192, 1024, 512, 100],
                                   [6, 49, 294, 1800, 2040, 61], [64] * 130, [512] * 32, [2048] * 8,
-                                  [4096, 4096, 4096], [64] * 200, [8192, 64, 4096]])
+                                  [4096, 4096, 4096], [64] * 200, [8192, 64, 4096],
+                                  [256] * 4, [384] * 8, [150] * 12, [100, 700], [800, 64, 64],
+                                  [128] * 16, [768] * 12])
 def test_prefill_built_in_form_choice(cuda_device, lens):
     # The built-in choice is bit-identical to the form the rule names, and
     # the flag the index kernel leaves in the workspace is that form.

@@ -119,20 +119,22 @@ def _cost_by_block(L, g):
             + math.ceil(g / 512) * math.ceil(L / 16) * per_block)
 
 
-def _t_form_wins(nt, lc):
-    return nt >= 192 and (nt > 3 * lc or (nt >= 384 and nt >= 2 * lc))
+def _t_form_wins(nt, lc, units):
+    large = nt >= 144 and (nt > 3 * lc or (nt >= 384 and nt >= 1.5 * lc))
+    small = units <= 768 and lc <= 12 and nt > lc
+    return large or small
 
 
 def _cost_by_chunks_form(L, nt, hv, N, t):
     lc, units = math.ceil(L / 64), N * hv * 8
     steps = max(lc, nt * hv / 64)
     if t:
-        return 10.6 + 0.039 * nt * hv + (1.09 if units <= 256 else 1.85) * steps
-    return 24.6 + 0.033 * nt * hv + (0.81 if units <= 256 else 1.80) * steps
+        return 20.6 + 0.0457 * nt * hv + (0.631 if units <= 256 else 0.785) * steps
+    return 19.8 + 0.0567 * nt * hv + (0.373 if units <= 256 else 0.454) * steps
 
 
 def _cost_by_chunks(L, nt, hv, N):
-    return _cost_by_chunks_form(L, nt, hv, N, _t_form_wins(nt, math.ceil(L / 64)))
+    return _cost_by_chunks_form(L, nt, hv, N, _t_form_wins(nt, math.ceil(L / 64), N * hv * 8))
 
 
 def _expected_path(lens, hv=8):
@@ -181,7 +183,7 @@ def _lens_1500():
 DEVICE_CHOICE = {
     "256x1": ([1] * 256, "token"),
     "64x16": ([16] * 64, "block"),
-    "mixed40": ([3, 17, 96, 0, 40] * 8, "block"),
+    "mixed40": ([3, 17, 80, 0, 40] * 8, "block"),
     "1500": (_lens_1500(), "token"),
     "10x2+200": ([2] * 10 + [200], "chunks"),
     "16x8": ([8] * 16, "block"),
