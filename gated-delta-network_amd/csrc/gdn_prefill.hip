@@ -24,8 +24,9 @@
 //               every later sequence).  It also records whether cu_seqlens
 //               kept its contract (status words).
 //   2. intra  : per (chunk, v-head): gating, cumsum, K K^T on MFMA, the
-//               64x64 triangular inverse in LDS.  No GVA copies: v-head h
-//               reads q/k head h/2 directly.
+//               64x64 triangular inverse in LDS (and, in the WY form, its
+//               products with K and V).  No GVA copies: v-head h reads q/k
+//               head h/2 directly.
 //   3. state  : per (sequence, v-head, 16 columns of V): the serial
 //               recurrence over chunks with the f32 state in MFMA
 //               accumulators; stores the chunk-start state and v_new.
@@ -465,7 +466,10 @@ __device__ __forceinline__ void diag_inverse(float *sA, int wave, int lane) {
 }
 
 // Blocked forward substitution (I + A) Y = diag(scl) X for the 32 columns
-// col0.. of this wave; X row-major in sX ([64][kStrideK] bf16).
+// col0.. of this wave; X row-major in sX ([64][kStrideK] bf16), A in sA with
+// the diagonal inverses D_i in place of A_ii.  16x16x16 MFMAs (a result
+// tile's layout is the next product's B-operand layout), each row block
+// waiting on the ones above it.
 __device__ __forceinline__ void wy_solve(const uint16_t *sX, const float *scl, const float *sA,
                                          int col0, int g, int r16, f32x4 (&Y)[4][2]) {
   u32x2 Yh[4][2], Yl[4][2];  // hi/lo splits of Y (B operands)
@@ -504,13 +508,131 @@ __device__ __forceinline__ void wy_solve(const uint16_t *sX, const float *scl, c
   }
 }
 
+// Block column j = wave of T = (I + A)^-1 from the ten lower blocks of sA
+// (A, with the diagonal inverses D_i in place of A_ii): T_jj = D_j and, for
+// i > j, T_ij = -D_i sum_{j<=m<i} A_im T_mj, on split-bf16 16x16x16 MFMAs (a
+// result tile's layout is the next product's B-operand layout, so the column
+// stays in registers).  Tc[i] = T_ij in MFMA result order (lane holds rows
+// 4g..4g+3, column r16); zero above the diagonal.
+__device__ __forceinline__ void t_column(const float *sA, int wave, int g, int r16,
+                                         f32x4 (&Tc)[4]) {
+  const int j = wave;
+  u32x2 Th[4], Tl[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i < j) {  // above the diagonal
+      Tc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      Th[i] = Tl[i] = u32x2{0u, 0u};
+    } else if (i == j) {  // T_jj = D_j
+      const float *d = &sA[ablk(i, i) + (4 * g) * 20 + r16];
+      Tc[i] = f32x4{d[0], d[20], d[40], d[60]};
+      split4(Tc[i], Th[i], Tl[i]);
+    } else {
+      // Z = -sum_{j<=m<i} A_im T_mj, then T_ij = D_i Z
+      f32x4 Z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < i; ++m) {
+        if (m < j) continue;
+        const f32x4 la = *reinterpret_cast<const f32x4 *>(&sA[ablk(i, m) + r16 * 20 + 4 * g]);
+        u32x2 lh, ll;
+        split4(-la, lh, ll);
+        Z = mfma16_x3(lh, ll, Th[m], Tl[m], Z);
+      }
+      const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&sA[ablk(i, i) + r16 * 20 + 4 * g]);
+      u32x2 dh, dl, zh, zl;
+      split4(d4, dh, dl);
+      split4(Z, zh, zl);
+      Tc[i] = mfma16_x3(dh, dl, zh, zl, f32x4{0.f, 0.f, 0.f, 0.f});
+      split4(Tc[i], Th[i], Tl[i]);
+    }
+  }
+}
+
+// Y = T diag(scl) X for the 32 columns col0.. of this wave: X row-major in
+// sX ([64][kStrideK] bf16, exact), T = (I + A)^-1 in the ten lower blocks of
+// sA (f32, rows of 20), scl per token.  T diag(scl) is split into bf16 hi and
+// lo A operands of 16x16x32 MFMAs (two products per k-step, X exact); the
+// k-steps of T's zero blocks above the diagonal are skipped, a half-zero one
+// reads zeros.  Result tiles Y[i][nt]: rows 16 i + 4 g .., column col0 +
+// 16 nt + r16.
+__device__ __forceinline__ void wy_gemm(const uint16_t *sX, const float *scl, const float *sA,
+                                        int col0, int g, int r16, f32x4 (&Y)[4][2]) {
+  const int kg = 8 * g;
+  u32x4 xb[2][2];  // X: k-step kk (tokens 32 kk + 8 g ..), column tile nt
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const u32x2 y = tile_col4(sX, 32 * kk + kg + 4 * hh, col0 + 16 * nt, r16);
+        xb[kk][nt][2 * hh] = y[0];
+        xb[kk][nt][2 * hh + 1] = y[1];
+      }
+  f32x4 s0[2], s1[2];  // scl of the lane's 8 tokens per k-step
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    s0[kk] = *reinterpret_cast<const f32x4 *>(&scl[32 * kk + kg]);
+    s1[kk] = *reinterpret_cast<const f32x4 *>(&scl[32 * kk + kg + 4]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) Y[i][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      if (kk == 1 && i < 2) continue;  // block columns 2, 3 of row tiles 0, 1: zero
+      // T[16 i + r16][32 kk + 8 g ..]: block (i, jb), columns 8 (g & 1) ..
+      const int jb = 2 * kk + (g >> 1);
+      const bool live = jb <= i;
+      const float *row = &sA[ablk(i, live ? jb : i) + r16 * 20 + 8 * (g & 1)];
+      const f32x4 t0 = *reinterpret_cast<const f32x4 *>(row);
+      const f32x4 t1 = *reinterpret_cast<const f32x4 *>(row + 4);
+      float x8[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x8[e] = live ? t0[e] * s0[kk][e] : 0.f;
+        x8[4 + e] = live ? t1[e] * s1[kk][e] : 0.f;
+      }
+      u32x4 ah, al;
+      split8(x8, ah, al);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        Y[i][nt] = mfma_bf16(ah, xb[kk][nt], Y[i][nt]);
+        Y[i][nt] = mfma_bf16(al, xb[kk][nt], Y[i][nt]);
+      }
+    }
+  }
+}
+
+// T of the chunk over A in sA (every wave calls it; LDS barriers inside):
+// each wave's block column by t_column, then, once no wave reads A any
+// more, written over the ten lower blocks of sA.
+__device__ __forceinline__ void t_into_sA(float *sA, int wave, int g, int r16) {
+  f32x4 Tc[4];
+  t_column(sA, wave, g, r16, Tc);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i < wave) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sA[ablk(i, wave) + (4 * g + r) * 20 + r16] = Tc[i][r];
+  }
+  __syncthreads();
+}
+
+// Batches of at least this many (chunk, v-head) units (three per CU) form
+// w and u as T and two products (wy_gemm) instead of two solves.
+constexpr int kIntraGemmMinUnits = 3 * 256;
+
 template <int PART>
 __device__ __forceinline__ void wy_intra(
     char *smem, int c, int h, int start, int len, const uint16_t *__restrict__ k,
     const uint16_t *__restrict__ v, const float *__restrict__ A_log, const uint16_t *__restrict__ a,
     const float *__restrict__ dt_bias, const uint16_t *__restrict__ b, const Heads &H,
     float *__restrict__ ws_G, float *__restrict__ ws_dcy, float *__restrict__ ws_eg,
-    uint16_t *__restrict__ ws_w, float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
+    uint16_t *__restrict__ ws_w, float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt,
+    bool gemm) {
   constexpr bool kW = PART != 2, kU = PART != 1;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -529,31 +651,12 @@ __device__ __forceinline__ void wy_intra(
   constexpr int kStrideS = 68;
   static_assert(kChunk * kStrideS * 4 <= kChunk * kStrideK * 2, "w scratch must fit the tile");
 
-  // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding tokens
-  // get g = 0 and beta = 0, so G stays at G_last past the end of the chunk.
-  if (wave == 0) {
-    float gl, be;
-    chunk_gates(lane, start, len, h, H, A_log, a, dt_bias, b, gl, be);
-    float G = gl;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(G, off);
-      if (lane >= off) G += y;
-    }
-    sG[lane] = G;
-    sBeta[lane] = be;
-    sBG[lane] = be * expf(G);
-    if (kW) {  // (the u-only half leaves these to the w half)
-      const float G_last = __shfl(G, 63);
-      ws_G[ch_head * kChunk + lane] = G;
-      ws_dcy[ch_head * kChunk + lane] = expf(G_last - G);
-      if (lane == 0) ws_eg[ch_head] = expf(G_last);
-    }
-  }
-
-  // K rows -> LDS; V rows into registers (rows past the chunk read zero
-  // through the descriptors' range).  Thread t moves 16 bytes of rows
-  // (t + 256 i) / 16.
+  // K rows -> LDS, then V rows into registers (rows past the chunk read
+  // zero through the descriptors' range).  Thread t moves 16 bytes of rows
+  // (t + 256 i) / 16.  The K loads go first, the gating of wave 0 runs while
+  // they are in flight; V is loaded only once K is in LDS: every workgroup of
+  // a launch loads at once, and K alone arrives sooner (V is first needed
+  // after the w-solve, or after A for the u-only half).
   u32x4 vrows[4];
   {
     const uint32_t kstride = static_cast<uint32_t>(H.qk) * (kDK * 2);
@@ -565,14 +668,26 @@ __device__ __forceinline__ void wy_intra(
       const int idx = tid + 256 * i;
       krows[i] = buf_load16(rk, static_cast<uint32_t>(idx >> 4) * kstride + (idx & 15) * 16);
     }
-    if (kU) {
-      const uint32_t vstride = static_cast<uint32_t>(H.v) * (kDV * 2);
-      const auto rv = buf_rsrc(v + (static_cast<size_t>(start) * H.v + h) * kDV,
-                               static_cast<uint32_t>(len) * vstride);
+    // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding
+    // tokens get g = 0 and beta = 0, so G stays at G_last past the end of the
+    // chunk.
+    if (wave == 0) {
+      float gl, be;
+      chunk_gates(lane, start, len, h, H, A_log, a, dt_bias, b, gl, be);
+      float G = gl;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int idx = tid + 256 * i;
-        vrows[i] = buf_load16(rv, static_cast<uint32_t>(idx >> 4) * vstride + (idx & 15) * 16);
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(G, off);
+        if (lane >= off) G += y;
+      }
+      sG[lane] = G;
+      sBeta[lane] = be;
+      sBG[lane] = be * expf(G);
+      if (kW) {  // (the u-only half leaves these to the w half)
+        const float G_last = __shfl(G, 63);
+        ws_G[ch_head * kChunk + lane] = G;
+        ws_dcy[ch_head * kChunk + lane] = expf(G_last - G);
+        if (lane == 0) ws_eg[ch_head] = expf(G_last);
       }
     }
 #pragma unroll
@@ -582,6 +697,16 @@ __device__ __forceinline__ void wy_intra(
     }
   }
   __syncthreads();
+  if (kU) {
+    const uint32_t vstride = static_cast<uint32_t>(H.v) * (kDV * 2);
+    const auto rv = buf_rsrc(v + (static_cast<size_t>(start) * H.v + h) * kDV,
+                             static_cast<uint32_t>(len) * vstride);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      vrows[i] = buf_load16(rv, static_cast<uint32_t>(idx >> 4) * vstride + (idx & 15) * 16);
+    }
+  }
 
   build_A(sX, sA, sG, sBeta, len, wave, lane);
   // K^T as A-operand fragments of the state kernel (one v-head per q/k head
@@ -615,11 +740,28 @@ __device__ __forceinline__ void wy_intra(
   }
   diag_inverse(sA, wave, lane);
   __syncthreads();
-
+  // w = T diag(beta e^G) K and u = T diag(beta) V: with `gemm`, T =
+  // (I + A)^-1 first (over A) and two products (wy_gemm); else two blocked
+  // forward substitutions (wy_solve).  T's serial column walk costs ~1.9 us
+  // at 1x8192, and the products (16x16x32, no chain between row blocks) save
+  // more once several workgroups share each CU (intra 21.7 -> 20.8 us at
+  // 1x8192, 23.1 -> 21.9 us at 2x4096, 15.4 us either way at 1x4096 with two
+  // per CU); with fewer, and for the split halves (one solve each), the
+  // solves are faster (1x1024 11.7 vs 12.5 us, configs[3] 19.2 vs 20.0 us).
+  // The choice depends on the batch's chunk count alone (not on the launch
+  // grid, an upper bound), so a batch gets the same bits whichever way it
+  // was indexed and whether its form was set or picked on the device.
+  if (gemm) t_into_sA(sA, wave, g, r16);
+  auto solve = [&](const float *scl, f32x4 (&Y)[4][2]) {
+    if (gemm)
+      wy_gemm(sX, scl, sA, 32 * wave, g, r16, Y);
+    else
+      wy_solve(sX, scl, sA, 32 * wave, g, r16, Y);
+  };
   const int col0 = 32 * wave;
   if (kW) {
     f32x4 Y[4][2];
-    wy_solve(sX, sBG, sA, col0, g, r16, Y);
+    solve(sBG, Y);
     {
       float m = 0.f;
 #pragma unroll
@@ -688,7 +830,7 @@ __device__ __forceinline__ void wy_intra(
   }
   if (kU) {
     f32x4 Y[4][2];
-    wy_solve(sX, sBeta, sA, col0, g, r16, Y);
+    solve(sBeta, Y);
     // u tiles in MFMA result order: [chunk][head][row tile][col tile][lane][4]
     float *ut = ws_u + ch_head * (kChunk * kDV);
 #pragma unroll
@@ -782,42 +924,9 @@ __device__ __forceinline__ void t_intra(
   diag_inverse(sA, wave, lane);  // D_w = (I + A_ww)^-1 in place of A_ww
   __syncthreads();
 
-  // Block column j = wave of T.  Tiles in MFMA result order: lane holds
-  // T_ij[4g + r][r16]; their hi/lo splits are the B operands of the next
-  // products.
+  // Block column j = wave of T (t_column), in MFMA result order.
   f32x4 Tc[4];
-  {
-    const int j = wave;
-    u32x2 Th[4], Tl[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (i < j) {  // above the diagonal
-        Tc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-        Th[i] = Tl[i] = u32x2{0u, 0u};
-      } else if (i == j) {  // T_jj = D_j
-        const float *d = &sA[ablk(i, i) + (4 * g) * 20 + r16];
-        Tc[i] = f32x4{d[0], d[20], d[40], d[60]};
-        split4(Tc[i], Th[i], Tl[i]);
-      } else {
-        // Z = -sum_{j<=m<i} A_im T_mj, then T_ij = D_i Z
-        f32x4 Z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int m = 0; m < i; ++m) {
-          if (m < j) continue;
-          const f32x4 la = *reinterpret_cast<const f32x4 *>(&sA[ablk(i, m) + r16 * 20 + 4 * g]);
-          u32x2 lh, ll;
-          split4(-la, lh, ll);
-          Z = mfma16_x3(lh, ll, Th[m], Tl[m], Z);
-        }
-        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(&sA[ablk(i, i) + r16 * 20 + 4 * g]);
-        u32x2 dh, dl, zh, zl;
-        split4(d4, dh, dl);
-        split4(Z, zh, zl);
-        Tc[i] = mfma16_x3(dh, dl, zh, zl, f32x4{0.f, 0.f, 0.f, 0.f});
-        split4(Tc[i], Th[i], Tl[i]);
-      }
-    }
-  }
+  t_column(sA, wave, g, r16, Tc);
   // sK (K) is dead since A was built: T (f32) goes there, upper blocks zero.
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -865,16 +974,16 @@ __device__ __forceinline__ void intra_wy_unit(
     const uint16_t *__restrict__ a, const float *__restrict__ dt_bias,
     const uint16_t *__restrict__ b, const Heads &H, float *__restrict__ ws_G,
     float *__restrict__ ws_dcy, float *__restrict__ ws_eg, uint16_t *__restrict__ ws_w,
-    float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt) {
+    float *__restrict__ ws_u, uint16_t *__restrict__ ws_kt, bool gemm) {
   if (!SPLIT)
-    wy_intra<0>(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w,
-                ws_u, ws_kt);
+    wy_intra<0>(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg,
+                    ws_w, ws_u, ws_kt, gemm);
   else if (half)
-    wy_intra<2>(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w,
-                ws_u, ws_kt);
+    wy_intra<2>(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg,
+                    ws_w, ws_u, ws_kt, false);
   else
-    wy_intra<1>(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w,
-                ws_u, ws_kt);
+    wy_intra<1>(smem, c, h, ch.y, ch.z, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg,
+                    ws_w, ws_u, ws_kt, false);
 }
 
 template <int FORM, bool SPLIT>
@@ -901,10 +1010,12 @@ __device__ __forceinline__ void intra_body(
   const bool unit = chunk_head_of(pair, nt_max, H, c, h);
   int form = FORM;
   int4 ch;
+  int nt;  // the batch's chunks
   if (si.cu != nullptr) {
     if (!unit && id != 0) return;
     const SelfIndexed x = self_index(smem, si, nt_max, H.v);
     if (FORM < 0) form = x.form;
+    nt = x.nt;
     ch = self_chunk(smem, si.N, c, x.nt);
     if (unit && h == 0 && half == 0) si.chunks[c] = ch;
     __syncthreads();  // the LDS arrays are dead: the unit's tiles take their place
@@ -915,6 +1026,13 @@ __device__ __forceinline__ void intra_body(
       si.status[0] = cu_status_bits(raw_cu(one.cu, one.cu64, 0), raw_cu(one.cu, one.cu64, 1), one.T);
     if (!unit) return;
     if (FORM < 0) form = *form_flag;
+    if (one.cu != nullptr) {
+      int bos, eos;
+      one_seq_bounds(one, bos, eos);
+      nt = (eos - bos + kChunk - 1) / kChunk;
+    } else {
+      nt = si.offsets[si.N];  // the index kernel's chunk count
+    }
     ch = chunk_info(chunks, c, one);
   }
   if (ch.x < 0) return;
@@ -922,7 +1040,7 @@ __device__ __forceinline__ void intra_body(
     t_intra(smem, c, h, ch.y, ch.z, k, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg, ws_w, ws_u);
   else
     intra_wy_unit<SPLIT>(smem, c, h, ch, half, k, v, A_log, a, dt_bias, b, H, ws_G, ws_dcy, ws_eg,
-                         ws_w, ws_u, ws_kt);
+                         ws_w, ws_u, ws_kt, !SPLIT && nt * H.v >= kIntraGemmMinUnits);
 }
 
 template <int FORM, bool SPLIT>
