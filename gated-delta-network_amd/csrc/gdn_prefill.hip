@@ -876,30 +876,9 @@ __device__ __forceinline__ void t_intra(
   static_assert(kChunk * kStrideA4 * 4 <= kChunk * kStrideK * 2, "T must fit in the K tile");
   float *const sT = reinterpret_cast<float *>(sK);
 
-  // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding tokens
-  // get g = 0 and beta = 0, so G stays at G_last past the end of the chunk.
-  if (wave == 0) {
-    float gl, be;
-    chunk_gates(lane, start, len, h, H, A_log, a, dt_bias, b, gl, be);
-    float G = gl;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(G, off);
-      if (lane >= off) G += y;
-    }
-    sG[lane] = G;
-    sBeta[lane] = be;
-    const float G_last = __shfl(G, 63);
-    ws_G[ch_head * kChunk + lane] = G;
-    ws_dcy[ch_head * kChunk + lane] = expf(G_last - G);
-    float *bb = ws_u + ch_head * (kChunk * kDV);  // (beta, beta e^G) in the u region
-    bb[lane] = be;
-    bb[kChunk + lane] = be * expf(G);
-    if (lane == 0) ws_eg[ch_head] = expf(G_last);
-  }
-
   // K row-major into LDS (rows past the chunk read zero through the
-  // descriptor's range); every load issued before the LDS stores.
+  // descriptor's range); every load issued before the LDS stores, and the
+  // gating of wave 0 runs while they are in flight.
   {
     const uint32_t rstride = static_cast<uint32_t>(H.qk) * (kDK * 2);
     const auto rs = buf_rsrc(k + (static_cast<size_t>(start) * H.qk + hq) * kDK,
@@ -909,6 +888,28 @@ __device__ __forceinline__ void t_intra(
     for (int i = 0; i < 4; ++i) {
       const int idx = tid + 256 * i;
       kv[i] = buf_load16(rs, static_cast<uint32_t>(idx >> 4) * rstride + (idx & 15) * 16);
+    }
+    // Gating and the chunk-local cumsum (wave 0, lane = token).  Padding
+    // tokens get g = 0 and beta = 0, so G stays at G_last past the end of the
+    // chunk.
+    if (wave == 0) {
+      float gl, be;
+      chunk_gates(lane, start, len, h, H, A_log, a, dt_bias, b, gl, be);
+      float G = gl;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(G, off);
+        if (lane >= off) G += y;
+      }
+      sG[lane] = G;
+      sBeta[lane] = be;
+      const float G_last = __shfl(G, 63);
+      ws_G[ch_head * kChunk + lane] = G;
+      ws_dcy[ch_head * kChunk + lane] = expf(G_last - G);
+      float *bb = ws_u + ch_head * (kChunk * kDV);  // (beta, beta e^G) in the u region
+      bb[lane] = be;
+      bb[kChunk + lane] = be * expf(G);
+      if (lane == 0) ws_eg[ch_head] = expf(G_last);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
