@@ -93,6 +93,9 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
 
   // The state as result tiles of S^T: St[kt][vi] holds S[v][k] at
   // k = 16 kt + q4 + r, v = 32 wave + 16 vi + r16.
+  // The state is read once and written once: non-temporal accesses, as in
+  // the decode kernel (B=64 T=8 decode 19.1 -> 16.3 us; 64x16 prefill over
+  // rotating state sets 29.6 -> 24.5 us).
   const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;
   f32x4 St[8][CV];
 #pragma unroll
@@ -101,7 +104,8 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
     for (int vi = 0; vi < CV; ++vi) {
       const int vc = col0 + 16 * vi + r16;
       if (state != nullptr && len > 0)
-        St[kt][vi] = *reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + 16 * kt + q4);
+        St[kt][vi] = __builtin_nontemporal_load(
+            reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + 16 * kt + q4));
       else
         St[kt][vi] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -413,7 +417,8 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
       f32x4 x = St[kt][vi];
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[r] *= c;
-      *reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + 16 * kt + q4) = x;
+      __builtin_nontemporal_store(
+          x, reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + 16 * kt + q4));
     }
   // A packed batch: rows outside every sequence get zeros.
   if (cu != nullptr) zero_uncovered_rows(out, cu, cu64, N, T, H.v, blockIdx.x, gridDim.x);

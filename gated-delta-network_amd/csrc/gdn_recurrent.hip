@@ -69,14 +69,17 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
     len = fixed_len;
   }
   const int hq = h / H.ratio;
+  // The state is read once and written once: non-temporal accesses, as in
+  // the decode kernel (over rotating state sets: B=64 T=2 decode 15.3 ->
+  // 12.5 us, 256x1 prefill 63.2 -> 58.5 us).
   const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;
   f32x4 Sa[PASSES], Sb[PASSES];  // columns c4.. and 64 + c4..
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
     const size_t off = sbase + static_cast<size_t>(row0 + 4 * p) * kDK + c4;
     if (state != nullptr && len > 0) {
-      Sa[p] = *reinterpret_cast<const f32x4 *>(state + off);
-      Sb[p] = *reinterpret_cast<const f32x4 *>(state + off + 64);
+      Sa[p] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(state + off));
+      Sb[p] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(state + off + 64));
     } else {
       Sa[p] = f32x4{0.f, 0.f, 0.f, 0.f};
       Sb[p] = Sa[p];
@@ -195,8 +198,8 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
     const size_t off = sbase + static_cast<size_t>(row0 + 4 * p) * kDK + c4;
-    *reinterpret_cast<f32x4 *>(new_state + off) = Sa[p];
-    *reinterpret_cast<f32x4 *>(new_state + off + 64) = Sb[p];
+    __builtin_nontemporal_store(Sa[p], reinterpret_cast<f32x4 *>(new_state + off));
+    __builtin_nontemporal_store(Sb[p], reinterpret_cast<f32x4 *>(new_state + off + 64));
   }
   // A packed batch: rows outside every sequence get zeros.
   if (cu != nullptr) zero_uncovered_rows(out, cu, cu64, N, T, H.v, blockIdx.x, gridDim.x);
