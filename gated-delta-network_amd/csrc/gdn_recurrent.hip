@@ -235,13 +235,18 @@ void launch_rec(long long groups, hipStream_t stream, const uint16_t *q, const u
 int recurrent_num_variants() { return kNumRecVariants + 1; }
 int recurrent_block_variant() { return kNumRecVariants; }
 
-// Built-in tiling from a sweep on MI355X: few (sequence, head) groups -> the
-// smallest row blocks (the serial token loop is spread over the most waves);
-// many -> 64-row blocks (fewer waves repeat the per-token overhead).
+// Built-in tiling from a sweep on MI355X (every tiling, B = 1..256 rows of
+// T = 2, 4, 8 tokens, graph replay over rotating states): few (sequence,
+// head) groups -> the smallest row blocks (the serial token loop is spread
+// over the most waves); more -> one wave streaming 8..32 rows (within ~5 % of
+// the best tiling everywhere; 64-row four-wave blocks, the earlier choice for
+// more than 128 groups, were up to 14 % slower at B = 64..256).
 int recurrent_default_variant(long long groups) {
-  if (groups <= 32) return 0;    // 4 rows, 1 wave
-  if (groups <= 128) return 5;   // 32 rows, 4 waves
-  return 7;                      // 64 rows, 4 waves
+  if (groups <= 32) return 0;     // 4 rows, 1 wave
+  if (groups <= 64) return 3;     // 8 rows, 1 wave
+  if (groups <= 256) return 6;    // 16 rows, 1 wave
+  if (groups <= 1024) return 8;   // 32 rows, 1 wave
+  return 6;                       // 16 rows, 1 wave
 }
 
 int recurrent_launch(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *state,

@@ -110,7 +110,7 @@ def test_routing_zero_length_sequences_get_zero_state(cuda_device):
 
 
 def _cost_by_token(L, T, hv, g):
-    return 3 + 0.24 * L + 0.003 * T * hv + 0.021 * g
+    return 3.56 + 0.216 * L + 0.00297 * T * hv + 0.0131 * g
 
 
 def _cost_by_block(L, g):
