@@ -537,12 +537,17 @@ def main():
         _, mg = bench_decode(64, 50, 5, dev, tokens=T)
         mtp[f"B64_T{T}"] = round(mg * 1e3, 2)
     log(f"multi-token decode B=64 (us per call): {mtp}")
-    short = {}
+    # Short batches: one input set replayed (warm in the Infinity Cache, as
+    # the other single-set lines) and over rotating sets (cache-cold, as a
+    # serving loop meets each request's state).
+    short, short_rot = {}, {}
     for name, lens in (("256x1", [1] * 256), ("64x16", [16] * 64), ("1x64", [64]),
                        ("32x64", [64] * 32), ("64x256", [256] * 64)):
         _, pg = bench_prefill(lens, 20, 3, dev)
         short[name] = round(pg, 4)
-    log(f"short-sequence prefill (ms per call): {short}")
+        if len(lens) > 1:  # (one 64-token sequence would need ~1000 sets)
+            short_rot[name] = round(bench_prefill_rotated(lens, dev)[0], 4)
+    log(f"short-sequence prefill (ms per call): {short}, over rotating sets {short_rot}")
 
     # the decode batch sweep (one step in graph replay per B), and
     # the prefill configurations configs[3] and configs[4] (configs[2] is
@@ -626,6 +631,7 @@ def main():
         "prefill_configs": cfg_detail,
         "decode_multi_token_us": mtp,
         "prefill_ms_short_batches": short,
+        "prefill_ms_short_batches_rotated": short_rot,
         "prefill_roofline": {"bound": "mfma", "achieved": round(pre_tflops, 2), "peak": 2500.0,
                              "unit": "TFLOP/s", "frac": round(pre_tflops / 2500.0, 5),
                              "hbm_gbs": round(pre_gbs, 1),
