@@ -621,8 +621,8 @@ __device__ __forceinline__ void t_into_sA(float *sA, int wave, int g, int r16) {
   __syncthreads();
 }
 
-// Batches of at least this many (chunk, v-head) units (three per CU) form
-// w and u as T and two products (wy_gemm) instead of two solves.
+// Batches of at least this many (chunk, v-head) units (three per CU of the
+// 256) form w and u as T and two products (wy_gemm) instead of two solves.
 constexpr int kIntraGemmMinUnits = 3 * 256;
 
 template <int PART>
@@ -846,7 +846,7 @@ __device__ __forceinline__ void wy_intra(
 //   * wave 0: gating, chunk-local cumsum G, the per-token vectors.
 //   * A = strictly-lower(beta_i exp(G_i - G_j) K K^T) on MFMA (K exact bf16).
 //   * T = (I + A)^-1: the four 16x16 diagonal blocks D_i by forward
-//     substitution (wave i), then wave j walks block column j,
+//     substitution (wave i), then wave j walks block column j (t_column),
 //       T_jj = D_j,   T_ij = -D_i sum_{j<=m<i} A_im T_mj   (i > j),
 //     on split-bf16 16x16x16 MFMAs (a result tile's layout is the next
 //     product's B-operand layout, so the column stays in registers).
