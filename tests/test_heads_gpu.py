@@ -143,6 +143,19 @@ def test_prefill_heads_single_long_sequence(cuda_device):
     assert_state_close(ns.cpu().numpy(), s_ref)
 
 
+def test_prefill_heads_wy_product_form(cuda_device):
+    # 1600 tokens at 32 v-heads: 25 chunks x 32 = 800 (chunk, v-head) units,
+    # past the 768 from which the WY intra kernel forms w and u as T and two
+    # products instead of two solves (one sequence: WY form, one chain)
+    heads = (16, 32)
+    inp = O.make_prefill_inputs([1600], seed=62, heads=heads, with_state=True)
+    print(f"prefill heads={heads} lens=[1600] (product form)", flush=True)
+    out, ns = _prefill(_to_dev(inp, cuda_device), cuda_device, -1)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    assert_output_close(out.float().cpu().numpy(), o_ref)
+    assert_state_close(ns.cpu().numpy(), s_ref)
+
+
 def _ptr(t):
     return None if t is None else t.data_ptr()
 

@@ -215,6 +215,20 @@ def test_prefill_built_in_form_choice(cuda_device, lens):
     check(o_a, s_a, o_ref, s_ref)
 
 
+def test_prefill_wy_product_form_ragged_batch(cuda_device):
+    # 40 + 47 + 11 + 1 = 99 chunks (partial last chunks in every sequence) x 8
+    # v-heads = 792 units: past the 768 from which the WY intra kernel forms w
+    # and u as T and two products; the built-in choice keeps the WY form
+    # (99 < 144 chunks) and indexes the batch in the intra kernel
+    lens = [2500, 3000, 700, 33]
+    inp = O.make_prefill_inputs(lens, seed=29)
+    print(f"prefill product form lens={lens}", flush=True)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, route="chunked")
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    check(o, s, o_ref, s_ref)
+    assert form_rule(lens) == 0
+
+
 @pytest.mark.parametrize("form", list(FORMS))
 def test_prefill_self_index_matches_index_kernel(cuda_device, form):
     # A batch of at most 256 sequences and two rounds of intra workgroups
