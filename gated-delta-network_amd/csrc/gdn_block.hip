@@ -26,7 +26,8 @@
 // and U are read transposed out of the block's K and V rows in LDS
 // (ds_read_b64_tr_b16).  Products whose error reaches the state use split
 // bf16 (x = hi + lo), as in the chunk pipeline; P v_new uses single bf16
-// operands.
+// operands, as the chunk pipeline's output (at large outputs, where only the
+// relative 1e-2 bar applies, that costs up to ~0.4 %).
 #include "gdn_device.h"
 #include "gdn_host.h"
 
@@ -36,9 +37,15 @@ constexpr int kBlk = 16;        // tokens per block
 constexpr int kBStride = 136;   // bf16 row stride of the q/k/v block tiles
 constexpr int kBStrideA = 20;   // f32 row stride of the 16x16 A^T and Ti tiles
 constexpr int kBStrideP = 24;   // bf16 row stride of P
-// Smallest pending decay factor of the state tiles (step (7)): the tiles hold
-// at most 2^60 times the state, far inside f32 range.
-constexpr float kMinDecay = 0x1p-60f;
+// Pending decay factor below which step (7) folds the decay into the state
+// tiles: 1, so every block's decay e^{G_last} < 1 is folded and the tiles
+// hold the state itself, finite wherever the reference's f32 state is (a
+// lazy S / c with c down to 2^-60 overflowed at |S| ~ 3e20: the all-0.5
+// input of OPTIMIZATION_LOG.md:217-220 passes that at ~65 tokens).  c stays
+// a run-time value, 1 or an unfolded exact-1 decay: with c a compile-time 1
+// the compiler orders the block loop differently, measured 1.5 us slower at
+// B=64 T=16 (16.4 -> 18.0 us).
+constexpr float kFoldBelow = 1.f;
 // Largest (sequence, v-head) count that runs as two 64-column workgroups.
 constexpr long long kBlockHalfMaxPairs = 128;
 
@@ -98,18 +105,6 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
   // rotating state sets 29.6 -> 24.5 us).
   const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;
   f32x4 St[8][CV];
-#pragma unroll
-  for (int kt = 0; kt < 8; ++kt)
-#pragma unroll
-    for (int vi = 0; vi < CV; ++vi) {
-      const int vc = col0 + 16 * vi + r16;
-      if (state != nullptr && len > 0)
-        St[kt][vi] = __builtin_nontemporal_load(
-            reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + 16 * kt + q4));
-      else
-        St[kt][vi] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
   const uint32_t qk_stride = static_cast<uint32_t>(H.qk) * (kDK * 2);
   const uint32_t v_stride = static_cast<uint32_t>(H.v) * (kDV * 2);
   // The inputs of a block -- this thread's 16 bytes of its q, k and v rows
@@ -160,12 +155,25 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
       sED[par][lane] = expf(G_last - G);
     }
   };
-  float c = 1.f;  // the state is c * St (decay applied lazily, step (7))
+  float c = 1.f;  // the state is c * St (step (7))
+  // The first block's inputs are requested before the state: the loads
+  // return in order, so steps (1)-(4), which do not read the state, need not
+  // wait for all 64 KB of it.
   BlockIn cur;
-  if (len > 0) {
-    load_block(0, cur);
-    if (wave == 0) gate_block(len < kBlk ? len : kBlk, cur.a, cur.b, 0);
-  }
+  if (len > 0) load_block(0, cur);
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+    for (int vi = 0; vi < CV; ++vi) {
+      const int vc = col0 + 16 * vi + r16;
+      if (state != nullptr && len > 0)
+        St[kt][vi] = __builtin_nontemporal_load(
+            reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + 16 * kt + q4));
+      else
+        St[kt][vi] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  if (len > 0 && wave == 0) gate_block(len < kBlk ? len : kBlk, cur.a, cur.b, 0);
   for (int t0 = 0; t0 < len; t0 += kBlk) {
     const int n = len - t0 < kBlk ? len - t0 : kBlk;
     const int start = bos + t0;
@@ -366,13 +374,13 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
 
     // (7) S <- e^{G_last} S + K^T (D v_new), D = e^{G_last - G}: A = K^T rows
     //     (a transposed read of the K rows), B = D v_new split.  The tiles
-    //     hold S / c; the block's decay e^{G_last} only moves c, and the
-    //     update is added as K^T (D v_new) / c -- unless c would fall below
-    //     kMinDecay (or to zero), when the tiles take c e^{G_last} and c
-    //     returns to 1.
+    //     hold S / c: a pending factor cn = c e^{G_last} below kFoldBelow
+    //     (every decay below 1, or NaN) is folded in, the tiles take
+    //     cn and c returns to 1; otherwise the update is added as
+    //     K^T (D v_new) / cn.
     {
       float cn = c * bEG[kBlk - 1];
-      const bool rescale = !(cn >= kMinDecay);
+      const bool rescale = !(cn >= kFoldBelow);
       if (rescale) {
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt)

@@ -440,6 +440,33 @@ def make_prefill_inputs(lens, seed: int = 0, with_state: bool = True,
                 a=a, dt_bias=dt_bias, b=b, cu_seqlens=cu, scale=1.0 / math.sqrt(DK))
 
 
+def make_all_same_inputs(lens, value: float = 0.5, noise: float = 0.0, seed: int = 0,
+                         with_state: bool = True):
+    """The reference's "all_same" adversarial input (OPTIMIZATION_LOG.md:217-220):
+    every tensor -- q, k, v, state, A_log, a, dt_bias, b -- filled with
+    ``value``; scale 1/sqrt(128).  With 0.5, beta |k|^2 = 19.9 and the decay
+    is 0.115, so the state grows ~2.2x per token (f32 stays finite to ~110
+    tokens).  ``noise`` > 0 multiplies each element by (1 + noise N(0,1)) so
+    the tensors are no longer uniform.  Returns prefill inputs for ``lens``
+    (cu_seqlens int64); bf16 tensors are rounded to bf16."""
+    lens = [int(x) for x in lens]
+    T, N = sum(lens), len(lens)
+    rng = np.random.default_rng(seed)
+
+    def fill(shape, bf16=True):
+        x = np.full(shape, value, np.float32)
+        if noise:
+            x = (x * (1.0 + noise * rng.standard_normal(shape))).astype(np.float32)
+        return bf16_round(x) if bf16 else x
+
+    q, k, v = fill((T, H_QK, DK)), fill((T, H_QK, DK)), fill((T, HV, DV))
+    state = fill((N, HV, DV, DK), bf16=False)
+    A_log, a, dt_bias, b = fill((HV,), False), fill((T, HV)), fill((HV,), False), fill((T, HV))
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    return dict(q=q, k=k, v=v, state=state if with_state else None, A_log=A_log, a=a,
+                dt_bias=dt_bias, b=b, cu_seqlens=cu, scale=1.0 / math.sqrt(DK))
+
+
 # The workloads of BASELINE.json, in one place.
 CONFIGS = {
     "decode_b1": dict(kind="decode", B=1, seed=0),
