@@ -45,9 +45,11 @@
 //            intra kernel's HBM traffic and fewer bytes per step -- best
 //            when many sequences keep every CU and the memory system busy.
 // Rule (index kernel, t_form_wins in gdn_common.h, from sweeps of both on
-// MI355X): the T form from 192 chunks on when the batch holds more than three
-// times the chunks of its longest sequence, or from 384 on with at least
-// twice.  One sequence always takes the WY form.
+// MI355X): the T form from 144 chunks on when the batch holds more than three
+// times the chunks of its longest sequence, or from 384 on with at least 1.5
+// times; and for small batches of at most 768 state units (sequence x v-head
+// x 16-column block) whose longest sequence has at most 12 chunks.  One
+// sequence always takes the WY form.
 //
 // Precision.  The state recurrence must hold 1e-3 of max|S| after 128-512
 // chunks.  Rounding any operand of w S or K^T v_new (or u, w themselves) to
@@ -2254,6 +2256,13 @@ __global__ __launch_bounds__(256) void prefill_zero_kernel(uint16_t *out, const 
   zero_uncovered_rows(out, cu, cu64, 0, T, hv, blockIdx.x, gridDim.x);
 }
 
+// The contract bits of one sequence whose call launches no intra kernel (no
+// tokens: the intra kernel otherwise writes them).
+__global__ __launch_bounds__(64) void prefill_status_kernel(const void *cu, int cu64, int T,
+                                                          int *status) {
+  if (threadIdx.x == 0) status[0] = cu_status_bits(raw_cu(cu, cu64, 0), raw_cu(cu, cu64, 1), T);
+}
+
 static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
                           const float *state, const float *A_log, const gdn_bf16 *a,
                           const float *dt_bias, const gdn_bf16 *b, const void *cu_seqlens,
@@ -2335,6 +2344,11 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   }
   if (P.choose != 0 && P.self_index) {
     if ((rc = sequential_kernel())) return rc;
+  }
+  if (P.single && P.intra_grid == 0) {
+    hipLaunchKernelGGL(prefill_status_kernel, dim3(1), dim3(64), 0, stream, cu_seqlens, cu64, T,
+                       status);
+    if ((rc = check_launch(what))) return rc;
   }
   SplitScan sp{P.split_nt0, nullptr, nullptr, nullptr, nullptr};
   if (sp.nt0 > 0) {

@@ -212,10 +212,12 @@ int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
  * shortest chain), 1 = T form (the intra kernel stores only (I+A)^-1; each
  * state step forms beta V - beta e^G K S from the inputs: less memory
  * traffic, one more exchange per step), -1 = the built-in choice (what
- * gdn_prefill_fwd uses: the T form for batches of at least 192 chunks with
- * more than three times the chunks of their longest sequence, or of at least
- * 384 with at least twice, decided on the device; the WY form otherwise and
- * for one sequence), 2 = WY form with one
+ * gdn_prefill_fwd uses, decided on the device: the T form for batches of at
+ * least 144 chunks with more than three times the chunks of their longest
+ * sequence, or of at least 384 with at least 1.5 times, and for batches of
+ * at most 768 state units -- sequence x v-head x 16-column block -- whose
+ * longest sequence has at most 12 chunks; the WY form otherwise and for one
+ * sequence: t_form_wins in csrc/gdn_common.h), 2 = WY form with one
  * serial chain of state steps per sequence, 3 = WY form with the two-segment
  * scan for a single sequence of at least two chunks (the second half of the
  * chunks runs beside the first from a zero state and from the identity, and

@@ -154,3 +154,22 @@ def test_status_of_the_allocation_free_entry_point(cuda_device):
         rc = lib.gdn_prefill_status(None, T, 3, 4, 8, stream, ctypes.byref(got))
         _lib.check(rc, "gdn_prefill_status")
         assert got.value == want, cu
+
+
+@pytest.mark.parametrize("rec_max", [-2, -1])
+def test_status_of_a_call_without_tokens(cuda_device, rec_max):
+    # T = 0 and one sequence: through the chunks (-2) no intra kernel runs, so
+    # the status word has a launch of its own; a stale word from the previous
+    # call of the same (T, N) must not survive.
+    dev = cuda_device
+    print(f"status T=0 N=1 rec_max={rec_max}", flush=True)
+    for cu, want in (([0, 5], 2), ([0, 0], 0), ([3, 1], 3), ([0, 0], 0)):
+        inp = _inputs(0, cu, seed=11, int64=True)
+        d = _to_dev(inp, dev)
+        out = torch.empty((0, 8, 128), dtype=torch.bfloat16, device=dev)
+        ns = torch.full((1, 8, 128, 128), 7.0, dtype=torch.float32, device=dev)
+        prefill.kernel(d["q"], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"],
+                       d["b"], d["cu_seqlens"], inp["scale"], out, ns, recurrent_max_len=rec_max)
+        assert prefill.batch_status(0, 1) == want, cu
+        if want == 0:  # a zero-length sequence: zero state (gdn_prefill_ref.py:61-62)
+            assert not ns.cpu().numpy().any()
