@@ -54,6 +54,72 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+# Every reported time is the median of TRIALS timed trials, with the min and
+# max beside it (the reference's harness reports the median,
+# scripts/benchmark.py:23-39).
+TRIALS = 5
+
+
+class Timing(tuple):
+    """Per-call time over trials, in ms: (median, min, max, trials)."""
+
+    def __new__(cls, times_ms):
+        import statistics
+        return super().__new__(cls, (statistics.median(times_ms), min(times_ms), max(times_ms),
+                                     len(times_ms)))
+
+    ms = property(lambda self: self[0])
+    lo = property(lambda self: self[1])
+    hi = property(lambda self: self[2])
+    n = property(lambda self: self[3])
+
+    def js(self, scale=1.0, digits=4):
+        """{"median", "min", "max", "trials"} in ms (scale=1e3: µs)."""
+        return {"median": round(self.ms * scale, digits), "min": round(self.lo * scale, digits),
+                "max": round(self.hi * scale, digits), "trials": self.n}
+
+
+def _event_ms(fn):
+    """Milliseconds between HIP events recorded before and after fn() on
+    torch's current stream (the stream every call here launches on)."""
+    import torch
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    fn()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1)
+
+
+def _trials(fn, calls, trials=TRIALS):
+    """Timing per call of `calls` calls made by each fn(), over `trials` runs."""
+    return Timing([_event_ms(fn) / calls for _ in range(trials)])
+
+
+def _graph_trials(graph, calls, trials=TRIALS):
+    """Steady-state Timing per call of a captured graph of `calls` calls: each
+    timed replay is enqueued right behind an untimed replay of the same graph,
+    so the device is busy when the first timed call starts and the graph's
+    launch latency (~7 us, 0.35 us per step at 20 decode steps) falls outside
+    the timed region, as it does for every step but the first of a serving
+    loop.  The events bracket exactly `calls` calls."""
+    import torch
+    times = []
+    for _ in range(trials):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        graph.replay()  # untimed: keeps the device busy while the timed replay is enqueued
+        t0.record()
+        graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        times.append(t0.elapsed_time(t1) / calls)
+    return Timing(times)
+
+
 def _dev_inputs(inp, dev):
     import numpy as np
     import torch
@@ -85,7 +151,7 @@ ONLY_WORKLOADS = {
 
 def bench_decode(B, steps, warmup, dev, variant=-1, tokens=1):
     """Times `steps` decode calls at batch B (`tokens` tokens per row; 1 is the
-    plain decode step) two ways and returns (eager ms/call, graph ms/call).
+    plain decode step) two ways and returns (eager, graph) Timings per call.
 
     eager: back-to-back calls of the DPS entry point (validation, ctypes call
     and launch on the host each time).  graph: the same `steps` launches
@@ -115,19 +181,9 @@ def bench_decode(B, steps, warmup, dev, variant=-1, tokens=1):
     def step(i):
         decode.kernel(*args, states[i % ROTATE], *tail, new_states[i % ROTATE], variant=variant)
 
-    def timed(fn):
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0.record()
-        fn()
-        t1.record()
-        torch.cuda.synchronize()
-        return t0.elapsed_time(t1)
-
     for i in range(warmup):
         step(i)
-    ms_eager = timed(lambda: [step(i) for i in range(steps)]) / steps
+    eager = _trials(lambda: [step(i) for i in range(steps)], steps)
 
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream(device=dev)
@@ -139,14 +195,13 @@ def bench_decode(B, steps, warmup, dev, variant=-1, tokens=1):
         for i in range(steps):
             step(i)
     graph.replay()
-    ms_graph = min(timed(graph.replay) for _ in range(3)) / steps
-    return ms_eager, ms_graph
+    return eager, _graph_trials(graph, steps)
 
 
 def bench_prefill(lens, steps, warmup, dev, variant=-1, slow_decay_heads=None):
     """Times `steps` prefill calls on a packed batch with sequence lengths
     `lens` (the configs[2..4] recipe, zero initial state for one sequence)
-    and returns (eager ms/call, graph ms/call)."""
+    and returns (eager, graph) Timings per call."""
     import numpy as np
     import torch
     from gdn_amd import prefill
@@ -164,19 +219,9 @@ def bench_prefill(lens, steps, warmup, dev, variant=-1, slow_decay_heads=None):
         prefill.kernel(d["q"], d["k"], d["v"], d["state"], d["A_log"], d["a"], d["dt_bias"],
                        d["b"], cu, inp["scale"], out, ns, variant=variant)
 
-    def timed(fn):
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0.record()
-        fn()
-        t1.record()
-        torch.cuda.synchronize()
-        return t0.elapsed_time(t1)
-
     for _ in range(warmup):
         step()
-    ms_eager = timed(lambda: [step() for _ in range(steps)]) / steps
+    eager = _trials(lambda: [step() for _ in range(steps)], steps)
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream(device=dev)
     side.wait_stream(torch.cuda.current_stream(dev))
@@ -187,8 +232,7 @@ def bench_prefill(lens, steps, warmup, dev, variant=-1, slow_decay_heads=None):
         for _ in range(steps):
             step()
     graph.replay()
-    ms_graph = min(timed(graph.replay) for _ in range(3)) / steps
-    return ms_eager, ms_graph
+    return eager, _graph_trials(graph, steps)
 
 
 def bench_prefill_rotated(lens, dev, min_bytes=768 << 20, steps=None):
@@ -196,7 +240,7 @@ def bench_prefill_rotated(lens, dev, min_bytes=768 << 20, steps=None):
     cycle over S distinct sets of inputs, outputs and workspace, S chosen so
     that the sets together exceed `min_bytes` (three times the 256 MB Infinity
     Cache), so no call finds its operands left in the MALL by the previous
-    call on the same set.  Returns (ms per call, S, bytes per set)."""
+    call on the same set.  Returns (Timing per call, S, bytes per set)."""
     import torch
     from gdn_amd import prefill
     from oracle import gdn_oracle as O  # input recipe only
@@ -234,28 +278,18 @@ def bench_prefill_rotated(lens, dev, min_bytes=768 << 20, steps=None):
         for i in range(steps):
             step(i)
     graph.replay()
-    best = None
-    for _ in range(3):
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0.record()
-        graph.replay()
-        t1.record()
-        torch.cuda.synchronize()
-        ms = t0.elapsed_time(t1) / steps
-        best = ms if best is None else min(best, ms)
+    timing = _graph_trials(graph, steps)
     del graph, sets
     torch.cuda.empty_cache()
-    return best, S, per_set
+    return timing, S, per_set
 
 
 def bench_prefill_clone(lens, reps, dev):
     """FlashInfer-Bench's clone mode (OPTIMIZATION_LOG.md:263-300): before each
     timed call every argument is cloned into fresh memory and the device is
     idle; the timed region is one DPS call from the host (validation, ctypes,
-    launches) to the end of its last kernel.  Returns the median ms/call."""
-    import statistics
+    launches) to the end of its last kernel.  Returns the Timing over the
+    `reps` calls after three untimed ones."""
     import torch
     from gdn_amd import prefill
     from oracle import gdn_oracle as O  # input recipe only
@@ -279,14 +313,14 @@ def bench_prefill_clone(lens, reps, dev):
         torch.cuda.synchronize()
         if i >= 3:
             times.append(t0.elapsed_time(t1))
-    return statistics.median(times)
+    return Timing(times)
 
 
 def bench_copy(nbytes, steps, warmup, dev):
     """The streaming ceiling of the decode step: `steps` calls of the library's
     gdn_stream_copy (the decode kernel's access pattern, nbytes read and
     nbytes written per call) over 8 rotating buffer pairs, captured in a HIP
-    graph as bench_decode's steps are; returns ms per call."""
+    graph as bench_decode's steps are; returns the Timing per call."""
     import torch
     from gdn_amd import _lib
     from gdn_amd._common import stream_of
@@ -312,18 +346,7 @@ def bench_copy(nbytes, steps, warmup, dev):
         for i in range(steps):
             step(i)
     graph.replay()
-    best = None
-    for _ in range(3):
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0.record()
-        graph.replay()
-        t1.record()
-        torch.cuda.synchronize()
-        ms = t0.elapsed_time(t1) / steps
-        best = ms if best is None else min(best, ms)
-    return best
+    return _graph_trials(graph, steps)
 
 
 def measured_traffic(path=os.path.join(ROOT, "profiles", "decode_b64_hbm_traffic.md")):
@@ -337,6 +360,21 @@ def measured_traffic(path=os.path.join(ROOT, "profiles", "decode_b64_hbm_traffic
     except OSError:
         pass
     return None
+
+
+def measured_mfma(path=os.path.join(ROOT, "profiles", "prefill_mfma_counters.md")):
+    """The prefill kernels' MFMA utilisation from the committed rocprofv3 PMC
+    summary (lines "mfma_util.<workload>.<kernel>: <fraction>"), or None when
+    the summary is absent."""
+    out = {}
+    try:
+        for line in open(path):
+            if line.startswith("mfma_util."):
+                key, val = line.split(":", 1)
+                out[key[len("mfma_util."):].strip()] = float(val)
+    except OSError:
+        return None
+    return out or None
 
 
 def host_cores():
@@ -458,31 +496,37 @@ def main():
     if args.only:
         kind, arg = ONLY_WORKLOADS[args.only]
         if kind == "decode":
-            me, mg = bench_decode(arg[0], args.steps, args.warmup, dev, tokens=arg[1])
+            te, tg = bench_decode(arg[0], args.steps, args.warmup, dev, tokens=arg[1])
         else:
-            me, mg = bench_prefill(arg, args.steps, args.warmup, dev)
-        log(f"{args.only}: eager {me * 1e3:.2f} us, graph {mg * 1e3:.2f} us per call")
+            te, tg = bench_prefill(arg, args.steps, args.warmup, dev)
+        log(f"{args.only}: eager {te.ms * 1e3:.2f} us, graph {tg.ms * 1e3:.2f} us per call "
+            f"(median of {tg.n}; graph min {tg.lo * 1e3:.2f}, max {tg.hi * 1e3:.2f})")
         return
 
     if args.sweep:
         for b in (1, 2, 4, 8, 16, 32, 48, 64):
             for var in [-1] + list(range(10)) + [16 + i for i in range(10)]:
-                me, mg = bench_decode(b, args.steps, args.warmup, dev, var)
-                gbs = O.decode_bytes(b) / (mg * 1e-3) / 1e9
-                log(f"sweep decode B={b:3d} variant={var:3d}: eager {me * 1e3:8.2f} us/step, "
-                    f"graph {mg * 1e3:8.2f} us/step, {gbs:8.1f} GB/s")
+                te, tg = bench_decode(b, args.steps, args.warmup, dev, var)
+                gbs = O.decode_bytes(b) / (tg.ms * 1e-3) / 1e9
+                log(f"sweep decode B={b:3d} variant={var:3d}: eager {te.ms * 1e3:8.2f} us/step, "
+                    f"graph {tg.ms * 1e3:8.2f} us/step, {gbs:8.1f} GB/s")
 
-    ms_eager, ms_step = bench_decode(B, args.steps, args.warmup, dev, args.variant)
+    # The headline: one decode step at B, K steps per graph replay, the median
+    # of TRIALS replays.
+    eager, graph = bench_decode(B, args.steps, args.warmup, dev, args.variant)
+    ms_step = graph.ms
     nbytes = O.decode_bytes(B)
-    gbs_step = nbytes / (ms_step * 1e-3) / 1e9
-    log(f"decode B={B}: graph {ms_step * 1e3:.2f} us/step ({gbs_step:.1f} GB/s, "
-        f"{gbs_step / HBM_PEAK_GBPS:.1%} of peak); eager {ms_eager * 1e3:.2f} us/step")
+    gbs = lambda ms: nbytes / (ms * 1e-3) / 1e9
+    gbs_step = gbs(ms_step)
+    log(f"decode B={B}: graph {ms_step * 1e3:.2f} us/step median of {graph.n} "
+        f"(min {graph.lo * 1e3:.2f}, max {graph.hi * 1e3:.2f}; {gbs_step:.1f} GB/s, "
+        f"{gbs_step / HBM_PEAK_GBPS:.1%} of peak); eager {eager.ms * 1e3:.2f} us/step")
     state_bytes = B * 8 * 128 * 128 * 4
-    copy_ms = bench_copy(state_bytes, args.steps, args.warmup, dev)
-    copy_gbs = 2 * state_bytes / (copy_ms * 1e-3) / 1e9
+    copy = bench_copy(state_bytes, args.steps, args.warmup, dev)
+    copy_gbs = 2 * state_bytes / (copy.ms * 1e-3) / 1e9
     log(f"copy of the decode state (read + write {2 * state_bytes >> 20} MiB, the decode "
-        f"kernel's access pattern): {copy_ms * 1e3:.2f} us/call ({copy_gbs:.1f} GB/s); decode "
-        f"step / copy = {ms_step / copy_ms:.3f}")
+        f"kernel's access pattern): {copy.ms * 1e3:.2f} us/call ({copy_gbs:.1f} GB/s); decode "
+        f"step / copy = {ms_step / copy.ms:.3f}")
 
     if args.sweep:
         for lens in ([1024], [6, 49, 294, 1800, 2040, 61], [8192], [8192] * 4, [64], [256]):
@@ -490,27 +534,29 @@ def main():
                 pe, pg = bench_prefill(lens, max(5, args.steps // 10), 3, dev, var)
                 T = sum(lens)
                 log(f"sweep prefill lens={lens if len(lens) < 5 else f'{len(lens)}x{lens[0]}'} "
-                    f"variant={var}: eager {pe:.3f} ms, graph {pg:.3f} ms, "
-                    f"{T / (pg * 1e-3) / 1e6:.2f} M tok/s")
+                    f"variant={var}: eager {pe.ms:.3f} ms, graph {pg.ms:.3f} ms, "
+                    f"{T / (pg.ms * 1e-3) / 1e6:.2f} M tok/s")
 
     pre_lens = [8192]
-    pre_eager, pre_ms = bench_prefill(pre_lens, max(10, args.steps // 10), 3, dev)
+    pre_eager, pre = bench_prefill(pre_lens, max(10, args.steps // 10), 3, dev)
+    pre_ms = pre.ms
     T8 = sum(pre_lens)
     nt8 = sum(-(-L // 64) for L in pre_lens)
     pre_tflops = O.prefill_flops(nt8) / (pre_ms * 1e-3) / 1e12
     pre_gbs = O.prefill_bytes(T8, len(pre_lens)) / (pre_ms * 1e-3) / 1e9
-    log(f"prefill 1x8192: graph {pre_ms:.3f} ms ({T8 / (pre_ms * 1e-3) / 1e6:.2f} M tok/s, "
-        f"{pre_tflops:.1f} TFLOP/s, {pre_gbs:.0f} GB/s); eager {pre_eager:.3f} ms")
+    log(f"prefill 1x8192: graph {pre_ms:.4f} ms median (min {pre.lo:.4f}, max {pre.hi:.4f}; "
+        f"{T8 / (pre_ms * 1e-3) / 1e6:.2f} M tok/s, {pre_tflops:.1f} TFLOP/s, {pre_gbs:.0f} GB/s); "
+        f"eager {pre_eager.ms:.4f} ms")
 
     pre_clone = bench_prefill_clone(pre_lens, 20, dev)
-    pre1k_eager, pre1k_ms = bench_prefill([1024], max(10, args.steps // 10), 3, dev)
+    pre1k_eager, pre1k = bench_prefill([1024], max(10, args.steps // 10), 3, dev)
     pre1k_clone = bench_prefill_clone([1024], 20, dev)
-    log(f"prefill clone mode: 1x8192 {pre_clone:.3f} ms, 1x1024 {pre1k_clone:.3f} ms; "
-        f"1x1024 graph {pre1k_ms:.3f} ms, eager {pre1k_eager:.3f} ms")
+    log(f"prefill clone mode: 1x8192 {pre_clone.ms:.3f} ms, 1x1024 {pre1k_clone.ms:.3f} ms; "
+        f"1x1024 graph {pre1k.ms:.3f} ms, eager {pre1k_eager.ms:.3f} ms")
     rotated = {}
     for name, lens in (("1x8192", pre_lens), ("1x1024", [1024])):
-        ms, sets, per_set = bench_prefill_rotated(lens, dev)
-        rotated[name] = {"ms": round(ms, 4), "sets": sets, "bytes_per_set": per_set}
+        t, sets, per_set = bench_prefill_rotated(lens, dev)
+        rotated[name] = {"ms": t.js(), "sets": sets, "bytes_per_set": per_set}
     log(f"prefill over rotating input/output/workspace sets (> 768 MiB in all): {rotated}")
 
     # The reference's other published points: prefill of one sequence of
@@ -521,21 +567,21 @@ def main():
         pe, pg = bench_prefill([L], 20, 3, dev)
         pc = bench_prefill_clone([L], 10, dev)
         ref_points["prefill"][f"1x{L}"] = {
-            "graph_ms": round(pg, 4), "eager_ms": round(pe, 4), "clone_ms": round(pc, 4),
+            "graph_ms": pg.js(), "eager_ms": pe.js(), "clone_ms": pc.js(),
             "b200_reuse_ms": B200_PREFILL_REUSE_MS.get(L),
             "b200_clone_ms": B200_PREFILL_CLONE_MS.get(L)}
     for b in (128, 512):
-        me, mg = bench_decode(b, 50, 5, dev)
+        te, tg = bench_decode(b, 50, 5, dev)
         ref_points["decode"][f"B{b}"] = {
-            "us": round(mg * 1e3, 3), "us_eager": round(me * 1e3, 3),
-            "GBps": round(O.decode_bytes(b) / (mg * 1e-3) / 1e9, 1),
+            "us": tg.js(1e3, 3), "us_eager": te.js(1e3, 3),
+            "GBps": round(O.decode_bytes(b) / (tg.ms * 1e-3) / 1e9, 1),
             "b200_device_us": B200_DECODE_DEVICE_US[b]}
     log(f"reference points: {ref_points}")
 
     mtp = {}
     for T in (2, 4, 8, 16):
-        _, mg = bench_decode(64, 50, 5, dev, tokens=T)
-        mtp[f"B64_T{T}"] = round(mg * 1e3, 2)
+        _, tg = bench_decode(64, 50, 5, dev, tokens=T)
+        mtp[f"B64_T{T}"] = tg.js(1e3, 2)
     log(f"multi-token decode B=64 (us per call): {mtp}")
     # Short batches: one input set replayed (warm in the Infinity Cache, as
     # the other single-set lines) and over rotating sets (cache-cold, as a
@@ -544,9 +590,9 @@ def main():
     for name, lens in (("256x1", [1] * 256), ("64x16", [16] * 64), ("1x64", [64]),
                        ("32x64", [64] * 32), ("64x256", [256] * 64)):
         _, pg = bench_prefill(lens, 20, 3, dev)
-        short[name] = round(pg, 4)
+        short[name] = pg.js()
         if len(lens) > 1:  # (one 64-token sequence would need ~1000 sets)
-            short_rot[name] = round(bench_prefill_rotated(lens, dev)[0], 4)
+            short_rot[name] = bench_prefill_rotated(lens, dev)[0].js()
     log(f"short-sequence prefill (ms per call): {short}, over rotating sets {short_rot}")
 
     # the decode batch sweep (one step in graph replay per B), and
@@ -555,29 +601,27 @@ def main():
     # decay.
     sweep = {}
     for b in (1, 2, 4, 8, 16, 32, 48, 64):
-        _, mg = bench_decode(b, 100, 10, dev)
-        sweep[f"B{b}"] = {"us": round(mg * 1e3, 3),
-                          "GBps": round(O.decode_bytes(b) / (mg * 1e-3) / 1e9, 1)}
+        _, tg = bench_decode(b, 100, 10, dev)
+        sweep[f"B{b}"] = {"us": tg.js(1e3, 3),
+                          "GBps": round(O.decode_bytes(b) / (tg.ms * 1e-3) / 1e9, 1)}
     log(f"decode sweep (graph us/step, GB/s): {sweep}")
-    cfg_ms = {}
     cfg_detail = {}
 
-    def detail(lens, ms):
+    def detail(lens, t):
         T, N = sum(lens), len(lens)
         nt = sum(-(-L // 64) for L in lens)
-        tflops = O.prefill_flops(nt) / (ms * 1e-3) / 1e12
-        return {"ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+        tflops = O.prefill_flops(nt) / (t.ms * 1e-3) / 1e12
+        return {"ms": t.js(), "tokens_per_s": round(T / (t.ms * 1e-3), 1),
                 "tflops": round(tflops, 2), "mfma_frac": round(tflops / 2500.0, 5),
-                "hbm_gbps": round(O.prefill_bytes(T, N) / (ms * 1e-3) / 1e9, 1)}
+                "hbm_gbps": round(O.prefill_bytes(T, N) / (t.ms * 1e-3) / 1e9, 1)}
 
     for name, lens, kw in (("configs3_varlen6", [6, 49, 294, 1800, 2040, 61], {}),
                            ("configs4_4x8192", [8192] * 4, {"slow_decay_heads": (6, 7)})):
         _, pg = bench_prefill(lens, 10, 2, dev, **kw)
-        cfg_ms[name] = round(pg, 4)
         cfg_detail[name] = detail(lens, pg)
-    cfg_detail["configs2_1x1024"] = detail([1024], pre1k_ms)
-    cfg_detail["north_star_1x8192"] = detail(pre_lens, pre_ms)
-    log(f"prefill configs (graph ms per call): {cfg_ms}")
+    cfg_detail["configs2_1x1024"] = detail([1024], pre1k)
+    cfg_detail["north_star_1x8192"] = detail(pre_lens, pre)
+    log(f"prefill configs: {cfg_detail}")
 
     # CPU baseline (the reference's loops restated; a reported baseline, not a
     # target): about --cpu-seconds of CPU work in all.
@@ -611,23 +655,26 @@ def main():
         "data": "synthetic: numpy default_rng(seed=1), configs[1] recipe; 8 rotating state buffers",
         "config": {"workload": f"decode step, B={B} (configs[1]), k-last f32 state",
                    "batch": B, "heads_qk": 4, "heads_v": 8, "head_dim": 128},
-        "decode_us_per_step": round(ms_step * 1e3, 3),
-        "decode_us_per_step_eager": round(ms_eager * 1e3, 3),
-        "decode_copy_ceiling": {"us": round(copy_ms * 1e3, 3), "GBps": round(copy_gbs, 1),
+        "statistic": f"median of {graph.n} HIP-graph replays of the {args.steps} steps; "
+                     "every other time in this line: median, min and max of its trials",
+        "decode_us_per_step": graph.js(1e3, 3),
+        "decode_GBps_min_max": [round(gbs(graph.hi), 1), round(gbs(graph.lo), 1)],
+        "decode_us_per_step_eager": eager.js(1e3, 3),
+        "decode_copy_ceiling": {"us": copy.js(1e3, 3), "GBps": round(copy_gbs, 1),
                                 "bytes_moved": 2 * state_bytes,
-                                "decode_time_over_copy": round(ms_step / copy_ms, 4)},
+                                "decode_time_over_copy": round(ms_step / copy.ms, 4)},
         "prefill_ms_1x8192": round(pre_ms, 4),
-        "prefill_ms_1x8192_eager": round(pre_eager, 4),
+        "prefill_ms_1x8192_trials": pre.js(),
+        "prefill_ms_1x8192_eager": pre_eager.js(),
         "prefill_tokens_per_s": round(T8 / (pre_ms * 1e-3), 1),
-        "prefill_ms_1x8192_clone": round(pre_clone, 4),
-        "prefill_ms_1x1024": round(pre1k_ms, 4),
-        "prefill_ms_1x1024_clone": round(pre1k_clone, 4),
+        "prefill_ms_1x8192_clone": pre_clone.js(),
+        "prefill_ms_1x1024": pre1k.js(),
+        "prefill_ms_1x1024_clone": pre1k_clone.js(),
         "prefill_ms_1x8192_rotated": rotated["1x8192"]["ms"],
         "prefill_ms_1x1024_rotated": rotated["1x1024"]["ms"],
         "prefill_rotated_sets": rotated,
         "reference_points": ref_points,
         "decode_sweep": sweep,
-        "prefill_ms_configs": cfg_ms,
         "prefill_configs": cfg_detail,
         "decode_multi_token_us": mtp,
         "prefill_ms_short_batches": short,
@@ -636,7 +683,8 @@ def main():
                              "unit": "TFLOP/s", "frac": round(pre_tflops / 2500.0, 5),
                              "hbm_gbs": round(pre_gbs, 1),
                              "flops_per_call": O.prefill_flops(nt8),
-                             "bytes_per_call": O.prefill_bytes(T8, len(pre_lens))},
+                             "bytes_per_call": O.prefill_bytes(T8, len(pre_lens)),
+                             "counters": measured_mfma()},
         "roofline": {"bound": "hbm", "achieved": round(gbs_step, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(gbs_step / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic() if (B == 64 and args.variant == -1) else None,
