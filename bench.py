@@ -363,15 +363,16 @@ def measured_traffic(path=os.path.join(ROOT, "profiles", "decode_b64_hbm_traffic
 
 
 def measured_mfma(path=os.path.join(ROOT, "profiles", "prefill_mfma_counters.md")):
-    """The prefill kernels' MFMA utilisation from the committed rocprofv3 PMC
-    summary (lines "mfma_util.<workload>.<kernel>: <fraction>"), or None when
-    the summary is absent."""
+    """The prefill kernels' MFMA counters from the committed rocprofv3 PMC
+    summary: lines "mfma_util.<workload>.<kernel>: <fraction of time the
+    matrix cores are busy>" and "mfma_executed_over_algorithmic.<workload>:
+    <ratio>", keyed by the line's name; None when the summary is absent."""
     out = {}
     try:
         for line in open(path):
-            if line.startswith("mfma_util."):
+            if line.startswith(("mfma_util.", "mfma_executed_over_algorithmic.")):
                 key, val = line.split(":", 1)
-                out[key[len("mfma_util."):].strip()] = float(val)
+                out[key.strip()] = float(val)
     except OSError:
         return None
     return out or None
