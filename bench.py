@@ -99,54 +99,10 @@ def _trials(fn, calls, trials=TRIALS):
 
 
 def _graph_trials(graph, calls, trials=TRIALS):
-    """Steady-state Timing per call of a captured graph of `calls` calls: each
-    timed replay is enqueued right behind an untimed replay of the same graph,
-    so the device is busy when the first timed call starts and the graph's
-    launch latency (~7 us, 0.35 us per step at 20 decode steps) falls outside
-    the timed region, as it does for every step but the first of a serving
-    loop.  The events bracket exactly `calls` calls."""
-    import torch
-    times = []
-    for _ in range(trials):
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        graph.replay()  # untimed: keeps the device busy while the timed replay is enqueued
-        t0.record()
-        graph.replay()
-        t1.record()
-        torch.cuda.synchronize()
-        times.append(t0.elapsed_time(t1) / calls)
-    return Timing(times)
-
-
-def _dev_inputs(inp, dev):
-    import numpy as np
-    import torch
-    d = {}
-    for name in ("q", "k", "v", "a", "b"):
-        d[name] = torch.from_numpy(np.ascontiguousarray(inp[name])).to(dev).to(torch.bfloat16)
-    for name in ("A_log", "dt_bias"):
-        d[name] = torch.from_numpy(inp[name]).to(dev)
-    d["state"] = None if inp["state"] is None else torch.from_numpy(inp["state"]).to(dev)
-    return d
-
-
-# Single workloads for `--only` (profiling): decode (batch, tokens per row)
-# or prefill sequence lengths.
-ONLY_WORKLOADS = {
-    "decode_b64": ("decode", (64, 1)),
-    "decode_b64_t4": ("decode", (64, 4)),
-    "decode_b64_t16": ("decode", (64, 16)),
-    "prefill_1x8192": ("prefill", [8192]),
-    "prefill_4x8192": ("prefill", [8192] * 4),
-    "prefill_1x1024": ("prefill", [1024]),
-    "prefill_64x16": ("prefill", [16] * 64),
-    "prefill_256x1": ("prefill", [1] * 256),
-    "prefill_64x256": ("prefill", [256] * 64),
-    "prefill_configs3": ("prefill", [6, 49, 294, 1800, 2040, 61]),
-    "prefill_8x2048": ("prefill", [2048] * 8),
-}
+    """Timing per call of a captured graph of `calls` calls: each trial
+    synchronizes, then HIP events on the replay stream bracket one replay
+    (exactly `calls` calls) and it synchronizes again."""
+    return _trials(graph.replay, calls, trials)
 
 
 def bench_decode(B, steps, warmup, dev, variant=-1, tokens=1):
