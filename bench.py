@@ -105,6 +105,35 @@ def _graph_trials(graph, calls, trials=TRIALS):
     return _trials(graph.replay, calls, trials)
 
 
+def _dev_inputs(inp, dev):
+    import numpy as np
+    import torch
+    d = {}
+    for name in ("q", "k", "v", "a", "b"):
+        d[name] = torch.from_numpy(np.ascontiguousarray(inp[name])).to(dev).to(torch.bfloat16)
+    for name in ("A_log", "dt_bias"):
+        d[name] = torch.from_numpy(inp[name]).to(dev)
+    d["state"] = None if inp["state"] is None else torch.from_numpy(inp["state"]).to(dev)
+    return d
+
+
+# Single workloads for `--only` (profiling): decode (batch, tokens per row)
+# or prefill sequence lengths.
+ONLY_WORKLOADS = {
+    "decode_b64": ("decode", (64, 1)),
+    "decode_b64_t4": ("decode", (64, 4)),
+    "decode_b64_t16": ("decode", (64, 16)),
+    "prefill_1x8192": ("prefill", [8192]),
+    "prefill_4x8192": ("prefill", [8192] * 4),
+    "prefill_1x1024": ("prefill", [1024]),
+    "prefill_64x16": ("prefill", [16] * 64),
+    "prefill_256x1": ("prefill", [1] * 256),
+    "prefill_64x256": ("prefill", [256] * 64),
+    "prefill_configs3": ("prefill", [6, 49, 294, 1800, 2040, 61]),
+    "prefill_8x2048": ("prefill", [2048] * 8),
+}
+
+
 def bench_decode(B, steps, warmup, dev, variant=-1, tokens=1):
     """Times `steps` decode calls at batch B (`tokens` tokens per row; 1 is the
     plain decode step) two ways and returns (eager, graph) Timings per call.

@@ -56,3 +56,24 @@ def test_fast_ok_rejects_non_tensors_and_mismatches():
     t = torch.zeros(2, 3)
     assert not _common.fast_ok((t,), (torch.float32,), ((2, 3),))  # host tensor
     assert not _common.fast_ok((None,), (torch.float32,), ((2, 3),))
+
+
+def test_bench_script_imports_and_refuses_more_gpus():
+    # bench.py's helpers and profiling workloads exist; --gpus N > 1 exits 2
+    # before touching a device
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, root)
+    import bench
+    for name in ("bench_decode", "bench_prefill", "bench_prefill_rotated", "bench_prefill_clone",
+                 "bench_copy", "_dev_inputs", "measured_traffic", "measured_mfma", "main"):
+        assert callable(getattr(bench, name)), name
+    assert "decode_b64" in bench.ONLY_WORKLOADS and "prefill_1x8192" in bench.ONLY_WORKLOADS
+    t = bench.Timing([3.0, 1.0, 2.0, 5.0, 4.0])
+    assert (t.ms, t.lo, t.hi, t.n) == (3.0, 1.0, 5.0, 5)
+    assert bench.measured_traffic() > 0 and bench.measured_mfma()["mfma_util.1x8192.call"] > 0
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr
