@@ -22,6 +22,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep]
 """
 
 import argparse
+import hashlib
 import json
 import math
 import os
@@ -334,32 +335,62 @@ def bench_copy(nbytes, steps, warmup, dev):
     return _graph_trials(graph, steps)
 
 
-def measured_traffic(path=os.path.join(ROOT, "profiles", "decode_b64_hbm_traffic.md")):
+KERNEL_SOURCE_DIRS = ("gated-delta-network_amd/csrc", "include")
+
+
+def kernel_sources_sha16(root=ROOT):
+    """The first 16 hex digits of a SHA-256 over the kernel and C-ABI sources
+    (the .hip, .h and .cpp files and the Makefile of the directories above,
+    by name).  The committed counter summaries name the value they were
+    measured on ("kernel_sources_sha16: ..."), so that a summary left behind
+    by a kernel change is not read as current."""
+    h = hashlib.sha256()
+    for d in KERNEL_SOURCE_DIRS:
+        base = os.path.join(root, d)
+        for name in sorted(os.listdir(base)):
+            path = os.path.join(base, name)
+            if os.path.isfile(path) and (name.endswith((".hip", ".h", ".cpp")) or name == "Makefile"):
+                h.update(f"{d}/{name}\0".encode())
+                with open(path, "rb") as f:
+                    h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def _current_summary_lines(path, sources=None):
+    """The lines of a committed counter summary, or None when it is absent
+    or was measured on other kernel sources than the tree's."""
+    try:
+        with open(path) as f:
+            lines = f.readlines()
+    except OSError:
+        return None
+    stamp = [ln.split(":", 1)[1].strip() for ln in lines if ln.startswith("kernel_sources_sha16:")]
+    if not stamp or stamp[0] != (sources or kernel_sources_sha16()):
+        return None
+    return lines
+
+
+def measured_traffic(path=os.path.join(ROOT, "profiles", "decode_b64_hbm_traffic.md"), sources=None):
     """HBM bytes per decode launch at B=64 from the committed rocprofv3 PMC
     summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of known size);
-    None when the summary is absent."""
-    try:
-        for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1])
-    except OSError:
-        pass
+    None when the summary is absent or stale (other kernel sources)."""
+    for line in _current_summary_lines(path, sources) or ():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
     return None
 
 
-def measured_mfma(path=os.path.join(ROOT, "profiles", "prefill_mfma_counters.md")):
+def measured_mfma(path=os.path.join(ROOT, "profiles", "prefill_mfma_counters.md"), sources=None):
     """The prefill kernels' MFMA counters from the committed rocprofv3 PMC
     summary: lines "mfma_util.<workload>.<kernel>: <fraction of time the
     matrix cores are busy>" and "mfma_executed_over_algorithmic.<workload>:
-    <ratio>", keyed by the line's name; None when the summary is absent."""
+    <ratio>", keyed by the line's name; None when the summary is absent or
+    stale (other kernel sources)."""
     out = {}
-    try:
-        for line in open(path):
-            if line.startswith(("mfma_util.", "mfma_executed_over_algorithmic.")):
-                key, val = line.split(":", 1)
-                out[key.strip()] = float(val)
-    except OSError:
-        return None
+    for line in _current_summary_lines(path, sources) or ():
+        if line.startswith(("mfma_util.", "mfma_executed_over_algorithmic.")):
+            key, val = line.split(":", 1)
+            out[key.strip()] = float(val)
     return out or None
 
 
@@ -674,6 +705,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs_step, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(gbs_step / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic() if (B == 64 and args.variant == -1) else None,
+                     "traffic_source": "profiles/decode_b64_hbm_traffic.md (rocprofv3 PMC; "
+                                       "null when measured on other kernel sources than "
+                                       f"these, sha16 {kernel_sources_sha16()})",
                      "kernel": "gdn::decode_kernel",
                      "bytes_per_launch": nbytes},
         "cpu_baseline": {

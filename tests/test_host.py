@@ -73,7 +73,25 @@ def test_bench_script_imports_and_refuses_more_gpus():
     assert "decode_b64" in bench.ONLY_WORKLOADS and "prefill_1x8192" in bench.ONLY_WORKLOADS
     t = bench.Timing([3.0, 1.0, 2.0, 5.0, 4.0])
     assert (t.ms, t.lo, t.hi, t.n) == (3.0, 1.0, 5.0, 5)
-    assert bench.measured_traffic() > 0 and bench.measured_mfma()["mfma_util.1x8192.call"] > 0
+    # the committed counter summaries name the kernel sources they were
+    # measured on, and are read only while the tree's sources match
+    for f in ("decode_b64_hbm_traffic.md", "prefill_mfma_counters.md", "prefill_hbm_traffic.md"):
+        with open(os.path.join(root, "profiles", f)) as fh:
+            assert any(ln.startswith("kernel_sources_sha16: ") for ln in fh), f
+    sha = bench.kernel_sources_sha16()
+    assert len(sha) == 16 and int(sha, 16) >= 0
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        cur, old = os.path.join(d, "cur.md"), os.path.join(d, "old.md")
+        body = "traffic_bytes_per_launch: 123\nmfma_util.x.call: 0.5\n"
+        with open(cur, "w") as fh:
+            fh.write(f"kernel_sources_sha16: {sha}\n" + body)
+        with open(old, "w") as fh:
+            fh.write("kernel_sources_sha16: 0123456789abcdef\n" + body)
+        assert bench.measured_traffic(cur) == 123
+        assert bench.measured_mfma(cur) == {"mfma_util.x.call": 0.5}
+        assert bench.measured_traffic(old) is None and bench.measured_mfma(old) is None
+        assert bench.measured_traffic(os.path.join(d, "absent.md")) is None
     r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
