@@ -56,6 +56,23 @@ __device__ __forceinline__ float dpp(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
 }
 
+// Lane j of each aligned group of 16 lanes (one DPP "row"), to every lane of
+// the group: DPP row_newbcast:j (control 0x150 + j).  j must be a constant
+// after unrolling.
+__device__ __forceinline__ float row_bcast16(float x, int j) {
+  switch (j) {
+#define GDN_BCAST(J) \
+  case J:            \
+    return dpp<0x150 + J>(x);
+    GDN_BCAST(0) GDN_BCAST(1) GDN_BCAST(2) GDN_BCAST(3) GDN_BCAST(4) GDN_BCAST(5) GDN_BCAST(6)
+    GDN_BCAST(7) GDN_BCAST(8) GDN_BCAST(9) GDN_BCAST(10) GDN_BCAST(11) GDN_BCAST(12)
+    GDN_BCAST(13) GDN_BCAST(14) GDN_BCAST(15)
+#undef GDN_BCAST
+    default:
+      return x;
+  }
+}
+
 // Sum over each aligned group of 16 lanes (one DPP "row"); every lane of the
 // group receives the total.  Four DPP adds, no LDS traffic.
 __device__ __forceinline__ float row16_sum(float x) {
@@ -261,6 +278,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uin
 }
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+// Streaming 16-byte accesses through a descriptor, cache policy nt (bit 1 of
+// the instruction's cache-policy operand): for state read or written once
+// (decode at B=64: ~1 % faster than flat non-temporal accesses).
+constexpr int kCachePolicyNt = 2;
+__device__ __forceinline__ f32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0,
+                                                                         kCachePolicyNt));
+}
+__device__ __forceinline__ void buf_store16_nt(__amdgpu_buffer_rsrc_t r, uint32_t byte_off,
+                                               f32x4 x) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, byte_off, 0,
+                                         kCachePolicyNt);
 }
 // One float at a wave-uniform address, as a vector load issued in program
 // order with the fragments it belongs to.
