@@ -73,7 +73,6 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
   // by block parity: G, beta, e^G and e^(G_last - G) of each token
   __shared__ float sG[2][kBlk], sBeta[2][kBlk], sEG[2][kBlk], sED[2][kBlk];
 
-  if (enable != nullptr && *enable == 0) return;  // the batch went through the chunks
   const int half = CV == 2 ? 0 : static_cast<int>(blockIdx.x & 1u);
   const int pair = CV == 2 ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x >> 1);
   const int h = pair % H.v, s = pair / H.v;
@@ -83,14 +82,22 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
   const int r16 = lane & 15, g = lane >> 4, q4 = 4 * g, kg = 8 * g;
   const int hq = h / H.ratio;
 
+  // The path flag and the sequence's bounds, loaded together (one wait).
+  const int en = enable != nullptr ? *enable : 1;
+  long long lo = 0, hi = 0;
+  if (cu != nullptr) {
+    lo = raw_cu(cu, cu64, s);
+    hi = raw_cu(cu, cu64, s + 1);
+  }
+  if (en == 0) return;  // the batch went through the chunks
   int bos, len;
   if (cu != nullptr) {
-    bos = load_cu(cu, cu64, s, T);
-    const int eos = load_cu(cu, cu64, s + 1, T);
+    bos = static_cast<int>(lo < 0 ? 0 : lo > T ? T : lo);
+    const int eos = static_cast<int>(hi < 0 ? 0 : hi > T ? T : hi);
     len = eos > bos ? eos - bos : 0;
     // the batch's contract bits, one entry per sequence (host-routed batches)
     if (status != nullptr && h == 0 && half == 0 && threadIdx.x == 0)
-      status[s] = cu_status_bits(raw_cu(cu, cu64, s), raw_cu(cu, cu64, s + 1), T);
+      status[s] = cu_status_bits(lo, hi, T);
   } else {
     bos = s * fixed_len;
     len = fixed_len;

@@ -48,7 +48,6 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
   constexpr int kTiles = kDV / kRows;
   static_assert(kDV % kRows == 0, "row block must divide 128");
 
-  if (enable != nullptr && *enable == 0) return;  // the batch went through the chunks
   const int h = blockIdx.x % H.v;  // consecutive workgroups: the v-heads
   const int rest = blockIdx.x / H.v;
   const int tile = rest % kTiles, s = rest / kTiles;
@@ -56,34 +55,51 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
   const int c4 = 4 * (lane & 15);
   const int row0 = tile * kRows + wave * 4 * PASSES + (lane >> 4);  // pass p: row0 + 4p
 
+  // The path flag and the sequence's bounds, loaded together (one wait for
+  // both), before the state loads, which do not depend on them.
+  const int en = enable != nullptr ? *enable : 1;
+  long long lo = 0, hi = 0;
+  if (cu != nullptr) {
+    lo = raw_cu(cu, cu64, s);
+    hi = raw_cu(cu, cu64, s + 1);
+  }
+  if (en == 0) return;  // the batch went through the chunks
   int bos, len;
   if (cu != nullptr) {
-    bos = load_cu(cu, cu64, s, T);
-    const int eos = load_cu(cu, cu64, s + 1, T);
+    bos = static_cast<int>(lo < 0 ? 0 : lo > T ? T : lo);
+    const int eos = static_cast<int>(hi < 0 ? 0 : hi > T ? T : hi);
     len = eos > bos ? eos - bos : 0;
     // the batch's contract bits, one entry per sequence (host-routed batches)
     if (status != nullptr && h == 0 && tile == 0 && threadIdx.x == 0)
-      status[s] = cu_status_bits(raw_cu(cu, cu64, s), raw_cu(cu, cu64, s + 1), T);
+      status[s] = cu_status_bits(lo, hi, T);
   } else {
     bos = s * fixed_len;
     len = fixed_len;
   }
   const int hq = h / H.ratio;
-  // The state is read once and written once: non-temporal accesses, as in
-  // the decode kernel (over rotating state sets: B=64 T=2 decode 15.3 ->
-  // 12.5 us, 256x1 prefill 63.2 -> 58.5 us).
+  // The state is read once and written once: non-temporal accesses through
+  // a descriptor of the (sequence, head) state, as in the decode kernel (over
+  // rotating state sets: B=64 T=2 decode 15.3 -> 12.5 us, 256x1 prefill 63.2
+  // -> 58.5 us against plain accesses).  The loads do not wait for the
+  // sequence's length: a zero-length sequence's state is read and dropped.
   const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;
+  constexpr uint32_t kHeadBytes = kDV * kDK * 4;
   f32x4 Sa[PASSES], Sb[PASSES];  // columns c4.. and 64 + c4..
+  if (state != nullptr) {
+    const auto rs = buf_rsrc(state + sbase, kHeadBytes);
 #pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    const size_t off = sbase + static_cast<size_t>(row0 + 4 * p) * kDK + c4;
-    if (state != nullptr && len > 0) {
-      Sa[p] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(state + off));
-      Sb[p] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(state + off + 64));
-    } else {
-      Sa[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-      Sb[p] = Sa[p];
+    for (int p = 0; p < PASSES; ++p) {
+      const uint32_t off = static_cast<uint32_t>((row0 + 4 * p) * kDK + c4) * 4u;
+      Sa[p] = buf_load16_nt(rs, off);
+      Sb[p] = buf_load16_nt(rs, off + 256u);
     }
+    if (len == 0) {
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) Sa[p] = Sb[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) Sa[p] = Sb[p] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   if (len > 0) {
@@ -195,11 +211,12 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
   }
 
   // Final state; all zeros for a zero-length sequence (gdn_prefill_ref.py:61-62).
+  const auto rd = buf_rsrc(new_state + sbase, kHeadBytes);
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
-    const size_t off = sbase + static_cast<size_t>(row0 + 4 * p) * kDK + c4;
-    __builtin_nontemporal_store(Sa[p], reinterpret_cast<f32x4 *>(new_state + off));
-    __builtin_nontemporal_store(Sb[p], reinterpret_cast<f32x4 *>(new_state + off + 64));
+    const uint32_t off = static_cast<uint32_t>((row0 + 4 * p) * kDK + c4) * 4u;
+    buf_store16_nt(rd, off, Sa[p]);
+    buf_store16_nt(rd, off + 256u, Sb[p]);
   }
   // A packed batch: rows outside every sequence get zeros.
   if (cu != nullptr) zero_uncovered_rows(out, cu, cu64, N, T, H.v, blockIdx.x, gridDim.x);
