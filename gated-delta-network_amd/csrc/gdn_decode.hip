@@ -198,18 +198,19 @@ constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 constexpr int kNontemporalFlag = 16;
 
 // Built-in tiling per batch size, from the MI355X sweep of every tiling at
-// B = 1..512 (HIP-graph replay timing, 8 rotating states): small batches want
-// many small workgroups, B = 33..128 one wave streaming 64 rows (32 KiB in
+// B = 1..512 (HIP-graph replay timing in 20-step graphs, 8 rotating states;
+// the close calls confirmed by interleaved repeats): small batches want many
+// small workgroups, B = 17..128 one wave streaming 64 rows (32 KiB in
 // flight per wave), and beyond that -- many waves resident per CU for the
-// whole launch -- one wave of 8 rows (B = 512: 87.3 us against 93.1 us with
-// 64 rows and 90.4 us for a plain copy of the same bytes); non-temporal
-// state accesses win at every size.
+// whole launch -- 32-row workgroups of four waves (B = 256: 43.8 us against
+// 45.3 us with one-wave 8-row ones; B = 512: 85.1 against 87.7 us);
+// non-temporal state accesses win at every size.
 int default_variant(int batch) {
   if (batch <= 4) return 3 + kNontemporalFlag;    // 16 rows, 256 threads
-  if (batch <= 8) return 2 + kNontemporalFlag;    // 32 rows, 256 threads
-  if (batch <= 32) return 5 + kNontemporalFlag;   // 32 rows,  64 threads
+  if (batch <= 8) return 4 + kNontemporalFlag;    // 32 rows, 128 threads
+  if (batch <= 16) return 6 + kNontemporalFlag;   // 16 rows,  64 threads
   if (batch <= 128) return 9 + kNontemporalFlag;  // 64 rows,  64 threads
-  return 7 + kNontemporalFlag;                    //  8 rows,  64 threads
+  return 2 + kNontemporalFlag;                    // 32 rows, 256 threads
 }
 
 }  // namespace
