@@ -166,19 +166,23 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
   // The first block's inputs are requested before the state: the loads
   // return in order, so steps (1)-(4), which do not read the state, need not
   // wait for all 64 KB of it.
+  // No branch around these loads: the descriptors of an empty sequence, or
+  // of a call without a state, have range 0 and their loads return zeros.
+  // (With a branch, the compiler's load waits had to cover both paths, and
+  // wave 0's gating of block 0 waited for the whole state.)
   BlockIn cur;
-  if (len > 0) load_block(0, cur);
+  load_block(0, cur);
+  const auto rs = buf_rsrc(state != nullptr ? state + sbase : new_state + sbase,
+                           state != nullptr && len > 0 ? kDV * kDK * 4u : 0u);
+  // offset of S[col0 + 16 vi + r16][16 kt + q4]: per lane (r16, q4), per wave
+  // (col0, vi) and constant (kt)
+  const uint32_t lane_off = static_cast<uint32_t>(r16 * kDK + q4) * 4u;
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-    for (int vi = 0; vi < CV; ++vi) {
-      const int vc = col0 + 16 * vi + r16;
-      if (state != nullptr && len > 0)
-        St[kt][vi] = __builtin_nontemporal_load(
-            reinterpret_cast<const f32x4 *>(state + sbase + vc * kDK + 16 * kt + q4));
-      else
-        St[kt][vi] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int vi = 0; vi < CV; ++vi)
+      St[kt][vi] = buf_load16_nt(rs, lane_off + 64u * kt,
+                                 static_cast<uint32_t>((col0 + 16 * vi) * kDK) * 4u);
 
   if (len > 0 && wave == 0) gate_block(len < kBlk ? len : kBlk, cur.a, cur.b, 0);
   for (int t0 = 0; t0 < len; t0 += kBlk) {
@@ -424,16 +428,16 @@ void block_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k
 
   // Final state c St; all zeros for a zero-length sequence
   // (gdn_prefill_ref.py:61-62).
+  const auto rd = buf_rsrc(new_state + sbase, kDV * kDK * 4u);
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
     for (int vi = 0; vi < CV; ++vi) {
-      const int vc = col0 + 16 * vi + r16;
       f32x4 x = St[kt][vi];
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[r] *= c;
-      __builtin_nontemporal_store(
-          x, reinterpret_cast<f32x4 *>(new_state + sbase + vc * kDK + 16 * kt + q4));
+      buf_store16_nt(rd, lane_off + 64u * kt, static_cast<uint32_t>((col0 + 16 * vi) * kDK) * 4u,
+                     x);
     }
   // A packed batch: rows outside every sequence get zeros.
   if (cu != nullptr) zero_uncovered_rows(out, cu, cu64, N, T, H.v, blockIdx.x, gridDim.x);

@@ -292,6 +292,18 @@ __device__ __forceinline__ void buf_store16_nt(__amdgpu_buffer_rsrc_t r, uint32_
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, byte_off, 0,
                                          kCachePolicyNt);
 }
+// The same with a wave-uniform part of the offset in the instruction's
+// scalar offset (one VGPR of per-lane offset serves many loads).
+__device__ __forceinline__ f32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t lane_off,
+                                               uint32_t uniform_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, uniform_off,
+                                                                         kCachePolicyNt));
+}
+__device__ __forceinline__ void buf_store16_nt(__amdgpu_buffer_rsrc_t r, uint32_t lane_off,
+                                               uint32_t uniform_off, f32x4 x) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, lane_off, uniform_off,
+                                         kCachePolicyNt);
+}
 // One float at a wave-uniform address, as a vector load issued in program
 // order with the fragments it belongs to.
 __device__ __forceinline__ float buf_load_f32(const float *p) {

@@ -24,6 +24,9 @@ __global__ __launch_bounds__(64) void stream_copy_kernel(const f32x4 *__restrict
 #pragma unroll
   for (int i = 0; i < kCopyPerLane; ++i)
     r[i] = buf_load16_nt(rs, static_cast<uint32_t>(threadIdx.x + 64 * i) * 16u);
+  // every load before the first store (left alone, the compiler keeps only
+  // 14 loads in flight to save registers: 11.9 us instead of 10.7 us)
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < kCopyPerLane; ++i)
     buf_store16_nt(rd, static_cast<uint32_t>(threadIdx.x + 64 * i) * 16u, r[i]);

@@ -81,7 +81,9 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
   // a descriptor of the (sequence, head) state, as in the decode kernel (over
   // rotating state sets: B=64 T=2 decode 15.3 -> 12.5 us, 256x1 prefill 63.2
   // -> 58.5 us against plain accesses).  The loads do not wait for the
-  // sequence's length: a zero-length sequence's state is read and dropped.
+  // sequence's length: a zero-length sequence's state is read and dropped
+  // at the final store (zeroing it here would wait for the loads before the
+  // token loads go out).
   const size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;
   constexpr uint32_t kHeadBytes = kDV * kDK * 4;
   f32x4 Sa[PASSES], Sb[PASSES];  // columns c4.. and 64 + c4..
@@ -92,10 +94,6 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
       const uint32_t off = static_cast<uint32_t>((row0 + 4 * p) * kDK + c4) * 4u;
       Sa[p] = buf_load16_nt(rs, off);
       Sb[p] = buf_load16_nt(rs, off + 256u);
-    }
-    if (len == 0) {
-#pragma unroll
-      for (int p = 0; p < PASSES; ++p) Sa[p] = Sb[p] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   } else {
 #pragma unroll
@@ -212,11 +210,12 @@ __global__ __launch_bounds__(64 * WAVES) void recurrent_kernel(
 
   // Final state; all zeros for a zero-length sequence (gdn_prefill_ref.py:61-62).
   const auto rd = buf_rsrc(new_state + sbase, kHeadBytes);
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
     const uint32_t off = static_cast<uint32_t>((row0 + 4 * p) * kDK + c4) * 4u;
-    buf_store16_nt(rd, off, Sa[p]);
-    buf_store16_nt(rd, off + 256u, Sb[p]);
+    buf_store16_nt(rd, off, len > 0 ? Sa[p] : z);
+    buf_store16_nt(rd, off + 256u, len > 0 ? Sb[p] : z);
   }
   // A packed batch: rows outside every sequence get zeros.
   if (cu != nullptr) zero_uncovered_rows(out, cu, cu64, N, T, H.v, blockIdx.x, gridDim.x);
