@@ -281,7 +281,7 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t b
 }
 // Streaming 16-byte accesses through a descriptor, cache policy nt (bit 1 of
 // the instruction's cache-policy operand): for state read or written once
-// (decode at B=64: ~1 % faster than flat non-temporal accesses).
+// (decode loads at B=64: ~1 % faster than flat non-temporal loads).
 constexpr int kCachePolicyNt = 2;
 __device__ __forceinline__ f32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0,
@@ -298,11 +298,6 @@ __device__ __forceinline__ f32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_
                                                uint32_t uniform_off) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, uniform_off,
                                                                          kCachePolicyNt));
-}
-__device__ __forceinline__ void buf_store16_nt(__amdgpu_buffer_rsrc_t r, uint32_t lane_off,
-                                               uint32_t uniform_off, f32x4 x) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, lane_off, uniform_off,
-                                         kCachePolicyNt);
 }
 // One float at a wave-uniform address, as a vector load issued in program
 // order with the fragments it belongs to.
