@@ -38,8 +38,19 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(
 
   const int tile = blockIdx.x % kTiles;
   const int nh = blockIdx.x / kTiles;  // n * H.v + h
-  const int h = nh % H.v;
-  const int n = nh / H.v;
+  // The reference's head shape (8 v-heads over 4 q/k heads) by shifts: the
+  // divisions by run-time head counts put ~45 scalar instructions ahead of
+  // the first load (B=64: 11.30 -> 11.23 us per step in 20-step graphs).
+  int h, n, hq;
+  if (H.v == 8 && H.ratio == 2) {
+    h = nh & 7;
+    n = nh >> 3;
+    hq = h >> 1;
+  } else {
+    h = nh % H.v;
+    n = nh / H.v;
+    hq = h / H.ratio;
+  }
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15;
@@ -55,7 +66,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(
   const uint16_t a_raw = a[nh], b_raw = b[nh];
   const float alog = A_log[h], dtb = dt_bias[h];
   // This lane's 8 columns of q and k (q/k head h/2).
-  const int qk_off = (n * H.qk + h / H.ratio) * kDK;
+  const int qk_off = (n * H.qk + hq) * kDK;
   const u16x4 qa = *reinterpret_cast<const u16x4 *>(q + qk_off + 4 * c);
   const u16x4 qb = *reinterpret_cast<const u16x4 *>(q + qk_off + 64 + 4 * c);
   const u16x4 ka = *reinterpret_cast<const u16x4 *>(k + qk_off + 4 * c);
