@@ -129,6 +129,7 @@ PrefillLayout prefill_layout(int T, int N, const Heads &H) {
   L.send = take(one * hv * kDV * kDK * 4);
   L.cend = take(one * hv * kDV * kDK * 4);
   L.mend = take(one * hv * kDV * kDK * 4);
+  L.early = take(N == 1 ? static_cast<size_t>(early_words(split_first(static_cast<int>(nt)), H.v)) * 4 : 0);
   L.total = off;
   return L;
 }
@@ -267,7 +268,14 @@ int plan_prefill(int T, int N, const Heads &H, const PrefillLayout &L, int varia
   if (state_units > 0x7fffffffLL) return fail(GDN_ERR_INVALID, "%s: too many sequences", what);
   P.state_grid = cap(state_units, kStatePerCu);
   P.split_grid = split ? static_cast<long long>(L.nt_max - P.split_nt0) * H.v : 0;
-  P.out_grid = L.nt_max > 0 ? chunk_head_grid(split ? P.split_nt0 : L.nt_max, H) +
+  P.early_grid = split && H.v == 8 && state_units + kEarlyGrid <= kNumCus &&
+                         P.split_nt0 >= 2 * kEarlyTail
+                     ? kEarlyGrid
+                     : 0;
+  // with the early output, kEarlyTail workgroups per head cover the first
+  // segment (its last chunks, and any the early workgroups left)
+  P.out_grid = L.nt_max > 0 ? (P.early_grid > 0 ? static_cast<long long>(kEarlyTail) * H.v
+                                                 : chunk_head_grid(split ? P.split_nt0 : L.nt_max, H)) +
                                   (split ? kStateTiles * H.v : 0)
                             : 0;
   return GDN_OK;

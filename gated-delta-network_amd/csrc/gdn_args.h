@@ -70,7 +70,10 @@ struct PrefillLayout {
   // Two-segment scan of one sequence (N == 1 only, else empty): the map's
   // linear part per chunk of the second segment, the first segment's final
   // state and the second segment's map (offset, linear part).
-  size_t htm, send, cend, mend, total;
+  size_t htm, send, cend, mend;
+  // Early output of the two-segment scan (N == 1): a progress word per first-
+  // segment state unit, then a done flag per (chunk, v-head) of the segment.
+  size_t early, total;
 };
 
 // Upper bound on the chunks of N sequences totalling T tokens: each sequence
@@ -145,6 +148,9 @@ struct PrefillPlan {
   // launch grids (workgroups, capped at the resident ones; the kernels loop
   // over the remaining units); 0 = not launched
   long long intra_grid, state_grid, split_grid, out_grid;
+  // workgroups added to the state launch for the first segment's early output
+  // (two-segment scan with 8 v-heads); 0 none
+  long long early_grid;
 };
 
 // rec_max >= 0 (explicit): sequential iff the longest sequence has at most

@@ -123,4 +123,22 @@ constexpr int kNumRecTilings = 10;
 // new_state tiles of a two-segment scan, per v-head (16 rows x 32 columns).
 constexpr int kStateTiles = (kDV / 16) * (kDK / 32);
 
+// Early output of a two-segment scan (8 v-heads: each head's 24 state
+// workgroups on one XCD, 192 of the 256 CUs).  The state launch adds
+// kEarlyGrid workgroups, kEarlyGrid / 8 per head on the head's XCD, that
+// compute the first segment's output while its chain runs: chunk c as soon as
+// the head's 8 first-segment units have stored its ht and v_new (they publish
+// a progress word per unit, read through the XCD's L2).  The last kEarlyTail
+// chunks of the segment, finished too close to the chain's end, are left to
+// the output launch (kEarlyTail workgroups per head instead of one per
+// chunk), which also computes any chunk not marked done.  Built in from
+// 2 kEarlyTail first-segment chunks on (1x8192, graph replay: the state
+// launch 53.1 -> 55.3 us, the output launch 29.4 -> 23.2 us; a tail of 7
+// chunks left the early workgroups a backlog past the chain's end).
+constexpr int kEarlyGrid = 64;
+constexpr int kEarlyTail = 15;
+__host__ __device__ inline long long early_words(int nt0, int hv) {
+  return (static_cast<long long>(nt0) + kDV / 16) * hv;
+}
+
 }  // namespace gdn

@@ -162,6 +162,20 @@ __device__ __forceinline__ void one_seq_bounds(const OneSeq &o, int &bos, int &e
   eos = eos < bos ? bos : eos;
 }
 
+// The XCD (accelerator complex die) the wave runs on: hardware register
+// XCC_ID of gfx940 and later.  MI355X deals the workgroups of a launch
+// round-robin over its 8 XCDs (workgroups i and i + 8 on one XCD; which XCD
+// takes workgroup 0 varies from launch to launch), each with its own L2;
+// stores of one XCD are seen by the other CUs of that XCD through its L2
+// before any write-back.
+__device__ __forceinline__ int xcc_id() {
+  int x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x & 0xf;
+}
+// The XCD as the top byte of a progress word (never 0).
+__device__ __forceinline__ int early_tag() { return (xcc_id() + 1) << 24; }
+
 }  // namespace gdn
 
 namespace gdn {

@@ -70,6 +70,9 @@ namespace gdn {
 // LDS row strides (elements), padded by 16 bytes against bank conflicts.
 constexpr int kStrideK = 136;  // bf16 [64][128] tiles
 constexpr int kStrideT = 72;   // bf16 [*][64]   tiles
+// LDS of one chunk's output (Q, P, G): the output kernel's, and the state
+// kernel's early-output workgroups'
+constexpr int kOutputLds = kChunk * kStrideK * 2 + kChunk * kStrideT * 2 + kChunk * 4;
 
 constexpr int kTElems = kChunk * kChunk * 2;  // T of one (chunk, head): hi + lo bf16
 
@@ -262,6 +265,8 @@ struct SelfIndex {
   int4 *chunks;
   int *offsets;
   int *status;     // per-sequence contract bits (also for one sequence)
+  int *early;      // one sequence: words of the two-segment scan's early output,
+  int n_early;     // zeroed by the first workgroups (nullptr: none)
 };
 constexpr int kSelfIndexLds = 3 * kSelfIndexMax * 4 + 16 * 4;
 
@@ -1027,6 +1032,13 @@ __device__ __forceinline__ void intra_body(
     // one sequence: its contract bits (several: the index kernel's)
     if (one.cu != nullptr && id == 0 && threadIdx.x == 0)
       si.status[0] = cu_status_bits(raw_cu(one.cu, one.cu64, 0), raw_cu(one.cu, one.cu64, 1), one.T);
+    // the early-output words start each call at zero (the state launch
+    // after this one counts up from them): 256 per workgroup (the grid has
+    // more than enough); only the WY form runs one sequence
+    if constexpr (FORM == 0) {
+      const int i = id * 256 + static_cast<int>(threadIdx.x);
+      if (si.early != nullptr && i < si.n_early) si.early[i] = 0;
+    }
     if (!unit) return;
     if (FORM < 0) form = *form_flag;
     if (one.cu != nullptr) {
@@ -1144,13 +1156,15 @@ __device__ __forceinline__ void load_wy_part(WyFrag &f, int c, int h, const Head
 // rows v0..v0+15 of the identity as the start, u = 0 (no u loads), no v_new
 // stores; ht then receives M over the chunks before c (rows j = v0..v0+15 of
 // [j][k]) at chunk index c - ht_c0.
+// PROG: publish the unit's progress in *prog for the early output (every
+// thread stores the same word: no divergent branch splits the loop body).
 constexpr int kStateWyLds = 2 * 16 * kStrideK * 2 + 3 * 16 * kStrideT * 2;
-template <bool MAP>
+template <bool MAP, bool PROG>
 __device__ __forceinline__ void wy_state(
     char *smem, int c0, int nch, int npre, int h, int v0, int wave, int lane, size_t sbase,
     const float *state, float *new_state, const float *ws_dcy, const float *ws_eg,
     const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt, uint16_t *ws_ht,
-    uint16_t *ws_vnt, const Heads &H, int ht_c0) {
+    uint16_t *ws_vnt, const Heads &H, int ht_c0, int *prog, int prog_tag) {
   const int ct = 0;  // one 16-column tile per workgroup
   const int r16 = lane & 15, kg = (lane >> 4) * 8, q4 = 4 * (lane >> 4);
   const int lc = 16 * ct;
@@ -1258,6 +1272,14 @@ __device__ __forceinline__ void wy_state(
     }
     GDN_PART(4, g, cn);
     __syncthreads();
+    // Progress for the early output: each wave has used u of chunk c, loaded
+    // in step c - 2 after its ht and v_new stores of chunk c - 2; vector
+    // memory operations complete in order, so those stores have reached L2,
+    // and chunks c0 .. c - 2 are out.  The word carries the unit's XCD
+    // (prog_tag) above the chunk count.
+    if constexpr (PROG)
+      __hip_atomic_store(prog, prog_tag | (c - c0 >= 2 ? c - c0 - 1 : 0), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_WORKGROUP);
     // v_new: the workgroup's 16 rows of [v][token] bf16 (2 KB contiguous) from
     // the LDS copy, one 8-byte store per thread
     if constexpr (!MAP) {
@@ -1680,6 +1702,9 @@ struct SplitScan {
   int nt0;        // first chunk of the second segment; 0 = one chain
   uint16_t *htm;  // [nt - nt0][H.v][128 j][128 k] bf16
   float *send, *cend, *mend;  // [H.v][128][128] f32 each
+  // early output of the first segment (8 v-heads; nullptr: none): [H.v][8]
+  // progress words of the first segment's units, then [nt0][H.v] done flags
+  int *early;
 };
 
 // One unit of the state kernel: sequence s, v-head h, V-block vb (unit =
@@ -1700,6 +1725,7 @@ __device__ __forceinline__ void state_unit(
   // This unit's chunks: c0 .. c0 + nch - 1 (prefetches clamped to npre
   // chunks, known at launch for one sequence); the tokens [bos, eos).
   int c0 = 0, nch = 0, npre = 0, bos = 0, eos = 0;
+  int *prog = nullptr, prog_tag = 0;
   size_t sbase = (static_cast<size_t>(s) * H.v + h) * kDV * kDK;  // [V][K]
   if (one.cu != nullptr) {
     one_seq_bounds(one, bos, eos);
@@ -1718,14 +1744,19 @@ __device__ __forceinline__ void state_unit(
   if (sp.nt0 > 0) {  // two-segment scan of one sequence (WY form)
     sbase = static_cast<size_t>(h) * kDV * kDK;
     if (s == 2) {
-      wy_state<true>(smem, sp.nt0, nch - sp.nt0, nt_max - sp.nt0, h, vb * 16, wave, lane, sbase,
-                     nullptr, sp.mend, ws_dcy, ws_eg, ws_w, ws_u, ws_kt, sp.htm, ws_vnt, H, sp.nt0);
+      wy_state<true, false>(smem, sp.nt0, nch - sp.nt0, nt_max - sp.nt0, h, vb * 16, wave, lane, sbase,
+                     nullptr, sp.mend, ws_dcy, ws_eg, ws_w, ws_u, ws_kt, sp.htm, ws_vnt, H, sp.nt0,
+                     nullptr, 0);
       return;
     }
     if (s == 0) {
       nch = nch < sp.nt0 ? nch : sp.nt0;
       npre = sp.nt0;
       new_state = sp.send;
+      if (sp.early != nullptr) {
+        prog = sp.early + h * NVB + vb;
+        prog_tag = early_tag();
+      }
     } else {
       c0 = sp.nt0;
       nch -= sp.nt0;
@@ -1738,20 +1769,34 @@ __device__ __forceinline__ void state_unit(
     // the T form reads K and V itself: the sequence's tokens [bos, eos)
     t_state(smem, c0, nch, bos, eos, h, vb * 16, wave, lane, sbase, k, v, state, new_state, ws_dcy,
             ws_eg, ws_w, ws_u, ws_ht, ws_vnt, H);
+  } else if (prog != nullptr) {
+    wy_state<false, true>(smem, c0, nch, npre, h, vb * 16, wave, lane, sbase, state, new_state,
+                          ws_dcy, ws_eg, ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0, prog, prog_tag);
   } else {
-    wy_state<false>(smem, c0, nch, npre, h, vb * 16, wave, lane, sbase, state, new_state, ws_dcy,
-                    ws_eg, ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0);
+    wy_state<false, false>(smem, c0, nch, npre, h, vb * 16, wave, lane, sbase, state, new_state,
+                           ws_dcy, ws_eg, ws_w, ws_u, ws_kt, ws_ht, ws_vnt, H, 0, nullptr, 0);
   }
 }
 
+__device__ __forceinline__ void early_output(char *smem, int e, int ne, const uint16_t *q,
+                                             const uint16_t *k, const OneSeq &one, const Heads &H,
+                                             const float *ws_G, const uint16_t *ws_ht,
+                                             const uint16_t *ws_vnt, float scale, uint16_t *out,
+                                             const SplitScan &sp);
+constexpr int kStateLds0 = kStateWyLds > kStateTLds ? kStateWyLds : kStateTLds;
+constexpr int kStateLds = kStateLds0 > kOutputLds + 16 ? kStateLds0 : kOutputLds + 16;
+
+// The state launch of a two-segment scan with early output has kEarlyGrid
+// more workgroups than units, after them (early_output).
 template <bool LOOP>
 __global__ __launch_bounds__(256) void prefill_state_kernel(
     const uint16_t *k, const uint16_t *v, const float *state, float *new_state,
     const int4 *chunks, const int *offsets, const float *ws_dcy, const float *ws_eg,
     const uint16_t *ws_w, const float *ws_u, const uint16_t *ws_kt, uint16_t *ws_ht,
     uint16_t *ws_vnt, int N, int nt_max, OneSeq one, Heads H, int form, SplitScan sp,
-    const void *cu, int cu64, int T, uint16_t *out) {
-  __shared__ __align__(16) char smem[kStateWyLds > kStateTLds ? kStateWyLds : kStateTLds];
+    const void *cu, int cu64, int T, uint16_t *out, const uint16_t *q, const float *ws_G,
+    float scale) {
+  __shared__ __align__(16) char smem[kStateLds];
   // (the bounds of the rows this batch covers are loaded now, used at the end)
   const CoveredRows rows = covered_rows(cu, cu64, N, T);
   if (one.cu == nullptr) {
@@ -1760,8 +1805,12 @@ __global__ __launch_bounds__(256) void prefill_state_kernel(
   }
   const int units = (sp.nt0 > 0 ? 3 : N) * H.v * (kDV / 16);
   if (!LOOP) {
-    state_unit(smem, blockIdx.x, k, v, state, new_state, chunks, offsets, ws_dcy, ws_eg, ws_w,
-               ws_u, ws_kt, ws_ht, ws_vnt, nt_max, one, H, form, sp);
+    if (static_cast<int>(blockIdx.x) < units)
+      state_unit(smem, blockIdx.x, k, v, state, new_state, chunks, offsets, ws_dcy, ws_eg, ws_w,
+                 ws_u, ws_kt, ws_ht, ws_vnt, nt_max, one, H, form, sp);
+    else if (sp.early != nullptr)
+      early_output(smem, blockIdx.x - units, gridDim.x - units, q, k, one, H, ws_G, ws_ht, ws_vnt,
+                   scale, out, sp);
   } else {
     for (int unit = blockIdx.x; unit < units; unit += gridDim.x) {
       state_unit(smem, unit, k, v, state, new_state, chunks, offsets, ws_dcy, ws_eg, ws_w, ws_u,
@@ -2072,25 +2121,14 @@ __device__ __forceinline__ void split_state_tile(char *smem, int f, const Heads 
 //   P  = mask_{j<=i} exp(G_i - G_j) Q K^T      (waves split the rows)
 //   O  = exp(G_i) Q S_c + P v_new              (waves split the columns)
 // ---------------------------------------------------------------------------
-constexpr int kOutputLds = kChunk * kStrideK * 2 + kChunk * kStrideT * 2 + kChunk * 4;
-__device__ __forceinline__ void output_unit(
-    char *osmem, int id, const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
-    const int4 *__restrict__ chunks, const OneSeq &one, int nt_max, const Heads &H,
+__device__ __forceinline__ void output_chunk(
+    char *osmem, int c, int h, const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
+    const int4 *__restrict__ chunks, const OneSeq &one, const Heads &H,
     const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
-    uint16_t *__restrict__ out, const SplitScan &sp, float *__restrict__ new_state) {
+    uint16_t *__restrict__ out) {
   uint16_t *const sQ = reinterpret_cast<uint16_t *>(osmem);  // [64][kStrideK]
   uint16_t *const sP = sQ + kChunk * kStrideK;                // [64][kStrideT]
   float *const sG = reinterpret_cast<float *>(sP + kChunk * kStrideT);
-  static_assert(16 * kDK * 4 + kDK * 32 * 4 <= kOutputLds, "new_state tile must fit");
-  // After a two-segment scan the first kStateTiles H.v workgroups compute
-  // new_state.
-  const int nfix = sp.nt0 > 0 ? kStateTiles * H.v : 0;
-  if (id < nfix) {
-    split_state_tile(osmem, id, H, sp, new_state);
-    return;
-  }
-  int c, h;
-  if (!chunk_head_of(id - nfix, nt_max, H, c, h)) return;
   const int4 ch = chunk_info(chunks, c, one);
   if (ch.x < 0) return;
   const int start = ch.y, len = ch.z;
@@ -2217,6 +2255,136 @@ __device__ __forceinline__ void output_unit(
   }
 }
 
+// One workgroup of an output launch: a new_state tile of a two-segment scan
+// (the first kStateTiles H.v ids), else (chunk, v-head) = chunk_head_of(id).
+__device__ __forceinline__ void output_unit(
+    char *osmem, int id, const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
+    const int4 *__restrict__ chunks, const OneSeq &one, int nt_max, const Heads &H,
+    const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
+    uint16_t *__restrict__ out, const SplitScan &sp, float *__restrict__ new_state) {
+  static_assert(16 * kDK * 4 + kDK * 32 * 4 <= kOutputLds, "new_state tile must fit");
+  const int nfix = sp.nt0 > 0 ? kStateTiles * H.v : 0;
+  if (id < nfix) {
+    split_state_tile(osmem, id, H, sp, new_state);
+    return;
+  }
+  int c, h;
+  if (!chunk_head_of(id - nfix, nt_max, H, c, h)) return;
+  output_chunk(osmem, c, h, q, k, chunks, one, H, ws_G, ws_ht, ws_vnt, scale, out);
+}
+
+// Early output of a two-segment scan (SplitScan::early): workgroup e of the
+// ne added to the state launch computes, for v-head h = e % 8, the output of
+// the first segment's chunks c = e / 8, e / 8 + ne / 8, ... below the
+// segment's last kEarlyTail chunks, each as soon as the head's 8 first-
+// segment units have published it, and marks the chunk done for the output
+// launch.  Workgroups are dealt round-robin over the 8 XCDs, so the head's
+// state units (blockIdx.x = h + 8 (vb + 8 s)) and its early workgroups
+// (blockIdx.x = 192 + e, e = h mod 8) share an XCD and its L2.  A progress
+// word holds the publishing unit's XCD (early_tag) above its chunk count, and
+// is read past L1 (an agent-scope load): a word of the reader's XCD comes
+// from the shared L2, where the unit's ht and v_new stores already are; a
+// word of another XCD, which could only arrive through a write-back ahead of
+// its data, stops the workgroup.  So does a wait of kEarlyPatience ticks of
+// the 100 MHz wall clock without progress.  The output launch computes every
+// chunk not marked done.
+constexpr long long kEarlyPatience = 5000;  // 50 us
+__device__ __forceinline__ void early_output(char *smem, int e, int ne, const uint16_t *q,
+                                             const uint16_t *k, const OneSeq &one, const Heads &H,
+                                             const float *ws_G, const uint16_t *ws_ht,
+                                             const uint16_t *ws_vnt, float scale, uint16_t *out,
+                                             const SplitScan &sp) {
+  constexpr int NVB = kDV / 16;
+  constexpr int kCount = (1 << 24) - 1;
+  const int h = e % H.v, step = ne / H.v, me = early_tag();
+  int bos, eos;
+  one_seq_bounds(one, bos, eos);
+  const int nch = (eos - bos + kChunk - 1) / kChunk;
+  const int n1 = nch < sp.nt0 ? nch : sp.nt0;
+  const int *const prog = sp.early + h * NVB;
+  int *const done = sp.early + H.v * NVB;
+  int *const s_go = reinterpret_cast<int *>(smem + kOutputLds);
+  const int lane = threadIdx.x & 63;
+  int seen = 0;  // the head's least published count so far, and when it last grew
+  long long t_seen = wall_clock64();
+  for (int c = e / H.v; c < n1 - kEarlyTail; c += step) {
+    if (threadIdx.x < 64) {
+      int go = 1;
+      for (;;) {
+        const int w = lane < NVB ? __hip_atomic_load(prog + lane, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT)
+                                 : me | kCount;
+        if (__ballot(w != 0 && (w & ~kCount) != me) != 0) {
+          go = 0;  // published from another XCD
+          break;
+        }
+        int m = w & kCount;  // 0 while unpublished
+        m = min(m, __shfl_xor(m, 4));
+        m = min(m, __shfl_xor(m, 2));
+        m = min(m, __shfl_xor(m, 1));
+        m = __shfl(m, 0);
+        if (m > c) break;
+        const long long t = wall_clock64();
+        if (m > seen) {
+          seen = m;
+          t_seen = t;
+        } else if (t - t_seen > kEarlyPatience) {
+          go = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (threadIdx.x == 0) *s_go = go;
+    }
+    __syncthreads();
+    if (*s_go == 0) return;
+    output_chunk(smem, c, h, q, k, nullptr, one, H, ws_G, ws_ht, ws_vnt, scale, out);
+    __syncthreads();  // the chunk's LDS reads are done before the next one's writes
+    if (threadIdx.x == 0) done[c * H.v + h] = 1;
+  }
+}
+
+// The first segment's chunks that the early output leaves to the output
+// launch (SplitScan::early): workgroup (j, h) = (r / 8, r % 8) computes chunk
+// n1 - kEarlyTail + j of v-head h (n1: the segment's chunks of this
+// sequence), then every chunk c = j + kEarlyTail i below n1 - kEarlyTail
+// whose done flag the state launch did not set (none, unless an early
+// workgroup stopped).
+__device__ __forceinline__ void early_rest(char *smem, int r, const uint16_t *q, const uint16_t *k,
+                                           const OneSeq &one, const Heads &H, const float *ws_G,
+                                           const uint16_t *ws_ht, const uint16_t *ws_vnt,
+                                           float scale, uint16_t *out, const SplitScan &sp) {
+  const int h = r % H.v, j = r / H.v;
+  int bos, eos;
+  one_seq_bounds(one, bos, eos);
+  const int nch = (eos - bos + kChunk - 1) / kChunk;
+  const int n1 = nch < sp.nt0 ? nch : sp.nt0, first = n1 - kEarlyTail;
+  const int *const done = sp.early + H.v * (kDV / 16);
+  unsigned *const s_todo = reinterpret_cast<unsigned *>(smem + kOutputLds);
+  if (first + j >= 0)
+    output_chunk(smem, first + j, h, q, k, nullptr, one, H, ws_G, ws_ht, ws_vnt, scale, out);
+  for (int cb = j; cb < first; cb += 64 * kEarlyTail) {
+    __syncthreads();  // the LDS of the chunk before is free
+    if (threadIdx.x < 64) {
+      const int c = cb + kEarlyTail * static_cast<int>(threadIdx.x);
+      const unsigned long long m = __ballot(c < first && done[c * H.v + h] == 0);
+      if (threadIdx.x == 0) {
+        s_todo[0] = static_cast<unsigned>(m);
+        s_todo[1] = static_cast<unsigned>(m >> 32);
+      }
+    }
+    __syncthreads();
+    unsigned long long m = (static_cast<unsigned long long>(s_todo[1]) << 32) | s_todo[0];
+    while (m != 0) {
+      const int i = __builtin_ctzll(m);
+      m &= m - 1;
+      __syncthreads();
+      output_chunk(smem, cb + kEarlyTail * i, h, q, k, nullptr, one, H, ws_G, ws_ht, ws_vnt, scale,
+                   out);
+    }
+  }
+}
+
 // 27 KB of LDS and at most 128 VGPRs: four workgroups per CU.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 void prefill_output_kernel(
@@ -2242,8 +2410,11 @@ void prefill_output_split_kernel(
     uint16_t *__restrict__ out, SplitScan sp, float *__restrict__ new_state, int out_units) {
   static_assert(kOutputLds <= kSplitOutLds, "the output unit fits the split unit's LDS");
   __shared__ __align__(16) uint16_t smem[kSplitOutLds / 2];
-  const int id = blockIdx.x;
-  if (id < out_units)
+  const int id = blockIdx.x, nfix = kStateTiles * H.v;
+  if (sp.early != nullptr && id >= nfix && id < out_units)
+    early_rest(reinterpret_cast<char *>(smem), id - nfix, q, k, one, H, ws_G, ws_ht, ws_vnt, scale,
+               out, sp);
+  else if (id < out_units)
     output_unit(reinterpret_cast<char *>(smem), id, q, k, nullptr, one, out_chunks, H, ws_G, ws_ht,
                 ws_vnt, scale, out, sp, new_state);
   else
@@ -2329,10 +2500,13 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
   if (P.choose != 0 && !P.self_index) {
     if ((rc = sequential_kernel())) return rc;
   }
+  // two-segment scan with early output: its words, zeroed by the intra launch
+  int *early = P.early_grid > 0 ? reinterpret_cast<int *>(ws + L.early) : nullptr;
   if (P.intra_grid > 0) {
     const int *flag = offsets + N + 2;  // read only when the device picks the form
     const SelfIndex si{P.self_index ? cu_seqlens : nullptr, cu64, N, T, P.choose, rec_max, P.form,
-                       chunks, offsets, status};
+                       chunks, offsets, status, early,
+                       static_cast<int>(early_words(P.split_nt0, H.v))};
     auto intra = P.intra_split ? prefill_intra_kernel<0, true>
                  : P.form == 0 ? prefill_intra_kernel<0, false>
                  : P.form == 1 ? prefill_intra_kernel<1, false>
@@ -2350,17 +2524,19 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
                        status);
     if ((rc = check_launch(what))) return rc;
   }
-  SplitScan sp{P.split_nt0, nullptr, nullptr, nullptr, nullptr};
+  SplitScan sp{P.split_nt0, nullptr, nullptr, nullptr, nullptr, nullptr};
   if (sp.nt0 > 0) {
     sp.htm = reinterpret_cast<uint16_t *>(ws + L.htm);
     sp.send = reinterpret_cast<float *>(ws + L.send);
     sp.cend = reinterpret_cast<float *>(ws + L.cend);
     sp.mend = reinterpret_cast<float *>(ws + L.mend);
+    sp.early = early;
   }
   hipLaunchKernelGGL(P.loop ? prefill_state_kernel<true> : prefill_state_kernel<false>,
-                     dim3(static_cast<unsigned>(P.state_grid)), dim3(256), 0,
+                     dim3(static_cast<unsigned>(P.state_grid + P.early_grid)), dim3(256), 0,
                      stream, k, v, state, new_state, chunks, offsets, wsD, wsE, wsw, wsu, kt, ht,
-                     vnt, N, L.nt_max, one, H, P.form, sp, cu_seqlens, cu64, T, output);
+                     vnt, N, L.nt_max, one, H, P.form, sp, cu_seqlens, cu64, T, output, q, wsG,
+                     scale);
   if ((rc = check_launch(what))) return rc;
   if (P.split_grid > 0) {
     // the first segment's output and new_state (the output kernel's units),

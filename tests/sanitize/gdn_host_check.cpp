@@ -30,9 +30,10 @@ static T *ptr(unsigned long long x) {
 static void print_status(int rc) { printf("%d\t%s\n", rc, last_error_text()); }
 
 static void print_plan(int rc, const PrefillPlan &P) {
-  printf("%d %d %d %d %d %d %d %lld %lld %lld %lld %d %d %d\n", rc, P.sequential ? 1 : 0,
+  printf("%d %d %d %d %d %d %d %lld %lld %lld %lld %d %d %d %lld\n", rc, P.sequential ? 1 : 0,
          P.seq_variant, P.choose, P.single ? 1 : 0, P.form, P.split_nt0, P.intra_grid, P.state_grid,
-         P.split_grid, P.out_grid, P.intra_split ? 1 : 0, P.loop ? 1 : 0, P.self_index ? 1 : 0);
+         P.split_grid, P.out_grid, P.intra_split ? 1 : 0, P.loop ? 1 : 0, P.self_index ? 1 : 0,
+         P.early_grid);
 }
 
 int main() {

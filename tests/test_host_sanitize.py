@@ -171,15 +171,22 @@ def test_plan_sweep(driver):
         f = [int(x) for x in got.split()]
         plans[c] = dict(rc=f[0], sequential=f[1], seq_variant=f[2], choose=f[3], single=f[4],
                         form=f[5], nt0=f[6], intra=f[7], state=f[8], split=f[9], out=f[10],
-                        intra_split=f[11], loop=f[12], self_index=f[13])
+                        intra_split=f[11], loop=f[12], self_index=f[13], early=f[14])
     base = (-1, -1, -1)
     p = plans[(96, 1, 4, 8) + base]
     assert p["sequential"] == 1
     p = plans[(8192, 1, 4, 8) + base]
     assert (p["single"], p["form"], p["nt0"], p["state"], p["split"]) == (1, 0, 64, 192, 512)
-    assert p["out"] == 64 * 4 // 8 * 8 * 2 + 32 * 8  # chunk-head pairs + new_state tiles
+    # the first segment's early output: 64 workgroups more in the state
+    # launch; the output launch covers the first segment with 15 per head
+    assert p["early"] == 64
+    assert p["out"] == 15 * 8 + 32 * 8  # first segment's rest + new_state tiles
     assert p["intra_split"] == 0  # 1024 chunk-head pairs fill the CUs
-    assert plans[(1000, 1, 4, 8) + base]["intra_split"] == 1  # 128 pairs: two halves each
+    p = plans[(1000, 1, 4, 8) + base]
+    assert p["intra_split"] == 1  # 128 pairs: two halves each
+    assert p["nt0"] == 8 and p["early"] == 0  # too few first-segment chunks for early output
+    assert p["out"] == 8 * 4 // 8 * 8 * 2 + 32 * 8  # chunk-head pairs + new_state tiles
+    assert plans[(8192, 1, 16, 32, -1, -1, -1)]["early"] == 0  # no two-segment scan at 32 v-heads
     p = plans[(8192, 1, 4, 8, 2, -1, -1)]
     assert p["nt0"] == 0 and p["state"] == 64
     p = plans[(32768, 2, 4, 8) + base]
@@ -197,6 +204,11 @@ def test_plan_sweep(driver):
             # resident workgroups (2 per CU of 256)
             assert p["state"] % 8 == 0 and p["intra"] % 8 == 0 and p["out"] % 8 == 0, c
             assert p["loop"] == (p["choose"] != 0), c
+            # early output only with the two-segment scan of 8 v-heads, from
+            # 30 first-segment chunks on, its grid within the 256 CUs
+            assert p["early"] in (0, 64), c
+            if p["early"]:
+                assert c[3] == 8 and p["nt0"] >= 30 and p["state"] + p["early"] <= 256, c
             if p["loop"]:
                 assert p["state"] <= 512, c
             # batches of 2..256 sequences and at most 2560 intra workgroups

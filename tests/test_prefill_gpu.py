@@ -444,6 +444,10 @@ def _layout(T, N):
     take("send", one * 8 * 128 * 128 * 4)
     take("cend", one * 8 * 128 * 128 * 4)
     take("mend", one * 8 * 128 * 128 * 4)
+    # early output of the two-segment scan: a progress word per first-segment
+    # unit (8 v-heads x 8 column blocks), then a done flag per (chunk, v-head)
+    # of the first segment
+    take("early", one * ((nt + 1) // 2 + 8) * 8 * 4)
     L["total"] = off
     return L
 
@@ -644,6 +648,42 @@ def test_prefill_two_segment_heads(cuda_device, heads):
                        recurrent_max_len=-2)
         torch.cuda.synchronize()
         check(out.float().cpu().numpy(), ns.cpu().numpy(), o_ref, s_ref)
+
+
+EARLY_TAIL = 15  # kEarlyTail (gdn_common.h); built in from 2 * EARLY_TAIL first-segment chunks
+
+
+@pytest.mark.parametrize("T, cu", [(8192, [0, 8192]), (8192, [0, 3000]), (4000, [130, 3980])])
+def test_prefill_early_output_words(cuda_device, T, cu):
+    # Two-segment scan with early output (8 v-heads): while the first
+    # segment's chain runs, workgroups added to the state launch compute its
+    # output for the chunks below n1 - 15 (n1: the segment's chunks of this
+    # sequence) as the chain publishes them, and mark them done; the output
+    # launch computes the rest.  After the call every first-segment unit's
+    # progress word holds n1 - 2 (published at the segment's last step) below
+    # its XCD tag (XCD + 1 in the top byte, one XCD per head: MI355X deals
+    # workgroups round-robin over its 8 XCDs), and the done flags are set
+    # exactly below n1 - 15: no early workgroup stopped.  The output matches
+    # the oracle.
+    from gdn_amd import prefill
+    print(f"prefill early output words T={T} cu={cu}", flush=True)
+    inp = O.make_prefill_inputs([T], seed=45, with_state=True)
+    inp["cu_seqlens"] = np.asarray(cu, dtype=np.int64)
+    o_ref, s_ref = O.prefill_seq_c(**inp)
+    lay = _layout(T, 1)
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, variant=SPLIT, route="chunked")
+    check(o, s, o_ref, s_ref)
+    ws = prefill._workspace(cuda_device, _stream(cuda_device), 0).cpu().numpy()
+    nt0 = (lay["nt"] + 1) // 2
+    n1 = min(-(-(cu[1] - cu[0]) // 64), nt0)
+    words = np.frombuffer(ws[lay["early"]:lay["early"] + (nt0 + 8) * 8 * 4].tobytes(), np.int32)
+    prog, done = words[:64].reshape(8, 8), words[64:].reshape(nt0, 8)
+    assert ((prog & 0xffffff) == n1 - 2).all(), prog
+    tag = prog >> 24
+    assert ((tag >= 1) & (tag <= 8)).all() and (tag == tag[:, :1]).all(), tag
+    assert len(np.unique(tag[:, 0])) == 8, tag
+    expect = (np.arange(nt0) < n1 - EARLY_TAIL)[:, None]
+    assert np.array_equal(done, np.broadcast_to(expect, done.shape).astype(np.int32)), done[:, 0]
 
 
 def test_prefill_two_segment_stage_intermediates(cuda_device):
