@@ -156,9 +156,9 @@ int check_prefill_args(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v, 
   if (!aligned(output, 16)) return fail(GDN_ERR_INVALID, "%s: output must be 16-byte aligned", what);
   if (!aligned(a, 2) || !aligned(b, 2)) return fail(GDN_ERR_INVALID, "%s: a/b must be 2-byte aligned", what);
   if (!aligned(cu_seqlens, cu64 ? 8 : 4)) return fail(GDN_ERR_INVALID, "%s: cu_seqlens misaligned", what);
-  if (variant < -1 || variant > 3)
+  if (variant < -1 || variant > 4)
     return fail(GDN_ERR_INVALID, "%s: unknown variant %d (0 WY form, 1 T form, 2 WY one chain, 3 WY "
-                "two segments)", what, variant);
+                "two segments, 4 as 3 with the early output cut short)", what, variant);
   if (rec_max < -2) return fail(GDN_ERR_INVALID, "%s: recurrent_max_len %d < -2", what, rec_max);
   if (rec_variant < -1 || rec_variant >= num_rec_variants)
     return fail(GDN_ERR_INVALID, "%s: unknown recurrent tiling %d", what, rec_variant);
@@ -261,7 +261,7 @@ int plan_prefill(int T, int N, const Heads &H, const PrefillLayout &L, int varia
   };
 
   if (P.single && P.form == 0 && variant != 2 && L.nt_max >= 2 && 24 * H.v <= 256 &&
-      (variant == 3 || L.nt_max >= kSplitMinChunks))
+      (variant >= 3 || L.nt_max >= kSplitMinChunks))
     P.split_nt0 = split_first(L.nt_max);
   const bool split = P.split_nt0 > 0;
   const long long state_units = static_cast<long long>(split ? 3 : N) * H.v * (kDV / 16);
@@ -272,6 +272,7 @@ int plan_prefill(int T, int N, const Heads &H, const PrefillLayout &L, int varia
                          P.split_nt0 >= 2 * kEarlyTail
                      ? kEarlyGrid
                      : 0;
+  P.early_limit = variant == 4 ? 1 : 0;
   // with the early output, kEarlyTail workgroups per head cover the first
   // segment (its last chunks, and any the early workgroups left)
   P.out_grid = L.nt_max > 0 ? (P.early_grid > 0 ? static_cast<long long>(kEarlyTail) * H.v

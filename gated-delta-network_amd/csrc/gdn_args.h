@@ -151,6 +151,10 @@ struct PrefillPlan {
   // workgroups added to the state launch for the first segment's early output
   // (two-segment scan with 8 v-heads); 0 none
   long long early_grid;
+  // chunks each early workgroup computes before it stops (0: no limit;
+  // variant 4 stops them after one, so that the output launch computes the
+  // rest of the segment through its fallback)
+  int early_limit;
 };
 
 // rec_max >= 0 (explicit): sequential iff the longest sequence has at most

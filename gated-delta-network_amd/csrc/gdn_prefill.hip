@@ -1036,8 +1036,10 @@ __device__ __forceinline__ void intra_body(
     // after this one counts up from them): 256 per workgroup (the grid has
     // more than enough); only the WY form runs one sequence
     if constexpr (FORM == 0) {
-      const int i = id * 256 + static_cast<int>(threadIdx.x);
-      if (si.early != nullptr && i < si.n_early) si.early[i] = 0;
+      if (si.early != nullptr && id < (si.n_early + 255) / 256) {
+        const int i = id * 256 + static_cast<int>(threadIdx.x);
+        if (i < si.n_early) si.early[i] = 0;
+      }
     }
     if (!unit) return;
     if (FORM < 0) form = *form_flag;
@@ -1705,6 +1707,7 @@ struct SplitScan {
   // early output of the first segment (8 v-heads; nullptr: none): [H.v][8]
   // progress words of the first segment's units, then [nt0][H.v] done flags
   int *early;
+  int early_limit;  // chunks per early workgroup before it stops; 0 no limit
 };
 
 // One unit of the state kernel: sequence s, v-head h, V-block vb (unit =
@@ -2307,7 +2310,8 @@ __device__ __forceinline__ void early_output(char *smem, int e, int ne, const ui
   const int lane = threadIdx.x & 63;
   int seen = 0;  // the head's least published count so far, and when it last grew
   long long t_seen = wall_clock64();
-  for (int c = e / H.v; c < n1 - kEarlyTail; c += step) {
+  for (int c = e / H.v, n = 0; c < n1 - kEarlyTail; c += step, ++n) {
+    if (n == sp.early_limit && n > 0) return;
     if (threadIdx.x < 64) {
       int go = 1;
       for (;;) {
@@ -2524,7 +2528,7 @@ static int prefill_launch(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *
                        status);
     if ((rc = check_launch(what))) return rc;
   }
-  SplitScan sp{P.split_nt0, nullptr, nullptr, nullptr, nullptr, nullptr};
+  SplitScan sp{P.split_nt0, nullptr, nullptr, nullptr, nullptr, nullptr, P.early_limit};
   if (sp.nt0 > 0) {
     sp.htm = reinterpret_cast<uint16_t *>(ws + L.htm);
     sp.send = reinterpret_cast<float *>(ws + L.send);

@@ -182,7 +182,10 @@ def kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output, new_
     ``variant`` picks the form of the per-chunk operands
     (gdn_prefill_fwd_variant): 0 WY, 1 T, -1 the built-in choice; 2 WY with
     one serial chain per sequence, 3 WY with the two-segment scan of a single
-    sequence (0 and -1 take it from 9 chunks on).  ``workspace``: a caller-owned uint8
+    sequence (0 and -1 take it from 9 chunks on), 4 as 3 with the state
+    launch's early output of the first half stopped after one chunk per
+    workgroup (the output launch then computes the rest: a test of that
+    path).  ``workspace``: a caller-owned uint8
     buffer (``alloc_workspace``) used instead of the per-stream cache.
     ``recurrent_max_len``: a batch whose longest sequence has at most this
     many tokens runs through the sequential kernel instead of the chunks (-1

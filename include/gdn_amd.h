@@ -222,7 +222,12 @@ int gdn_prefill_fwd(const gdn_bf16 *q, const gdn_bf16 *k, const gdn_bf16 *v,
  * scan for a single sequence of at least two chunks (the second half of the
  * chunks runs beside the first from a zero state and from the identity, and
  * one more launch applies the first half's final state: half the serial
- * chain; 0 and -1 take it from 9 chunks on when 24 x num_v_heads <= 256).
+ * chain; 0 and -1 take it from 9 chunks on when 24 x num_v_heads <= 256;
+ * with 8 v-heads and at least 30 first-half chunks the state launch also
+ * computes the first half's output as its chain goes, on the CUs the scan
+ * leaves idle), 4 = as 3 with that early output stopped after one chunk per
+ * workgroup (a test of the path that computes the rest afterwards; same
+ * results as 3).
  * The counterpart of
  * the reference's autotuned launch parameters of
  * chunk_gated_delta_rule_fwd_kernel_h (solutions/

@@ -181,7 +181,7 @@ def test_decode_multi_zero_batch_is_a_no_op():
 TUNED_BAD = [
     ((-1, -3, -1), "recurrent_max_len"),
     ((-1, -1, 11), "recurrent tiling"),
-    ((4, -1, -1), "variant"),
+    ((5, -1, -1), "variant"),
     ((-2, -1, -1), "variant"),
 ]
 

@@ -161,7 +161,8 @@ def test_layout_matches_the_library(driver):
 def test_plan_sweep(driver):
     sizes = [1, 2, 16, 63, 64, 65, 96, 97, 1000, 2047, 2048, 8192, 32768, 1 << 20, INT_MAX]
     counts = [1, 2, 3, 6, 64, 1000, 1 << 16, INT_MAX]
-    tunings = [(-1, -1, -1), (0, -1, -1), (1, -1, -1), (2, -1, -1), (3, -1, -1), (-1, -2, -1),
+    tunings = [(-1, -1, -1), (0, -1, -1), (1, -1, -1), (2, -1, -1), (3, -1, -1), (4, -1, -1),
+               (-1, -2, -1),
                (-1, 100, -1), (-1, 0, 10), (-1, -1, 10), (-1, -1, 3)]
     cases = [(T, N, 4, 8) + t for T in sizes for N in counts if N <= T for t in tunings]
     cases += [(T, N, 16, 32, -1, -1, -1) for T in sizes for N in counts if N <= T]
@@ -187,6 +188,8 @@ def test_plan_sweep(driver):
     assert p["nt0"] == 8 and p["early"] == 0  # too few first-segment chunks for early output
     assert p["out"] == 8 * 4 // 8 * 8 * 2 + 32 * 8  # chunk-head pairs + new_state tiles
     assert plans[(8192, 1, 16, 32, -1, -1, -1)]["early"] == 0  # no two-segment scan at 32 v-heads
+    assert plans[(8192, 1, 4, 8, 4, -1, -1)] == plans[(8192, 1, 4, 8, 3, -1, -1)]  # 4: as 3
+    assert plans[(1000, 1, 4, 8, 4, -1, -1)]["nt0"] == 8  # forced, as 3
     p = plans[(8192, 1, 4, 8, 2, -1, -1)]
     assert p["nt0"] == 0 and p["state"] == 64
     p = plans[(32768, 2, 4, 8) + base]

@@ -52,6 +52,9 @@ ROUTES = {
     "chunks": dict(recurrent_max_len=-2),
     "chunks_one_chain": dict(recurrent_max_len=-2, variant=2),
     "chunks_two_segments": dict(recurrent_max_len=-2, variant=3),
+    # the early output of the first segment cut short: the output launch
+    # computes the rest through its fallback
+    "chunks_two_segments_early_cut": dict(recurrent_max_len=-2, variant=4),
     "chunks_t_form": dict(recurrent_max_len=-2, variant=1),
     "token": dict(recurrent_max_len=1 << 30, recurrent_variant=0),
     "block": dict(recurrent_max_len=1 << 30, recurrent_variant=10),

@@ -653,8 +653,10 @@ def test_prefill_two_segment_heads(cuda_device, heads):
 EARLY_TAIL = 15  # kEarlyTail (gdn_common.h); built in from 2 * EARLY_TAIL first-segment chunks
 
 
-@pytest.mark.parametrize("T, cu", [(8192, [0, 8192]), (8192, [0, 3000]), (4000, [130, 3980])])
-def test_prefill_early_output_words(cuda_device, T, cu):
+@pytest.mark.parametrize("T, cu, variant", [
+    (8192, [0, 8192], SPLIT), (8192, [0, 3000], SPLIT), (4000, [130, 3980], SPLIT),
+    (8192, [0, 8192], 4), (8192, [0, 3000], 4)])
+def test_prefill_early_output_words(cuda_device, T, cu, variant):
     # Two-segment scan with early output (8 v-heads): while the first
     # segment's chain runs, workgroups added to the state launch compute its
     # output for the chunks below n1 - 15 (n1: the segment's chunks of this
@@ -664,14 +666,16 @@ def test_prefill_early_output_words(cuda_device, T, cu):
     # its XCD tag (XCD + 1 in the top byte, one XCD per head: MI355X deals
     # workgroups round-robin over its 8 XCDs), and the done flags are set
     # exactly below n1 - 15: no early workgroup stopped.  The output matches
-    # the oracle.
+    # the oracle.  Variant 4 stops each early workgroup after its first chunk
+    # (chunk e // 8 of workgroup e): only chunks 0..7 are done early, and the
+    # output launch computes the rest of the segment through its fallback.
     from gdn_amd import prefill
-    print(f"prefill early output words T={T} cu={cu}", flush=True)
+    print(f"prefill early output words T={T} cu={cu} variant={variant}", flush=True)
     inp = O.make_prefill_inputs([T], seed=45, with_state=True)
     inp["cu_seqlens"] = np.asarray(cu, dtype=np.int64)
     o_ref, s_ref = O.prefill_seq_c(**inp)
     lay = _layout(T, 1)
-    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, variant=SPLIT, route="chunked")
+    o, s = run_gpu(to_dev(inp, cuda_device), cuda_device, variant=variant, route="chunked")
     check(o, s, o_ref, s_ref)
     ws = prefill._workspace(cuda_device, _stream(cuda_device), 0).cpu().numpy()
     nt0 = (lay["nt"] + 1) // 2
@@ -683,6 +687,8 @@ def test_prefill_early_output_words(cuda_device, T, cu):
     assert ((tag >= 1) & (tag <= 8)).all() and (tag == tag[:, :1]).all(), tag
     assert len(np.unique(tag[:, 0])) == 8, tag
     expect = (np.arange(nt0) < n1 - EARLY_TAIL)[:, None]
+    if variant == 4:
+        expect &= (np.arange(nt0) < 8)[:, None]
     assert np.array_equal(done, np.broadcast_to(expect, done.shape).astype(np.int32)), done[:, 0]
 
 
