@@ -2124,16 +2124,23 @@ __device__ __forceinline__ void split_state_tile(char *smem, int f, const Heads 
 //   P  = mask_{j<=i} exp(G_i - G_j) Q K^T      (waves split the rows)
 //   O  = exp(G_i) Q S_c + P v_new              (waves split the columns)
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void output_chunk(
+// ready(): (early output) called by every thread once the inputs' part is
+// done and before ht / v_new are read; false: stop without output.  Returns
+// false only then.
+struct AlwaysReady {
+  __device__ bool operator()() const { return true; }
+};
+template <typename Ready = AlwaysReady>
+__device__ __forceinline__ bool output_chunk(
     char *osmem, int c, int h, const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
     const int4 *__restrict__ chunks, const OneSeq &one, const Heads &H,
     const float *__restrict__ ws_G, const uint16_t *__restrict__ ws_ht, const uint16_t *__restrict__ ws_vnt, float scale,
-    uint16_t *__restrict__ out) {
+    uint16_t *__restrict__ out, Ready ready = Ready{}) {
   uint16_t *const sQ = reinterpret_cast<uint16_t *>(osmem);  // [64][kStrideK]
   uint16_t *const sP = sQ + kChunk * kStrideK;                // [64][kStrideT]
   float *const sG = reinterpret_cast<float *>(sP + kChunk * kStrideT);
   const int4 ch = chunk_info(chunks, c, one);
-  if (ch.x < 0) return;
+  if (ch.x < 0) return true;
   const int start = ch.y, len = ch.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2196,6 +2203,7 @@ __device__ __forceinline__ void output_chunk(
       }
     }
   }
+  if (!ready()) return false;
   // The chunk-start state and v_new fragments of this wave's columns, loaded
   // before the barrier (the K fragments are dead): their latency overlaps it.
   u32x4 hbf[2][4], vbf[2][2];
@@ -2256,6 +2264,7 @@ __device__ __forceinline__ void output_chunk(
       *reinterpret_cast<u32x4 *>(out + ((static_cast<size_t>(start) + row) * H.v + h) * kDV + c8) =
           *reinterpret_cast<const u32x4 *>(&sO[row * kStrideK + c8]);
   }
+  return true;
 }
 
 // One workgroup of an output launch: a new_state tile of a two-segment scan
@@ -2292,27 +2301,17 @@ __device__ __forceinline__ void output_unit(
 // the 100 MHz wall clock without progress.  The output launch computes every
 // chunk not marked done.
 constexpr long long kEarlyPatience = 5000;  // 50 us
-__device__ __forceinline__ void early_output(char *smem, int e, int ne, const uint16_t *q,
-                                             const uint16_t *k, const OneSeq &one, const Heads &H,
-                                             const float *ws_G, const uint16_t *ws_ht,
-                                             const uint16_t *ws_vnt, float scale, uint16_t *out,
-                                             const SplitScan &sp) {
-  constexpr int NVB = kDV / 16;
-  constexpr int kCount = (1 << 24) - 1;
-  const int h = e % H.v, step = ne / H.v, me = early_tag();
-  int bos, eos;
-  one_seq_bounds(one, bos, eos);
-  const int nch = (eos - bos + kChunk - 1) / kChunk;
-  const int n1 = nch < sp.nt0 ? nch : sp.nt0;
-  const int *const prog = sp.early + h * NVB;
-  int *const done = sp.early + H.v * NVB;
-  int *const s_go = reinterpret_cast<int *>(smem + kOutputLds);
-  const int lane = threadIdx.x & 63;
-  int seen = 0;  // the head's least published count so far, and when it last grew
-  long long t_seen = wall_clock64();
-  for (int c = e / H.v, n = 0; c < n1 - kEarlyTail; c += step, ++n) {
-    if (n == sp.early_limit && n > 0) return;
+struct EarlyWait {  // the early output's wait for chunk c (see early_output)
+  const int *prog;
+  int *s_go;
+  int c, me;
+  int *seen;
+  long long *t_seen;
+  __device__ bool operator()() const {
+    constexpr int NVB = kDV / 16;
+    constexpr int kCount = (1 << 24) - 1;
     if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
       int go = 1;
       for (;;) {
         const int w = lane < NVB ? __hip_atomic_load(prog + lane, __ATOMIC_RELAXED,
@@ -2329,10 +2328,10 @@ __device__ __forceinline__ void early_output(char *smem, int e, int ne, const ui
         m = __shfl(m, 0);
         if (m > c) break;
         const long long t = wall_clock64();
-        if (m > seen) {
-          seen = m;
-          t_seen = t;
-        } else if (t - t_seen > kEarlyPatience) {
+        if (m > *seen) {
+          *seen = m;
+          *t_seen = t;
+        } else if (t - *t_seen > kEarlyPatience) {
           go = 0;
           break;
         }
@@ -2341,8 +2340,31 @@ __device__ __forceinline__ void early_output(char *smem, int e, int ne, const ui
       if (threadIdx.x == 0) *s_go = go;
     }
     __syncthreads();
-    if (*s_go == 0) return;
-    output_chunk(smem, c, h, q, k, nullptr, one, H, ws_G, ws_ht, ws_vnt, scale, out);
+    return *s_go != 0;
+  }
+};
+__device__ __forceinline__ void early_output(char *smem, int e, int ne, const uint16_t *q,
+                                             const uint16_t *k, const OneSeq &one, const Heads &H,
+                                             const float *ws_G, const uint16_t *ws_ht,
+                                             const uint16_t *ws_vnt, float scale, uint16_t *out,
+                                             const SplitScan &sp) {
+  constexpr int NVB = kDV / 16;
+  const int h = e % H.v, step = ne / H.v;
+  int bos, eos;
+  one_seq_bounds(one, bos, eos);
+  const int nch = (eos - bos + kChunk - 1) / kChunk;
+  const int n1 = nch < sp.nt0 ? nch : sp.nt0;
+  int *const done = sp.early + H.v * NVB;
+  int seen = 0;  // the head's least published count so far, and when it last grew
+  long long t_seen = wall_clock64();
+  for (int c = e / H.v, n = 0; c < n1 - kEarlyTail; c += step, ++n) {
+    if (n == sp.early_limit && n > 0) return;
+    // the chunk's q, k and gates are read, and P formed, before the wait:
+    // only ht and v_new need the chain
+    const EarlyWait ready{sp.early + h * NVB, reinterpret_cast<int *>(smem + kOutputLds), c,
+                          early_tag(), &seen, &t_seen};
+    if (!output_chunk(smem, c, h, q, k, nullptr, one, H, ws_G, ws_ht, ws_vnt, scale, out, ready))
+      return;
     __syncthreads();  // the chunk's LDS reads are done before the next one's writes
     if (threadIdx.x == 0) done[c * H.v + h] = 1;
   }
