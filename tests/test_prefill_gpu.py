@@ -692,6 +692,21 @@ def test_prefill_early_output_words(cuda_device, T, cu, variant):
     assert np.array_equal(done, np.broadcast_to(expect, done.shape).astype(np.int32)), done[:, 0]
 
 
+@pytest.mark.parametrize("T, cu", [(8192, [0, 8192]), (6000, [37, 5980])])
+def test_prefill_early_output_same_bits(cuda_device, T, cu):
+    # A chunk of the first segment gets the same output whether the state
+    # launch's early workgroups compute it (variant 3) or the output launch
+    # does after they stopped (variant 4: one chunk per workgroup early): the
+    # same function on the same operands.
+    print(f"prefill early output, same bits either way: T={T} cu={cu}", flush=True)
+    inp = O.make_prefill_inputs([T], seed=46, with_state=True)
+    inp["cu_seqlens"] = np.asarray(cu, dtype=np.int64)
+    d = to_dev(inp, cuda_device)
+    o3, s3 = run_gpu(d, cuda_device, variant=SPLIT, route="chunked")
+    o4, s4 = run_gpu(d, cuda_device, variant=4, route="chunked")
+    assert np.array_equal(o3, o4) and np.array_equal(s3, s4)
+
+
 def test_prefill_two_segment_stage_intermediates(cuda_device):
     # The workspace after a two-segment call: the first segment's chunk-start
     # states (ht) and v_new (vnt) are those of one chain; send is the state
