@@ -721,6 +721,7 @@ __device__ __forceinline__ void wy_intra(
   // 8 g .. of feature 16 mt + r16; wave w writes fragments 4 w .. 4 w + 3.
   if (kW && h % H.ratio == 0) {
     uint16_t *ktf = ws_kt + (static_cast<size_t>(c) * H.qk + hq) * (kDK * kChunk);
+    const auto rkt = buf_rsrc(ktf, kDK * kChunk * 2);
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
       const int fi = 4 * wave + f, mt = fi >> 1, kk = fi & 1;
@@ -731,7 +732,7 @@ __device__ __forceinline__ void wy_intra(
         x[2 * hh] = y[0];
         x[2 * hh + 1] = y[1];
       }
-      *reinterpret_cast<u32x4 *>(ktf + (fi * 64 + lane) * 8) = x;
+      buf_store16_sc1(rkt, static_cast<uint32_t>(fi * 64 + lane) * 16u, x);
     }
   }
   __syncthreads();
@@ -789,6 +790,7 @@ __device__ __forceinline__ void wy_intra(
     // fill it, then wave w converts fragments (w, 2p) and (w, 2p + 1) and
     // stores their low parts as one 16-byte row.
     uint16_t *wf = ws_w + ch_head * (kChunk * kDK * 2);
+    const auto rwf = buf_rsrc(wf, kChunk * kDK * 4);
     float lo_inv;
     const float lo_sc = fp8_lo_scale(fmaxf(fmaxf(sWmax[0], sWmax[1]), fmaxf(sWmax[2], sWmax[3])),
                                      &lo_inv);
@@ -820,10 +822,10 @@ __device__ __forceinline__ void wy_intra(
         for (int e = 0; e < 8; ++e) lo[e] = (x8[e] - hf[e]) * lo_sc;
         lo8[2 * kk2] = pk4_fp8(lo[0], lo[1], lo[2], lo[3]);
         lo8[2 * kk2 + 1] = pk4_fp8(lo[4], lo[5], lo[6], lo[7]);
-        *reinterpret_cast<u32x4 *>(wf + ((wave * 4 + 2 * pass + kk2) * 64 + lane) * 8) = hi;
+        buf_store16_sc1(rwf, static_cast<uint32_t>((wave * 4 + 2 * pass + kk2) * 64 + lane) * 16u, hi);
       }
-      *reinterpret_cast<u32x4 *>(reinterpret_cast<char *>(wf) + kWLoOff + wave * 2048 +
-                                 pass * 1024 + lane * 16) = lo8;
+      buf_store16_sc1(rwf, kWLoOff + static_cast<uint32_t>(wave * 2048 + pass * 1024 + lane * 16),
+                      lo8);
       __syncthreads();
     }
     if (kU) {
@@ -839,12 +841,13 @@ __device__ __forceinline__ void wy_intra(
     f32x4 Y[4][2];
     solve(sBeta, Y);
     // u tiles in MFMA result order: [chunk][head][row tile][col tile][lane][4]
-    float *ut = ws_u + ch_head * (kChunk * kDV);
+    const auto rut = buf_rsrc(ws_u + ch_head * (kChunk * kDV), kChunk * kDV * 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
-        *reinterpret_cast<f32x4 *>(ut + ((i * 8 + 2 * wave + nt) * 64 + lane) * 4) = Y[i][nt];
+        buf_store16_sc1(rut, static_cast<uint32_t>((i * 8 + 2 * wave + nt) * 64 + lane) * 16u,
+                        __builtin_bit_cast(u32x4, Y[i][nt]));
   }
 }
 
@@ -945,6 +948,8 @@ __device__ __forceinline__ void t_intra(
 
   // T as A-operand fragments of the state kernel (row 16*rt + r16, 8
   // consecutive k), split hi/lo: [chunk][head][rt][kk][lane][hi 8 | lo 8].
+  // (Plain stores: written through, as the WY form's outputs are, T made
+  // the state kernel's T-form steps slower: 4x8192 252.7 -> 273.9 us.)
   uint16_t *tf = ws_w + ch_head * (kChunk * kDK * 2);  // T in the w region
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
