@@ -236,12 +236,15 @@ def test_prefill_release_workspaces(cuda_device):
     assert_state_close(outs[0][1].cpu().numpy(), s_ref)
 
 
-def test_prefill_graph_replays_two_segment_scan(cuda_device):
+@pytest.mark.parametrize("T", [2500, 4500])
+def test_prefill_graph_replays_two_segment_scan(cuda_device, T):
     # One sequence of 2500 tokens (40 chunks: the two-segment scan, its
-    # second-segment output kernel and the new_state tiles), captured once and
+    # second-segment output kernel and the new_state tiles), or of 4500 (71
+    # chunks: the state launch also computes the first 21 chunks' output,
+    # with progress words the intra launch zeroes), captured once and
     # replayed with new inputs; every replay equals the eager call.
     dev = cuda_device
-    T, N = 2500, 1
+    N = 1
     print(f"prefill graph two-segment T={T}", flush=True)
     st = _prefill_static(T, N, dev)
     inp = O.make_prefill_inputs([T], seed=50)
