@@ -2297,7 +2297,7 @@ __device__ __forceinline__ void output_unit(
 // segment units have published it, and marks the chunk done for the output
 // launch.  Workgroups are dealt round-robin over the 8 XCDs, so the head's
 // state units (blockIdx.x = h + 8 (vb + 8 s)) and its early workgroups
-// (blockIdx.x = 192 + e, e = h mod 8) share an XCD and its L2.  A progress
+// (blockIdx.x = 192 + e with e % 8 = h) share an XCD and its L2.  A progress
 // word holds the publishing unit's XCD (early_tag) above its chunk count, and
 // is read past L1 (an agent-scope load): a word of the reader's XCD comes
 // from the shared L2, where the unit's ht and v_new stores already are; a
