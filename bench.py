@@ -484,6 +484,10 @@ def main():
     ap.add_argument("--only", choices=sorted(ONLY_WORKLOADS),
                     help="profiling mode: time only this workload (eager and graph) and "
                          "print one line; for rocprofv3 summaries of single workloads")
+    ap.add_argument("--rotated", action="store_true",
+                    help="with --only and a prefill workload: time the calls over rotating "
+                         "sets of inputs, outputs and workspace (cache-cold, as "
+                         "prefill_ms_*_rotated) instead of one set")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 64 MiB device copy 10 times (the known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling)")
@@ -514,6 +518,12 @@ def main():
         kind, arg = ONLY_WORKLOADS[args.only]
         if kind == "decode":
             te, tg = bench_decode(arg[0], args.steps, args.warmup, dev, tokens=arg[1])
+        elif args.rotated:
+            tg, sets, per_set = bench_prefill_rotated(arg, dev)
+            log(f"{args.only}: graph {tg.ms * 1e3:.2f} us per call over {sets} rotating sets of "
+                f"{per_set / 2**20:.1f} MiB (median of {tg.n}; min {tg.lo * 1e3:.2f}, "
+                f"max {tg.hi * 1e3:.2f})")
+            return
         else:
             te, tg = bench_prefill(arg, args.steps, args.warmup, dev)
         log(f"{args.only}: eager {te.ms * 1e3:.2f} us, graph {tg.ms * 1e3:.2f} us per call "
